@@ -1,0 +1,280 @@
+/*
+ * orca_hip.h -- C ABI of the MI355X (gfx950) backend for Orca.
+ *
+ * The reference plugs compute backends in through the Rust `Backend` trait
+ * (orca-tensor/src/backend.rs:19-315) whose storages are opaque, cheaply
+ * cloned handles that every op borrows and every op returns anew.  This
+ * header is the FFI a Rust `HipBackend: Backend` binds: each `orca_hip_<op>`
+ * below stands in for the trait method named in its comment, takes the same
+ * logical shape / dtype arguments, and returns a NEW device buffer through
+ * `out` (allocated from the context's stream-ordered caching allocator; the
+ * caller releases it with orca_hip_free, which is what the Rust storage's
+ * Drop does).  Inputs are never modified.
+ *
+ * Error behaviour mirrors orca_core::OrcaError (orca-core/src/error.rs:5-31):
+ * every function returns 0 or a negative ORCA_HIP_ERR_* code naming the
+ * variant, and orca_hip_last_error() returns the message (thread-local).
+ * No function throws across the ABI.
+ *
+ * All work is enqueued on the context's single in-order HIP stream; only the
+ * host-reading calls (to_f32_vec, d2h, has_nan_or_inf, *_read_*) synchronise.
+ * Element type on the path is f32 (DType::F32 = 0); other dtypes return
+ * ORCA_HIP_ERR_UNSUPPORTED_DTYPE, like the reference's dispatch macros.
+ */
+#ifndef ORCA_HIP_H
+#define ORCA_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes (orca-core/src/error.rs:5-31) ---- */
+#define ORCA_HIP_OK 0
+#define ORCA_HIP_ERR_SHAPE (-1)              /* OrcaError::ShapeMismatch */
+#define ORCA_HIP_ERR_UNSUPPORTED_DTYPE (-2)  /* OrcaError::UnsupportedDType */
+#define ORCA_HIP_ERR_DTYPE_MISMATCH (-3)     /* OrcaError::DTypeMismatch */
+#define ORCA_HIP_ERR_DEVICE_MISMATCH (-4)    /* OrcaError::DeviceMismatch */
+#define ORCA_HIP_ERR_INTERNAL (-5)           /* OrcaError::InternalError */
+
+/* ---- dtype codes, in orca_core::DType order (orca-core/src/dtype.rs:5-22) ---- */
+#define ORCA_HIP_F32 0
+#define ORCA_HIP_F64 1
+#define ORCA_HIP_F16 2
+#define ORCA_HIP_BF16 3
+#define ORCA_HIP_I32 4
+#define ORCA_HIP_I64 5
+#define ORCA_HIP_U8 6
+#define ORCA_HIP_BOOL 7
+
+/* Layout of a matmul operand's storage.  TRANSPOSED means the buffer holds
+ * the operand with its last two dims swapped: a lazy `transpose` view as
+ * produced for MatMulBackward (orca-autograd/src/backend.rs:1467-1495). */
+#define ORCA_HIP_VIEW_CONTIGUOUS 0
+#define ORCA_HIP_VIEW_TRANSPOSED 1
+
+typedef struct orca_hip_ctx orca_hip_ctx;
+typedef struct orca_hip_mlp orca_hip_mlp;
+
+/* ======================= context, memory, host I/O ======================= */
+
+/* Creates a context on HIP device `device` with its own stream and caching
+ * allocator.  Replaces GpuBackend::new (orca-backend-gpu/src/backend.rs:53-211)
+ * as the process-global backend behind global_backend_gpu()
+ * (orca-python/src/lib.rs:23-33). */
+int orca_hip_ctx_create(int device, orca_hip_ctx** out);
+int orca_hip_ctx_destroy(orca_hip_ctx* ctx);
+/* Message of the calling thread's last failure ("" if none). */
+const char* orca_hip_last_error(void);
+/* Backend::device (orca-tensor/src/backend.rs:25): the HIP ordinal, reported
+ * as Device::Gpu(ordinal) so orca-python routes "gpu"/"cuda" here
+ * (orca-python/src/lib.rs:91-93). */
+int orca_hip_device(const orca_hip_ctx* ctx, int* ordinal);
+
+/* Stream-ordered caching allocator (replaces MemoryPool,
+ * orca-backend-gpu/src/pool.rs:8-71).  Blocks are 256-byte aligned; a freed
+ * block is reused by later work on the same stream without a hipMalloc. */
+int orca_hip_alloc(orca_hip_ctx* ctx, size_t bytes, void** out);
+int orca_hip_free(orca_hip_ctx* ctx, void* ptr);
+/* Returns cached blocks to the device (synchronises first). */
+int orca_hip_empty_cache(orca_hip_ctx* ctx);
+/* live bytes, cached bytes, and the number of hipMalloc calls so far. */
+int orca_hip_mem_stats(orca_hip_ctx* ctx, size_t* live, size_t* cached, size_t* device_allocs);
+
+int orca_hip_h2d(orca_hip_ctx* ctx, void* dst, const void* src, size_t bytes); /* synchronous */
+int orca_hip_d2h(orca_hip_ctx* ctx, void* dst, const void* src, size_t bytes); /* synchronous */
+int orca_hip_d2d(orca_hip_ctx* ctx, void* dst, const void* src, size_t bytes); /* stream-ordered */
+int orca_hip_fill(orca_hip_ctx* ctx, float* dst, float value, size_t n);       /* stream-ordered kernel */
+int orca_hip_sync(orca_hip_ctx* ctx);
+
+/* =========================== Backend trait ops =========================== */
+/* `shape`/`rank` are the logical shape (Shape, orca-core/src/shape.rs:6).
+ * `out` receives a new buffer of the result's element count. */
+
+/* Backend::zeros (backend.rs:27) */
+int orca_hip_zeros(orca_hip_ctx* ctx, const size_t* shape, size_t rank, int dtype, void** out);
+/* Backend::from_f32_slice (backend.rs:30-31); n must equal the shape's elements */
+int orca_hip_from_f32_slice(orca_hip_ctx* ctx, const size_t* shape, size_t rank, const float* data,
+                            size_t n, void** out);
+/* Backend::to_f32_vec (backend.rs:34): copies n floats to host (synchronises) */
+int orca_hip_to_f32_vec(orca_hip_ctx* ctx, const void* storage, size_t n, float* host_out);
+/* Backend::from_bytes / to_bytes (backend.rs:296-297), f32 payload */
+int orca_hip_from_bytes(orca_hip_ctx* ctx, const size_t* shape, size_t rank, const uint8_t* bytes,
+                        size_t n_bytes, int dtype, void** out);
+int orca_hip_to_bytes(orca_hip_ctx* ctx, const void* storage, size_t n_bytes, uint8_t* host_out);
+
+/* Backend::matmul (backend.rs:38-45): batched (..., M, K) x (..., K, N) with
+ * equal leading dims; lhs_view/rhs_view say whether a buffer holds its
+ * operand transposed (ORCA_HIP_VIEW_*). */
+int orca_hip_matmul(orca_hip_ctx* ctx, const void* lhs, const void* rhs, const size_t* lhs_shape,
+                    size_t lhs_rank, const size_t* rhs_shape, size_t rhs_rank, int dtype, int lhs_view,
+                    int rhs_view, void** out);
+/* Backend::transpose (backend.rs:48-55), materialised */
+int orca_hip_transpose(orca_hip_ctx* ctx, const void* s, const size_t* shape, size_t rank, size_t dim0,
+                       size_t dim1, int dtype, void** out);
+
+/* Backend::add / sub / mul / div (backend.rs:57-70, 80-86, 153-159) */
+int orca_hip_add(orca_hip_ctx* ctx, const void* lhs, const void* rhs, const size_t* shape, size_t rank,
+                 int dtype, void** out);
+int orca_hip_sub(orca_hip_ctx* ctx, const void* lhs, const void* rhs, const size_t* shape, size_t rank,
+                 int dtype, void** out);
+int orca_hip_mul(orca_hip_ctx* ctx, const void* lhs, const void* rhs, const size_t* shape, size_t rank,
+                 int dtype, void** out);
+int orca_hip_div(orca_hip_ctx* ctx, const void* lhs, const void* rhs, const size_t* shape, size_t rank,
+                 int dtype, void** out);
+/* Backend::mul_scalar (backend.rs:71-77) */
+int orca_hip_mul_scalar(orca_hip_ctx* ctx, const void* s, float scalar, const size_t* shape, size_t rank,
+                        int dtype, void** out);
+/* Backend::relu / sigmoid / exp / log / sqrt (backend.rs:87-93, 135-136, 160) */
+int orca_hip_relu(orca_hip_ctx* ctx, const void* s, const size_t* shape, size_t rank, int dtype, void** out);
+int orca_hip_sigmoid(orca_hip_ctx* ctx, const void* s, const size_t* shape, size_t rank, int dtype,
+                     void** out);
+int orca_hip_exp(orca_hip_ctx* ctx, const void* s, const size_t* shape, size_t rank, int dtype, void** out);
+int orca_hip_log(orca_hip_ctx* ctx, const void* s, const size_t* shape, size_t rank, int dtype, void** out);
+int orca_hip_sqrt(orca_hip_ctx* ctx, const void* s, const size_t* shape, size_t rank, int dtype, void** out);
+/* Backend::relu_backward (backend.rs:96-102): grad * [in_primal > 0] */
+int orca_hip_relu_backward(orca_hip_ctx* ctx, const void* grad_out, const void* in_primal,
+                           const size_t* shape, size_t rank, int dtype, void** out);
+/* Backend::sigmoid_backward (backend.rs:103-109) */
+int orca_hip_sigmoid_backward(orca_hip_ctx* ctx, const void* grad_out, const void* out_primal,
+                              const size_t* shape, size_t rank, int dtype, void** out);
+/* Backend::exp_backward / log_backward (backend.rs:137-150) */
+int orca_hip_exp_backward(orca_hip_ctx* ctx, const void* grad_out, const void* out_primal,
+                          const size_t* shape, size_t rank, int dtype, void** out);
+int orca_hip_log_backward(orca_hip_ctx* ctx, const void* grad_out, const void* in_primal,
+                          const size_t* shape, size_t rank, int dtype, void** out);
+/* Backend::sqrt_backward / div_backward_lhs / div_backward_rhs (backend.rs:161-183) */
+int orca_hip_sqrt_backward(orca_hip_ctx* ctx, const void* grad_out, const void* out_primal,
+                           const size_t* shape, size_t rank, int dtype, void** out);
+int orca_hip_div_backward_lhs(orca_hip_ctx* ctx, const void* grad_out, const void* rhs_primal,
+                              const size_t* shape, size_t rank, int dtype, void** out);
+int orca_hip_div_backward_rhs(orca_hip_ctx* ctx, const void* grad_out, const void* lhs_primal,
+                              const void* rhs_primal, const size_t* shape, size_t rank, int dtype,
+                              void** out);
+/* Backend::accumulate_grad (backend.rs:185): lhs + rhs over n elements */
+int orca_hip_accumulate_grad(orca_hip_ctx* ctx, const void* lhs, const void* rhs, size_t n, void** out);
+
+/* Backend::expand / sum_to_shape / reshape (backend.rs:112-133) */
+int orca_hip_expand(orca_hip_ctx* ctx, const void* s, const size_t* in_shape, size_t in_rank,
+                    const size_t* out_shape, size_t out_rank, int dtype, void** out);
+int orca_hip_sum_to_shape(orca_hip_ctx* ctx, const void* s, const size_t* in_shape, size_t in_rank,
+                          const size_t* out_shape, size_t out_rank, int dtype, void** out);
+int orca_hip_reshape(orca_hip_ctx* ctx, const void* s, const size_t* in_shape, size_t in_rank,
+                     const size_t* out_shape, size_t out_rank, int dtype, void** out);
+/* Backend::max_to_shape / max_to_shape_backward (backend.rs:299-314) */
+int orca_hip_max_to_shape(orca_hip_ctx* ctx, const void* s, const size_t* in_shape, size_t in_rank,
+                          const size_t* out_shape, size_t out_rank, int dtype, void** out);
+int orca_hip_max_to_shape_backward(orca_hip_ctx* ctx, const void* grad_out, const void* in_primal,
+                                   const void* out_primal, const size_t* in_shape, size_t in_rank,
+                                   const size_t* out_shape, size_t out_rank, int dtype, void** out);
+/* Backend::has_nan_or_inf (backend.rs:298); synchronises */
+int orca_hip_has_nan_or_inf(orca_hip_ctx* ctx, const void* s, size_t n, int dtype, int* result);
+
+/* ===================== fused kernels beyond the trait ===================== */
+/* Buffer-level entry points: the caller owns every output buffer. */
+
+/* GEMM epilogues. */
+#define ORCA_HIP_EPI_NONE 0      /* C = acc */
+#define ORCA_HIP_EPI_BIAS 1      /* C = acc + bias[n] */
+#define ORCA_HIP_EPI_BIAS_RELU 2 /* C = relu(acc + bias[n])  (x > 0 ? x : 0) */
+#define ORCA_HIP_EPI_RELU_MASK 3 /* C = mask[m][n] > 0 ? acc : 0  (ReLU backward on the product) */
+
+typedef struct {
+  int kind;            /* ORCA_HIP_EPI_* */
+  const float* bias;   /* [N] for EPI_BIAS / EPI_BIAS_RELU */
+  const float* mask;   /* [M][ldmask] for EPI_RELU_MASK: the ReLU output (or pre-activation) */
+  size_t ldmask;
+  float* colsum;       /* optional [N]: column sums of op(B) over K (bias gradient of dW = X^T dY) */
+} orca_hip_epilogue;
+
+/* C[M,N] = op(A)[M,K] . op(B)[K,N] in f32 on the fp32 MFMA units.
+ * trans_a = 0: A is row-major [M][lda]; 1: A is stored [K][lda] (A^T).
+ * trans_b = 0: B is row-major [K][ldb]; 1: B is stored [N][ldb] (B^T).
+ * This is the Linear layer's three products: Y = X W (+b, ReLU) with (0,0),
+ * dX = dY W^T (ReLU mask) with (0,1) and dW = X^T dY (+ bias colsum) with (1,0)
+ * (MatMulBackward, orca-autograd/src/backend.rs:1449-1499). */
+int orca_hip_gemm(orca_hip_ctx* ctx, int trans_a, int trans_b, size_t M, size_t N, size_t K, const float* A,
+                  size_t lda, const float* B, size_t ldb, float* C, size_t ldc, const orca_hip_epilogue* epi);
+
+/* Fused softmax cross-entropy forward + gradient, one wavefront per row
+ * (replaces the ~21-op composition of python/orca/nn/loss.py:59-100 and its
+ * tape backward).  Targets are either one-hot rows `onehot` [B][C] or class
+ * indices `labels` [B] (exactly one non-NULL).  Writes, each optional:
+ * loss[1] = mean over rows, dlogits[B][C] = dL/dlogits, preds[B] = first-max
+ * argmax (python/orca/nn/model.py:65-75), correct[1] = #rows with
+ * preds == target class.  All outputs are device pointers. */
+int orca_hip_softmax_ce(orca_hip_ctx* ctx, const float* logits, size_t B, size_t C, const float* onehot,
+                        const int32_t* labels, float* loss, float* dlogits, int32_t* preds, int64_t* correct);
+
+/* dpre = grad * [pre > 0] and, if colsum != NULL, colsum[n] = sum over rows of
+ * dpre (ReluBackward + the bias ExpandBackward's sum_to_shape,
+ * orca-autograd/src/backend.rs:1633-1645, 1684-1697). */
+int orca_hip_relu_bw_colsum(orca_hip_ctx* ctx, const float* grad, const float* pre, size_t rows, size_t cols,
+                            float* dpre, float* colsum);
+
+/* One AdamW step over flat buffers, same f32 op order as
+ * python/orca/optim/adamw.py:71-94 with the f64 scalars rounded to f32 as
+ * PyO3 does (orca-python/src/lib.rs:12-16).  t is the step count after
+ * increment (adamw.py:64). */
+int orca_hip_adamw_step(orca_hip_ctx* ctx, float* p, const float* g, float* m, float* v, size_t n, double lr,
+                        double beta1, double beta2, double eps, double weight_decay, int64_t t);
+/* One vanilla SGD step p -= f32(lr) * g (python/orca/optim/sgd.py:74-79). */
+int orca_hip_sgd_step(orca_hip_ctx* ctx, float* p, const float* g, size_t n, double lr);
+
+/* ===================== device-resident MLP training step ===================== */
+/* nn.Sequential(Linear, ReLU, ..., Linear) + CrossEntropyLoss + SGD/AdamW
+ * (python/orca/nn/{linear,activation,container,loss}.py, python/orca/optim)
+ * with parameters, gradients and moments in flat device arenas and every
+ * intermediate preallocated: a step is a fixed sequence of kernel launches
+ * with no host synchronisation and no allocation. */
+typedef struct {
+  int kind;            /* 0 = SGD (momentum = weight_decay = 0), 1 = AdamW */
+  double lr;
+  double weight_decay; /* AdamW only */
+  double beta1, beta2, eps;
+} orca_hip_optim;
+
+/* dims[0..n_layers]: features per layer (e.g. 784, H, H, 10). */
+int orca_hip_mlp_create(orca_hip_ctx* ctx, const size_t* dims, size_t n_layers, size_t batch,
+                        const orca_hip_optim* opt, orca_hip_mlp** out);
+int orca_hip_mlp_destroy(orca_hip_mlp* mlp);
+/* Parameter index i: W_{i/2} for even i ([dims[l]][dims[l+1]]), b_{i/2} ([1][dims[l+1]]) for odd i. */
+int orca_hip_mlp_param_numel(const orca_hip_mlp* mlp, size_t index, size_t* n);
+int orca_hip_mlp_set_param(orca_hip_mlp* mlp, size_t index, const float* host, size_t n);
+int orca_hip_mlp_get_param(orca_hip_mlp* mlp, size_t index, float* host, size_t n);
+int orca_hip_mlp_get_grad(orca_hip_mlp* mlp, size_t index, float* host, size_t n);
+/* which = 0: first moment m, 1: second moment v */
+int orca_hip_mlp_get_moment(orca_hip_mlp* mlp, int which, size_t index, float* host, size_t n);
+/* Uploads the batch: x [batch][dims[0]] and either one-hot targets
+ * [batch][dims[L]] or class labels [batch] (one of the two non-NULL). */
+int orca_hip_mlp_set_batch(orca_hip_mlp* mlp, const float* x, const float* onehot, const int32_t* labels);
+/* Device pointers of the resident batch, for callers that fill it on device. */
+int orca_hip_mlp_batch_ptrs(orca_hip_mlp* mlp, float** x, int32_t** labels);
+/* One forward + backward + optimizer step, enqueued; no host sync. */
+int orca_hip_mlp_step(orca_hip_mlp* mlp);
+/* Loss and correct-prediction count of the last step (synchronises). */
+int orca_hip_mlp_read_metrics(orca_hip_mlp* mlp, float* loss, int64_t* correct);
+/* Logits [batch][dims[L]] and predictions [batch] of the last step (synchronises). */
+int orca_hip_mlp_get_logits(orca_hip_mlp* mlp, float* host, size_t n);
+int orca_hip_mlp_get_preds(orca_hip_mlp* mlp, int32_t* host, size_t n);
+/* AdamW step counter t. */
+int orca_hip_mlp_get_step_count(const orca_hip_mlp* mlp, int64_t* t);
+
+/* ===================== kernel timing ===================== */
+/* When enabled, each GEMM / fused-kernel launch is bracketed by HIP events on
+ * the context stream.  The report is a JSON object
+ * {"kernels": [{"name", "launches", "total_ms", "flops", "bytes"}...]} with the
+ * algorithmic flops / bytes of the launches (synchronises). */
+int orca_hip_prof_enable(orca_hip_ctx* ctx, int enable);
+int orca_hip_prof_reset(orca_hip_ctx* ctx);
+int orca_hip_prof_report(orca_hip_ctx* ctx, char* buf, size_t len);
+/* Elapsed device time between two markers on the context stream. */
+int orca_hip_timer_start(orca_hip_ctx* ctx);
+int orca_hip_timer_stop(orca_hip_ctx* ctx, float* ms);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* ORCA_HIP_H */

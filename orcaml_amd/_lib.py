@@ -1,0 +1,186 @@
+"""ctypes binding of liborca_hip.so (the C ABI declared in include/orca_hip.h).
+
+There is no fallback: if the library is missing or fails to load, every entry
+point raises, so nothing can silently run on the CPU.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(PKG_DIR, "liborca_hip.so")
+
+# Status codes (orca-core/src/error.rs:5-31 variants).
+OK = 0
+ERR_SHAPE = -1
+ERR_UNSUPPORTED_DTYPE = -2
+ERR_DTYPE_MISMATCH = -3
+ERR_DEVICE_MISMATCH = -4
+ERR_INTERNAL = -5
+ERROR_NAMES = {
+    ERR_SHAPE: "ShapeMismatch",
+    ERR_UNSUPPORTED_DTYPE: "UnsupportedDType",
+    ERR_DTYPE_MISMATCH: "DTypeMismatch",
+    ERR_DEVICE_MISMATCH: "DeviceMismatch",
+    ERR_INTERNAL: "InternalError",
+}
+
+# DType codes in orca_core::DType order (orca-core/src/dtype.rs:5-22).
+F32, F64, F16, BF16, I32, I64, U8, BOOL = range(8)
+
+VIEW_CONTIGUOUS = 0
+VIEW_TRANSPOSED = 1
+
+EPI_NONE, EPI_BIAS, EPI_BIAS_RELU, EPI_RELU_MASK = range(4)
+
+
+class OrcaHipError(ValueError):
+    """A failed C-ABI call; `.code` is the ORCA_HIP_ERR_* status.  It is a
+    ValueError because orca-python maps every OrcaError to ValueError
+    (orca-python/src/lib.rs:124,128)."""
+
+    def __init__(self, code: int, message: str):
+        super().__init__(f"{ERROR_NAMES.get(code, code)}: {message}")
+        self.code = code
+
+
+class Epilogue(ctypes.Structure):
+    _fields_ = [
+        ("kind", ctypes.c_int),
+        ("bias", ctypes.c_void_p),
+        ("mask", ctypes.c_void_p),
+        ("ldmask", ctypes.c_size_t),
+        ("colsum", ctypes.c_void_p),
+    ]
+
+
+class Optim(ctypes.Structure):
+    _fields_ = [
+        ("kind", ctypes.c_int),
+        ("lr", ctypes.c_double),
+        ("weight_decay", ctypes.c_double),
+        ("beta1", ctypes.c_double),
+        ("beta2", ctypes.c_double),
+        ("eps", ctypes.c_double),
+    ]
+
+
+_P = ctypes.c_void_p
+_PP = ctypes.POINTER(ctypes.c_void_p)
+_SZ = ctypes.c_size_t
+_SZP = ctypes.POINTER(ctypes.c_size_t)
+_I = ctypes.c_int
+_F = ctypes.c_float
+_D = ctypes.c_double
+
+_EW1 = [_P, _P, _SZP, _SZ, _I, _PP]
+_EW2 = [_P, _P, _P, _SZP, _SZ, _I, _PP]
+_RESHAPE = [_P, _P, _SZP, _SZ, _SZP, _SZ, _I, _PP]
+
+SIGNATURES = {
+    "orca_hip_ctx_create": [_I, ctypes.POINTER(_P)],
+    "orca_hip_ctx_destroy": [_P],
+    "orca_hip_device": [_P, ctypes.POINTER(_I)],
+    "orca_hip_alloc": [_P, _SZ, _PP],
+    "orca_hip_free": [_P, _P],
+    "orca_hip_empty_cache": [_P],
+    "orca_hip_mem_stats": [_P, _SZP, _SZP, _SZP],
+    "orca_hip_h2d": [_P, _P, _P, _SZ],
+    "orca_hip_d2h": [_P, _P, _P, _SZ],
+    "orca_hip_d2d": [_P, _P, _P, _SZ],
+    "orca_hip_fill": [_P, _P, _F, _SZ],
+    "orca_hip_sync": [_P],
+    "orca_hip_zeros": [_P, _SZP, _SZ, _I, _PP],
+    "orca_hip_from_f32_slice": [_P, _SZP, _SZ, _P, _SZ, _PP],
+    "orca_hip_to_f32_vec": [_P, _P, _SZ, _P],
+    "orca_hip_from_bytes": [_P, _SZP, _SZ, _P, _SZ, _I, _PP],
+    "orca_hip_to_bytes": [_P, _P, _SZ, _P],
+    "orca_hip_matmul": [_P, _P, _P, _SZP, _SZ, _SZP, _SZ, _I, _I, _I, _PP],
+    "orca_hip_transpose": [_P, _P, _SZP, _SZ, _SZ, _SZ, _I, _PP],
+    "orca_hip_add": _EW2,
+    "orca_hip_sub": _EW2,
+    "orca_hip_mul": _EW2,
+    "orca_hip_div": _EW2,
+    "orca_hip_mul_scalar": [_P, _P, _F, _SZP, _SZ, _I, _PP],
+    "orca_hip_relu": _EW1,
+    "orca_hip_sigmoid": _EW1,
+    "orca_hip_exp": _EW1,
+    "orca_hip_log": _EW1,
+    "orca_hip_sqrt": _EW1,
+    "orca_hip_relu_backward": _EW2,
+    "orca_hip_sigmoid_backward": _EW2,
+    "orca_hip_exp_backward": _EW2,
+    "orca_hip_log_backward": _EW2,
+    "orca_hip_sqrt_backward": _EW2,
+    "orca_hip_div_backward_lhs": _EW2,
+    "orca_hip_div_backward_rhs": [_P, _P, _P, _P, _SZP, _SZ, _I, _PP],
+    "orca_hip_accumulate_grad": [_P, _P, _P, _SZ, _PP],
+    "orca_hip_expand": _RESHAPE,
+    "orca_hip_sum_to_shape": _RESHAPE,
+    "orca_hip_reshape": _RESHAPE,
+    "orca_hip_max_to_shape": _RESHAPE,
+    "orca_hip_max_to_shape_backward": [_P, _P, _P, _P, _SZP, _SZ, _SZP, _SZ, _I, _PP],
+    "orca_hip_has_nan_or_inf": [_P, _P, _SZ, _I, ctypes.POINTER(_I)],
+    "orca_hip_gemm": [_P, _I, _I, _SZ, _SZ, _SZ, _P, _SZ, _P, _SZ, _P, _SZ, ctypes.POINTER(Epilogue)],
+    "orca_hip_softmax_ce": [_P, _P, _SZ, _SZ, _P, _P, _P, _P, _P, _P],
+    "orca_hip_relu_bw_colsum": [_P, _P, _P, _SZ, _SZ, _P, _P],
+    "orca_hip_adamw_step": [_P, _P, _P, _P, _P, _SZ, _D, _D, _D, _D, _D, ctypes.c_int64],
+    "orca_hip_sgd_step": [_P, _P, _P, _SZ, _D],
+    "orca_hip_mlp_create": [_P, _SZP, _SZ, _SZ, ctypes.POINTER(Optim), ctypes.POINTER(_P)],
+    "orca_hip_mlp_destroy": [_P],
+    "orca_hip_mlp_param_numel": [_P, _SZ, _SZP],
+    "orca_hip_mlp_set_param": [_P, _SZ, _P, _SZ],
+    "orca_hip_mlp_get_param": [_P, _SZ, _P, _SZ],
+    "orca_hip_mlp_get_grad": [_P, _SZ, _P, _SZ],
+    "orca_hip_mlp_get_moment": [_P, _I, _SZ, _P, _SZ],
+    "orca_hip_mlp_set_batch": [_P, _P, _P, _P],
+    "orca_hip_mlp_batch_ptrs": [_P, _PP, _PP],
+    "orca_hip_mlp_step": [_P],
+    "orca_hip_mlp_read_metrics": [_P, ctypes.POINTER(_F), ctypes.POINTER(ctypes.c_int64)],
+    "orca_hip_mlp_get_logits": [_P, _P, _SZ],
+    "orca_hip_mlp_get_preds": [_P, _P, _SZ],
+    "orca_hip_mlp_get_step_count": [_P, ctypes.POINTER(ctypes.c_int64)],
+    "orca_hip_prof_enable": [_P, _I],
+    "orca_hip_prof_reset": [_P],
+    "orca_hip_prof_report": [_P, ctypes.c_char_p, _SZ],
+    "orca_hip_timer_start": [_P],
+    "orca_hip_timer_stop": [_P, ctypes.POINTER(_F)],
+}
+
+_lib = None
+
+
+def load() -> ctypes.CDLL:
+    """Loads liborca_hip.so; raises if it is not built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(
+            f"{LIB_PATH} is not built; run `python -m orcaml_amd.build` (the HIP backend has no CPU fallback)")
+    lib = ctypes.CDLL(LIB_PATH)
+    for name, argtypes in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.argtypes = argtypes
+        fn.restype = ctypes.c_int
+    lib.orca_hip_last_error.argtypes = []
+    lib.orca_hip_last_error.restype = ctypes.c_char_p
+    _lib = lib
+    return lib
+
+
+def check(rc: int) -> None:
+    if rc != OK:
+        msg = load().orca_hip_last_error()
+        raise OrcaHipError(rc, msg.decode() if msg else "")
+
+
+def call(name: str, *args) -> None:
+    check(getattr(load(), name)(*args))
+
+
+def dims(shape) -> tuple:
+    shape = tuple(int(s) for s in shape)
+    arr = (ctypes.c_size_t * max(1, len(shape)))(*shape)
+    return arr, len(shape)

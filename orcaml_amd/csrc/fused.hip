@@ -1,0 +1,466 @@
+// Fused kernels beyond the Backend trait:
+//  * softmax cross-entropy forward + gradient + argmax, one wave64 per row,
+//    replacing the ~21-op composition of python/orca/nn/loss.py:59-100 and
+//    the tape's backward through it;
+//  * ReLU-mask backward with the bias-gradient column sum;
+//  * single-pass AdamW / SGD over flat parameter arenas.
+// Built with -ffp-contract=off so the per-element arithmetic is the
+// reference's separate f32 operations.
+#include <cfloat>
+#include <cmath>
+
+#include "runtime.hpp"
+
+namespace orca_hip {
+namespace {
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = v + __shfl_xor(v, o, 64);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {  // strict `>`: NaN never wins
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    float w = __shfl_xor(v, o, 64);
+    if (w > v) v = w;
+  }
+  return v;
+}
+
+// Largest value, ties to the lowest index (idx = INT_MAX marks "no candidate").
+__device__ __forceinline__ void wave_argmax(float& v, int& idx) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    float w = __shfl_xor(v, o, 64);
+    int wi = __shfl_xor(idx, o, 64);
+    if (wi != INT_MAX && (idx == INT_MAX || w > v || (w == v && wi < idx))) {
+      v = w;
+      idx = wi;
+    }
+  }
+}
+
+// Row argmax with the reference's sequential rule (python/orca/nn/model.py:65-75):
+// best starts at r[0]; a later value replaces it only if strictly greater.
+// Lanes propose their first strict maximum over c >= 1 (NaN never proposes);
+// the winner beats r[0] only if strictly greater, and a NaN r[0] is never beaten.
+template <int VPL, class Get>
+__device__ __forceinline__ int row_argmax(Get get, int C) {
+  const int lane = threadIdx.x & 63;
+  float bv = -INFINITY;
+  int bi = INT_MAX;
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    int c = lane + 64 * j;
+    if (c >= 1 && c < C) {
+      float v = get(j);
+      if (v == v && (bi == INT_MAX || v > bv)) {
+        bv = v;
+        bi = c;
+      }
+    }
+  }
+  wave_argmax(bv, bi);
+  const float first = __shfl(get(0), 0, 64);
+  if (bi == INT_MAX) return 0;
+  return (bv > first) ? bi : 0;
+}
+
+// Logits and exp(logits - max) stay in registers (VPL values per lane,
+// column c = lane + 64 j); targets are re-read (one-hot) or derived (labels).
+template <int VPL>
+__global__ void __launch_bounds__(256) softmax_ce_kernel(const float* __restrict__ logits, int B, int C,
+                                                         const float* __restrict__ onehot,
+                                                         const int32_t* __restrict__ labels, float inv_b,
+                                                         float* __restrict__ row_loss, float* __restrict__ dlogits,
+                                                         int32_t* __restrict__ preds, int* __restrict__ row_correct) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6);
+  if (row >= B) return;
+  const float* xr = logits + (int64_t)row * C;
+  const float* tr = onehot ? onehot + (int64_t)row * C : nullptr;
+  const int label = labels ? labels[row] : -1;
+  auto tval = [&](int j) -> float {
+    int c = lane + 64 * j;
+    if (c >= C) return 0.0f;
+    return tr ? tr[c] : (c == label ? 1.0f : 0.0f);
+  };
+  float x[VPL], e[VPL];
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    int c = lane + 64 * j;
+    x[j] = c < C ? xr[c] : 0.0f;
+  }
+
+  // max_to_shape (init -FLT_MAX, strict >)
+  float mx = -FLT_MAX;
+#pragma unroll
+  for (int j = 0; j < VPL; ++j)
+    if (lane + 64 * j < C && x[j] > mx) mx = x[j];
+  mx = wave_max(mx);
+  // exp(p - max) and its row sum
+  float se = 0.0f;
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    e[j] = (lane + 64 * j < C) ? expf(x[j] - mx) : 0.0f;
+    se = se + e[j];
+  }
+  se = wave_sum(se);
+  const float lg = logf(fmaxf(se, 1e-7f));
+  const float lse = mx + lg;
+  // per-row loss: sum_c -(t * (p - lse))
+  float pb = 0.0f;
+#pragma unroll
+  for (int j = 0; j < VPL; ++j)
+    if (lane + 64 * j < C) pb = pb + (tval(j) * (x[j] - lse)) * -1.0f;
+  pb = wave_sum(pb);
+
+  if (dlogits) {
+    // The tape's gradient through the composition, element by element
+    // (seed 1 * (1/B), then -1, * target, the identity expands' 0 + g, ...).
+    const float g_tm = inv_b * -1.0f;
+    float gse = 0.0f;
+#pragma unroll
+    for (int j = 0; j < VPL; ++j)
+      if (lane + 64 * j < C) {
+        float g_lse = 0.0f + ((g_tm * tval(j)) * -1.0f);
+        gse = gse + (0.0f + g_lse) / se;
+      }
+    gse = wave_sum(gse);
+    float gmx = 0.0f;
+#pragma unroll
+    for (int j = 0; j < VPL; ++j)
+      if (lane + 64 * j < C) {
+        float g_lse = 0.0f + ((g_tm * tval(j)) * -1.0f);
+        float g_sh = gse * e[j];
+        gmx = gmx + ((0.0f + g_lse) + (0.0f + (g_sh * -1.0f)));
+      }
+    gmx = wave_sum(gmx);
+    float* dr = dlogits + (int64_t)row * C;
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+      int c = lane + 64 * j;
+      if (c < C) {
+        float g_ls = g_tm * tval(j);
+        float g_sh = gse * e[j];
+        float d = (0.0f + g_ls) + (0.0f + g_sh);
+        float g3 = 0.0f;
+        if (x[j] == mx) g3 = g3 + gmx;
+        dr[c] = d + g3;
+      }
+    }
+  }
+
+  if (lane == 0) row_loss[row] = pb;
+  if (preds || row_correct) {
+    int pred = row_argmax<VPL>([&](int j) { return x[j]; }, C);
+    int tcls = labels ? label : row_argmax<VPL>(tval, C);
+    if (lane == 0) {
+      if (preds) preds[row] = pred;
+      if (row_correct) row_correct[row] = (pred == tcls) ? 1 : 0;
+    }
+  }
+}
+
+// loss = (sum of row losses) * (1/B); correct = number of matching rows.
+__global__ void __launch_bounds__(1024) ce_finish_kernel(const float* __restrict__ row_loss,
+                                                          const int* __restrict__ row_correct, int B, float inv_b,
+                                                          float* __restrict__ loss, int64_t* __restrict__ correct) {
+  __shared__ float ls[1024];
+  __shared__ long long cs[1024];
+  const int t = threadIdx.x;
+  const int per = (B + 1023) / 1024;
+  float s = 0.0f;
+  long long c = 0;
+  for (int k = 0; k < per; ++k) {
+    int r = t * per + k;
+    if (r < B) {
+      s = s + row_loss[r];
+      if (row_correct) c += row_correct[r];
+    }
+  }
+  ls[t] = s;
+  cs[t] = c;
+  __syncthreads();
+  for (int w = 512; w > 0; w >>= 1) {
+    if (t < w) {
+      ls[t] = ls[t] + ls[t + w];
+      cs[t] += cs[t + w];
+    }
+    __syncthreads();
+  }
+  if (t == 0) {
+    if (loss) *loss = ls[0] * inv_b;
+    if (correct) *correct = cs[0];
+  }
+}
+
+// dpre = pre > 0 ? g : 0 and per-chunk column partial sums (4 columns per thread).
+__global__ void __launch_bounds__(256) relu_bw_colsum_vec_kernel(const float4* __restrict__ g, const float4* __restrict__ pre,
+                                                                 size_t rows, size_t cols4, int rows_per_chunk,
+                                                                 float4* __restrict__ dpre, float4* __restrict__ partial) {
+  size_t c = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= cols4) return;
+  size_t r0 = (size_t)blockIdx.y * rows_per_chunk;
+  size_t r1 = r0 + rows_per_chunk < rows ? r0 + rows_per_chunk : rows;
+  float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (size_t r = r0; r < r1; ++r) {
+    float4 gv = g[r * cols4 + c], pv = pre[r * cols4 + c];
+    float4 d = make_float4(pv.x > 0.0f ? gv.x : 0.0f, pv.y > 0.0f ? gv.y : 0.0f, pv.z > 0.0f ? gv.z : 0.0f,
+                           pv.w > 0.0f ? gv.w : 0.0f);
+    dpre[r * cols4 + c] = d;
+    s.x = s.x + d.x;
+    s.y = s.y + d.y;
+    s.z = s.z + d.z;
+    s.w = s.w + d.w;
+  }
+  if (partial) partial[(size_t)blockIdx.y * cols4 + c] = s;
+}
+
+__global__ void __launch_bounds__(256) relu_bw_colsum_scalar_kernel(const float* __restrict__ g, const float* __restrict__ pre,
+                                                                    size_t rows, size_t cols, int rows_per_chunk,
+                                                                    float* __restrict__ dpre, float* __restrict__ partial) {
+  size_t c = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= cols) return;
+  size_t r0 = (size_t)blockIdx.y * rows_per_chunk;
+  size_t r1 = r0 + rows_per_chunk < rows ? r0 + rows_per_chunk : rows;
+  float s = 0.0f;
+  for (size_t r = r0; r < r1; ++r) {
+    float d = pre[r * cols + c] > 0.0f ? g[r * cols + c] : 0.0f;
+    dpre[r * cols + c] = d;
+    s = s + d;
+  }
+  if (partial) partial[(size_t)blockIdx.y * cols + c] = s;
+}
+
+// colsum[c] = sum over chunks (in chunk order) of partial[chunk][c].
+__global__ void chunk_reduce_kernel(const float* __restrict__ partial, int chunks, size_t cols, float* __restrict__ out) {
+  size_t c = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= cols) return;
+  float s = 0.0f;
+  for (int k = 0; k < chunks; ++k) s = s + partial[(size_t)k * cols + c];
+  out[c] = s;
+}
+
+struct AdamWScalars {
+  float decay, b1, omb1, b2, omb2, c1, c2, eps, lr;
+};
+
+__device__ __forceinline__ void adamw_elem(float& p, float g, float& m, float& v, const AdamWScalars& k) {
+  float d = p * k.decay;                // p * (1 - lr*wd)
+  float mn = (m * k.b1) + (g * k.omb1); // m*b1 + g*(1-b1)
+  float vn = (v * k.b2) + ((g * g) * k.omb2);
+  float mh = mn * k.c1;
+  float vh = vn * k.c2;
+  float den = sqrtf(vh) + k.eps;
+  float u = (mh / den) * k.lr;
+  p = d - u;
+  m = mn;
+  v = vn;
+}
+
+__global__ void __launch_bounds__(256) adamw_vec_kernel(float4* __restrict__ p, const float4* __restrict__ g,
+                                                        float4* __restrict__ m, float4* __restrict__ v, size_t n4,
+                                                        AdamWScalars k) {
+  size_t stride = (size_t)gridDim.x * blockDim.x;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += stride) {
+    float4 pp = p[i], gg = g[i], mm = m[i], vv = v[i];
+    adamw_elem(pp.x, gg.x, mm.x, vv.x, k);
+    adamw_elem(pp.y, gg.y, mm.y, vv.y, k);
+    adamw_elem(pp.z, gg.z, mm.z, vv.z, k);
+    adamw_elem(pp.w, gg.w, mm.w, vv.w, k);
+    p[i] = pp;
+    m[i] = mm;
+    v[i] = vv;
+  }
+}
+
+__global__ void adamw_scalar_kernel(float* __restrict__ p, const float* __restrict__ g, float* __restrict__ m,
+                                    float* __restrict__ v, size_t begin, size_t n, AdamWScalars k) {
+  size_t stride = (size_t)gridDim.x * blockDim.x;
+  for (size_t i = begin + (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    float pp = p[i], mm = m[i], vv = v[i];
+    adamw_elem(pp, g[i], mm, vv, k);
+    p[i] = pp;
+    m[i] = mm;
+    v[i] = vv;
+  }
+}
+
+__global__ void __launch_bounds__(256) sgd_vec_kernel(float4* __restrict__ p, const float4* __restrict__ g, size_t n4, float lr) {
+  size_t stride = (size_t)gridDim.x * blockDim.x;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += stride) {
+    float4 pp = p[i], gg = g[i];
+    pp.x = pp.x - gg.x * lr;
+    pp.y = pp.y - gg.y * lr;
+    pp.z = pp.z - gg.z * lr;
+    pp.w = pp.w - gg.w * lr;
+    p[i] = pp;
+  }
+}
+
+__global__ void sgd_scalar_kernel(float* __restrict__ p, const float* __restrict__ g, size_t begin, size_t n, float lr) {
+  size_t stride = (size_t)gridDim.x * blockDim.x;
+  for (size_t i = begin + (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) p[i] = p[i] - g[i] * lr;
+}
+
+inline bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; }
+
+}  // namespace
+
+void softmax_ce(orca_hip_ctx* ctx, const float* logits, size_t B, size_t C, const float* onehot, const int32_t* labels,
+                float* loss, float* dlogits, int32_t* preds, int64_t* correct) {
+  if ((onehot == nullptr) == (labels == nullptr))
+    fail(ORCA_HIP_ERR_INTERNAL, "softmax_ce needs exactly one of one-hot targets or labels");
+  if (B == 0 || C == 0) fail(ORCA_HIP_ERR_SHAPE, "Shape mismatch during softmax_ce: empty logits");
+  if (C > 4096) fail(ORCA_HIP_ERR_SHAPE, "Shape mismatch during softmax_ce: expected at most 4096 classes, got " + std::to_string(C));
+  if (B > (size_t)INT32_MAX) fail(ORCA_HIP_ERR_SHAPE, "softmax_ce: too many rows");
+  Scratch row_loss(ctx, sizeof(float) * B);
+  Scratch row_correct(ctx, sizeof(int) * B);
+  const float inv_b = 1.0f / (float)B;
+  const int rows_per_block = 4;
+  dim3 grid((unsigned)((B + rows_per_block - 1) / rows_per_block));
+  int* rc = correct ? row_correct.as<int>() : nullptr;
+  {
+    ProfScope ps(ctx, "softmax_ce", 0.0, 4.0 * (double)B * C * (dlogits ? 2 : 1) + 4.0 * B);
+#define CE_LAUNCH(VPL)                                                                                      \
+  hipLaunchKernelGGL(softmax_ce_kernel<VPL>, grid, dim3(256), 0, ctx->stream, logits, (int)B, (int)C, onehot, \
+                     labels, inv_b, row_loss.as<float>(), dlogits, preds, rc)
+    if (C <= 64) CE_LAUNCH(1);
+    else if (C <= 256) CE_LAUNCH(4);
+    else if (C <= 1024) CE_LAUNCH(16);
+    else CE_LAUNCH(64);
+#undef CE_LAUNCH
+    ORCA_HIP_CHECK(hipGetLastError());
+  }
+  if (loss || correct) {
+    hipLaunchKernelGGL(ce_finish_kernel, dim3(1), dim3(1024), 0, ctx->stream, row_loss.as<float>(), rc, (int)B,
+                       inv_b, loss, correct);
+    ORCA_HIP_CHECK(hipGetLastError());
+  }
+}
+
+void adamw(orca_hip_ctx* ctx, float* p, const float* g, float* m, float* v, size_t n, double lr, double b1, double b2,
+           double eps, double wd, int64_t t) {
+  if (n == 0) return;
+  if (t < 1) fail(ORCA_HIP_ERR_INTERNAL, "adamw step count must be >= 1");
+  AdamWScalars k;
+  k.decay = (float)(1.0 - lr * wd);
+  k.b1 = (float)b1;
+  k.omb1 = (float)(1.0 - b1);
+  k.b2 = (float)b2;
+  k.omb2 = (float)(1.0 - b2);
+  k.c1 = (float)(1.0 / (1.0 - std::pow(b1, (double)t)));
+  k.c2 = (float)(1.0 / (1.0 - std::pow(b2, (double)t)));
+  k.eps = (float)eps;
+  k.lr = (float)lr;
+  ProfScope ps(ctx, "adamw", 0.0, 28.0 * (double)n);
+  size_t done = 0;
+  if (aligned16(p) && aligned16(g) && aligned16(m) && aligned16(v)) {
+    size_t n4 = n / 4;
+    if (n4) {
+      unsigned gsz = grid_for(n4, 256, ctx->num_cus * 8);
+      hipLaunchKernelGGL(adamw_vec_kernel, dim3(gsz), dim3(256), 0, ctx->stream, reinterpret_cast<float4*>(p),
+                         reinterpret_cast<const float4*>(g), reinterpret_cast<float4*>(m),
+                         reinterpret_cast<float4*>(v), n4, k);
+    }
+    done = 4 * n4;
+  }
+  if (done < n) {
+    unsigned gsz = grid_for(n - done, 256, ctx->num_cus * 8);
+    hipLaunchKernelGGL(adamw_scalar_kernel, dim3(gsz), dim3(256), 0, ctx->stream, p, g, m, v, done, n, k);
+  }
+  ORCA_HIP_CHECK(hipGetLastError());
+}
+
+void sgd(orca_hip_ctx* ctx, float* p, const float* g, size_t n, double lr) {
+  if (n == 0) return;
+  const float flr = (float)lr;
+  ProfScope ps(ctx, "sgd", 0.0, 12.0 * (double)n);
+  size_t done = 0;
+  if (aligned16(p) && aligned16(g)) {
+    size_t n4 = n / 4;
+    if (n4) {
+      unsigned gsz = grid_for(n4, 256, ctx->num_cus * 8);
+      hipLaunchKernelGGL(sgd_vec_kernel, dim3(gsz), dim3(256), 0, ctx->stream, reinterpret_cast<float4*>(p),
+                         reinterpret_cast<const float4*>(g), n4, flr);
+    }
+    done = 4 * n4;
+  }
+  if (done < n) {
+    unsigned gsz = grid_for(n - done, 256, ctx->num_cus * 8);
+    hipLaunchKernelGGL(sgd_scalar_kernel, dim3(gsz), dim3(256), 0, ctx->stream, p, g, done, n, flr);
+  }
+  ORCA_HIP_CHECK(hipGetLastError());
+}
+
+}  // namespace orca_hip
+
+using namespace orca_hip;
+
+extern "C" {
+
+int orca_hip_softmax_ce(orca_hip_ctx* ctx, const float* logits, size_t B, size_t C, const float* onehot,
+                        const int32_t* labels, float* loss, float* dlogits, int32_t* preds, int64_t* correct) {
+  return guard([&] {
+    bind(ctx);
+    softmax_ce(ctx, logits, B, C, onehot, labels, loss, dlogits, preds, correct);
+  });
+}
+
+int orca_hip_relu_bw_colsum(orca_hip_ctx* ctx, const float* grad, const float* pre, size_t rows, size_t cols,
+                            float* dpre, float* colsum) {
+  return guard([&] {
+    bind(ctx);
+    if (rows == 0 || cols == 0) {
+      if (colsum) launch_fill(ctx, colsum, 0.0f, cols);
+      return;
+    }
+    const int rows_per_chunk = 64;
+    const size_t chunks = (rows + rows_per_chunk - 1) / rows_per_chunk;
+    if (chunks > 65535) fail(ORCA_HIP_ERR_INTERNAL, "relu_bw_colsum: too many rows");
+    std::unique_ptr<Scratch> partial;
+    if (colsum) partial.reset(new Scratch(ctx, sizeof(float) * chunks * cols));
+    float* part = colsum ? partial->as<float>() : nullptr;
+    {
+      ProfScope ps(ctx, "relu_bw_colsum", 0.0, 12.0 * (double)rows * cols + (colsum ? 4.0 * cols : 0.0));
+      if (cols % 4 == 0 && aligned16(grad) && aligned16(pre) && aligned16(dpre)) {
+        size_t cols4 = cols / 4;
+        dim3 grid((unsigned)((cols4 + 255) / 256), (unsigned)chunks);
+        hipLaunchKernelGGL(relu_bw_colsum_vec_kernel, grid, dim3(256), 0, ctx->stream,
+                           reinterpret_cast<const float4*>(grad), reinterpret_cast<const float4*>(pre), rows, cols4,
+                           rows_per_chunk, reinterpret_cast<float4*>(dpre), reinterpret_cast<float4*>(part));
+      } else {
+        dim3 grid((unsigned)((cols + 255) / 256), (unsigned)chunks);
+        hipLaunchKernelGGL(relu_bw_colsum_scalar_kernel, grid, dim3(256), 0, ctx->stream, grad, pre, rows, cols,
+                           rows_per_chunk, dpre, part);
+      }
+      ORCA_HIP_CHECK(hipGetLastError());
+    }
+    if (colsum) {
+      ProfScope ps(ctx, "colsum_chunks", 0.0, 4.0 * (double)chunks * cols + 4.0 * cols);
+      hipLaunchKernelGGL(chunk_reduce_kernel, dim3((unsigned)((cols + 255) / 256)), dim3(256), 0, ctx->stream, part,
+                         (int)chunks, cols, colsum);
+      ORCA_HIP_CHECK(hipGetLastError());
+    }
+  });
+}
+
+int orca_hip_adamw_step(orca_hip_ctx* ctx, float* p, const float* g, float* m, float* v, size_t n, double lr,
+                        double beta1, double beta2, double eps, double weight_decay, int64_t t) {
+  return guard([&] {
+    bind(ctx);
+    adamw(ctx, p, g, m, v, n, lr, beta1, beta2, eps, weight_decay, t);
+  });
+}
+
+int orca_hip_sgd_step(orca_hip_ctx* ctx, float* p, const float* g, size_t n, double lr) {
+  return guard([&] {
+    bind(ctx);
+    sgd(ctx, p, g, n, lr);
+  });
+}
+
+}  // extern "C"

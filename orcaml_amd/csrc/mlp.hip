@@ -1,0 +1,309 @@
+// Device-resident training step of nn.Sequential(Linear, ReLU, ..., Linear)
+// + CrossEntropyLoss + SGD/AdamW (python/orca/nn/{linear,activation,
+// container,loss}.py, python/orca/optim/{sgd,adamw}.py).
+//
+// HBM layout: parameters, gradients and the AdamW moments live in four flat
+// arenas with one common layout, [W_0 | b_0 | W_1 | b_1 | ...], each tensor
+// starting on a 256-byte boundary (padding is zero in every arena and stays
+// zero under both updates).  Activations keep only the ReLU outputs: the
+// mask of ReluBackward ([pre > 0], orca-backend-cpu/src/backend.rs:434)
+// equals [relu(pre) > 0].  A step is, for L layers:
+//   forward   L GEMMs  (bias + ReLU fused into the epilogue; bias only on the last)
+//   loss      fused softmax-CE forward/gradient/argmax + a one-block finish
+//   backward  L GEMMs dW = A^T dZ with the bias column sum fused in, and
+//             L-1 GEMMs dZ_prev = (dZ W^T) * [H > 0] with the mask fused in
+//   update    one AdamW or SGD pass over the whole parameter arena.
+// Every buffer is allocated at creation; a step allocates nothing (split-K
+// workspaces come from the context's cache) and never synchronises.
+#include <cstring>
+#include <vector>
+
+#include "runtime.hpp"
+
+struct orca_hip_mlp {
+  orca_hip_ctx* ctx = nullptr;
+  std::vector<size_t> dims;
+  size_t L = 0, B = 0;
+  orca_hip_optim opt{};
+  int64_t t = 0;
+  std::vector<size_t> off;  // arena offset of parameter i (floats)
+  std::vector<size_t> cnt;  // element count of parameter i
+  size_t arena = 0;         // arena length (floats)
+  float *P = nullptr, *G = nullptr, *Mo = nullptr, *Vo = nullptr;
+  float* x = nullptr;
+  float* onehot = nullptr;
+  int32_t* labels = nullptr;
+  std::vector<float*> H;   // ReLU outputs of layers 0..L-2
+  float* logits = nullptr;
+  float* dlogits = nullptr;
+  float* dz[2] = {nullptr, nullptr};
+  float* loss = nullptr;
+  int64_t* correct = nullptr;
+  int32_t* preds = nullptr;
+  std::vector<void*> owned;
+  bool have_batch = false;
+
+  float* dev(size_t n) {
+    void* p = ctx->alloc.allocate(n * sizeof(float) + 256, ctx->stream);
+    owned.push_back(p);
+    return static_cast<float*>(p);
+  }
+  ~orca_hip_mlp() {
+    for (void* p : owned) ctx->alloc.release(p);
+  }
+};
+
+namespace orca_hip {
+namespace {
+
+void step(orca_hip_mlp* m) {
+  orca_hip_ctx* ctx = m->ctx;
+  const size_t L = m->L, B = m->B, C = m->dims[L];
+  // ---- forward ----
+  for (size_t l = 0; l < L; ++l) {
+    const size_t K = m->dims[l], N = m->dims[l + 1];
+    const float* a = l == 0 ? m->x : m->H[l - 1];
+    GemmEpi e;
+    e.kind = l + 1 < L ? ORCA_HIP_EPI_BIAS_RELU : ORCA_HIP_EPI_BIAS;
+    e.bias = m->P + m->off[2 * l + 1];
+    float* out = l + 1 < L ? m->H[l] : m->logits;
+    gemm(ctx, false, false, B, N, K, a, K, 0, m->P + m->off[2 * l], N, 0, out, N, 0, 1, e);
+  }
+  // ---- loss and its gradient ----
+  softmax_ce(ctx, m->logits, B, C, m->onehot, m->onehot ? nullptr : m->labels, m->loss, m->dlogits, m->preds,
+             m->correct);
+  // ---- backward ----
+  const float* g = m->dlogits;
+  int ping = 0;
+  for (size_t l = L; l-- > 0;) {
+    const size_t K = m->dims[l], N = m->dims[l + 1];
+    const float* a = l == 0 ? m->x : m->H[l - 1];
+    GemmEpi ew;
+    ew.colsum = m->G + m->off[2 * l + 1];  // bias gradient
+    gemm(ctx, true, false, K, N, B, a, K, 0, g, N, 0, m->G + m->off[2 * l], N, 0, 1, ew);
+    if (l > 0) {
+      GemmEpi ex;
+      ex.kind = ORCA_HIP_EPI_RELU_MASK;
+      ex.mask = m->H[l - 1];
+      ex.ldmask = K;
+      float* dz = m->dz[ping];
+      gemm(ctx, false, true, B, K, N, g, N, 0, m->P + m->off[2 * l], N, 0, dz, K, 0, 1, ex);
+      g = dz;
+      ping ^= 1;
+    }
+  }
+  // ---- update (parameter order W_0, b_0, W_1, ...; one pass over the arena) ----
+  if (m->opt.kind == 1) {
+    m->t += 1;
+    adamw(ctx, m->P, m->G, m->Mo, m->Vo, m->arena, m->opt.lr, m->opt.beta1, m->opt.beta2, m->opt.eps,
+          m->opt.weight_decay, m->t);
+  } else {
+    sgd(ctx, m->P, m->G, m->arena, m->opt.lr);
+  }
+}
+
+orca_hip_mlp* checked(orca_hip_mlp* m) {
+  if (!m) fail(ORCA_HIP_ERR_INTERNAL, "null orca_hip_mlp");
+  bind(m->ctx);
+  return m;
+}
+
+void check_index(const orca_hip_mlp* m, size_t index, size_t n) {
+  if (index >= m->off.size())
+    fail(ORCA_HIP_ERR_INTERNAL, "parameter index " + std::to_string(index) + " out of range");
+  if (n != m->cnt[index])
+    fail(ORCA_HIP_ERR_SHAPE, "Shape mismatch during mlp parameter copy: expected " + std::to_string(m->cnt[index]) +
+                                 " elements, got " + std::to_string(n));
+}
+
+}  // namespace
+}  // namespace orca_hip
+
+using namespace orca_hip;
+
+extern "C" {
+
+int orca_hip_mlp_create(orca_hip_ctx* ctx, const size_t* dims, size_t n_layers, size_t batch,
+                        const orca_hip_optim* opt, orca_hip_mlp** out) {
+  return guard([&] {
+    bind(ctx);
+    if (!dims || !opt || !out) fail(ORCA_HIP_ERR_INTERNAL, "null argument");
+    if (n_layers == 0 || batch == 0) fail(ORCA_HIP_ERR_SHAPE, "Shape mismatch during mlp_create: empty model or batch");
+    for (size_t i = 0; i <= n_layers; ++i)
+      if (dims[i] == 0) fail(ORCA_HIP_ERR_SHAPE, "Shape mismatch during mlp_create: zero-width layer");
+    if (dims[n_layers] > 4096) fail(ORCA_HIP_ERR_SHAPE, "Shape mismatch during mlp_create: at most 4096 classes");
+    if (opt->kind != 0 && opt->kind != 1) fail(ORCA_HIP_ERR_INTERNAL, "unknown optimizer kind");
+    auto m = std::unique_ptr<orca_hip_mlp>(new orca_hip_mlp());
+    m->ctx = ctx;
+    m->dims.assign(dims, dims + n_layers + 1);
+    m->L = n_layers;
+    m->B = batch;
+    m->opt = *opt;
+    size_t o = 0;
+    for (size_t l = 0; l < n_layers; ++l) {
+      for (size_t n : {dims[l] * dims[l + 1], dims[l + 1]}) {
+        m->off.push_back(o);
+        m->cnt.push_back(n);
+        o += (n + 63) / 64 * 64;
+      }
+    }
+    m->arena = o;
+    m->P = m->dev(o);
+    m->G = m->dev(o);
+    launch_fill(ctx, m->P, 0.0f, o);
+    launch_fill(ctx, m->G, 0.0f, o);
+    if (opt->kind == 1) {
+      m->Mo = m->dev(o);
+      m->Vo = m->dev(o);
+      launch_fill(ctx, m->Mo, 0.0f, o);
+      launch_fill(ctx, m->Vo, 0.0f, o);
+    }
+    const size_t C = dims[n_layers];
+    m->x = m->dev(batch * dims[0]);
+    m->labels = reinterpret_cast<int32_t*>(m->dev(batch));
+    size_t maxh = 1;
+    for (size_t l = 1; l < n_layers; ++l) {
+      m->H.push_back(m->dev(batch * dims[l]));
+      maxh = std::max(maxh, dims[l]);
+    }
+    m->logits = m->dev(batch * C);
+    m->dlogits = m->dev(batch * C);
+    m->dz[0] = m->dev(batch * maxh);
+    m->dz[1] = m->dev(batch * maxh);
+    m->loss = m->dev(1);
+    m->correct = reinterpret_cast<int64_t*>(m->dev(2));
+    m->preds = reinterpret_cast<int32_t*>(m->dev(batch));
+    ORCA_HIP_CHECK(hipStreamSynchronize(ctx->stream));
+    *out = m.release();
+  });
+}
+
+int orca_hip_mlp_destroy(orca_hip_mlp* mlp) {
+  return guard([&] {
+    if (!mlp) return;
+    bind(mlp->ctx);
+    ORCA_HIP_CHECK(hipStreamSynchronize(mlp->ctx->stream));
+    delete mlp;
+  });
+}
+
+int orca_hip_mlp_param_numel(const orca_hip_mlp* mlp, size_t index, size_t* n) {
+  return guard([&] {
+    if (!mlp || !n) fail(ORCA_HIP_ERR_INTERNAL, "null argument");
+    if (index >= mlp->cnt.size()) fail(ORCA_HIP_ERR_INTERNAL, "parameter index out of range");
+    *n = mlp->cnt[index];
+  });
+}
+
+int orca_hip_mlp_set_param(orca_hip_mlp* mlp, size_t index, const float* host, size_t n) {
+  return guard([&] {
+    checked(mlp);
+    check_index(mlp, index, n);
+    ORCA_HIP_CHECK(hipMemcpyAsync(mlp->P + mlp->off[index], host, n * sizeof(float), hipMemcpyHostToDevice,
+                                  mlp->ctx->stream));
+    ORCA_HIP_CHECK(hipStreamSynchronize(mlp->ctx->stream));
+  });
+}
+
+static int read_arena(orca_hip_mlp* mlp, const float* arena, size_t index, float* host, size_t n) {
+  return guard([&] {
+    checked(mlp);
+    check_index(mlp, index, n);
+    if (!arena) fail(ORCA_HIP_ERR_INTERNAL, "state not present for this optimizer");
+    ORCA_HIP_CHECK(hipMemcpyAsync(host, arena + mlp->off[index], n * sizeof(float), hipMemcpyDeviceToHost,
+                                  mlp->ctx->stream));
+    ORCA_HIP_CHECK(hipStreamSynchronize(mlp->ctx->stream));
+  });
+}
+
+int orca_hip_mlp_get_param(orca_hip_mlp* mlp, size_t index, float* host, size_t n) {
+  return read_arena(mlp, mlp ? mlp->P : nullptr, index, host, n);
+}
+
+int orca_hip_mlp_get_grad(orca_hip_mlp* mlp, size_t index, float* host, size_t n) {
+  return read_arena(mlp, mlp ? mlp->G : nullptr, index, host, n);
+}
+
+int orca_hip_mlp_get_moment(orca_hip_mlp* mlp, int which, size_t index, float* host, size_t n) {
+  return read_arena(mlp, mlp ? (which == 0 ? mlp->Mo : mlp->Vo) : nullptr, index, host, n);
+}
+
+int orca_hip_mlp_set_batch(orca_hip_mlp* mlp, const float* x, const float* onehot, const int32_t* labels) {
+  return guard([&] {
+    checked(mlp);
+    if (!x || (onehot == nullptr) == (labels == nullptr))
+      fail(ORCA_HIP_ERR_INTERNAL, "set_batch needs x and exactly one of one-hot targets or labels");
+    hipStream_t s = mlp->ctx->stream;
+    const size_t B = mlp->B, C = mlp->dims[mlp->L];
+    ORCA_HIP_CHECK(hipMemcpyAsync(mlp->x, x, B * mlp->dims[0] * sizeof(float), hipMemcpyHostToDevice, s));
+    if (onehot) {
+      if (!mlp->onehot) mlp->onehot = mlp->dev(B * C);
+      ORCA_HIP_CHECK(hipMemcpyAsync(mlp->onehot, onehot, B * C * sizeof(float), hipMemcpyHostToDevice, s));
+    } else {
+      ORCA_HIP_CHECK(hipMemcpyAsync(mlp->labels, labels, B * sizeof(int32_t), hipMemcpyHostToDevice, s));
+      if (mlp->onehot) {  // switch to label targets
+        mlp->ctx->alloc.release(mlp->onehot);
+        for (auto& p : mlp->owned)
+          if (p == mlp->onehot) p = nullptr;
+        mlp->owned.erase(std::remove(mlp->owned.begin(), mlp->owned.end(), nullptr), mlp->owned.end());
+        mlp->onehot = nullptr;
+      }
+    }
+    ORCA_HIP_CHECK(hipStreamSynchronize(s));
+    mlp->have_batch = true;
+  });
+}
+
+int orca_hip_mlp_batch_ptrs(orca_hip_mlp* mlp, float** x, int32_t** labels) {
+  return guard([&] {
+    checked(mlp);
+    if (x) *x = mlp->x;
+    if (labels) *labels = mlp->labels;
+  });
+}
+
+int orca_hip_mlp_step(orca_hip_mlp* mlp) {
+  return guard([&] {
+    checked(mlp);
+    if (!mlp->have_batch) fail(ORCA_HIP_ERR_INTERNAL, "mlp_step before set_batch");
+    step(mlp);
+  });
+}
+
+int orca_hip_mlp_read_metrics(orca_hip_mlp* mlp, float* loss, int64_t* correct) {
+  return guard([&] {
+    checked(mlp);
+    hipStream_t s = mlp->ctx->stream;
+    if (loss) ORCA_HIP_CHECK(hipMemcpyAsync(loss, mlp->loss, sizeof(float), hipMemcpyDeviceToHost, s));
+    if (correct) ORCA_HIP_CHECK(hipMemcpyAsync(correct, mlp->correct, sizeof(int64_t), hipMemcpyDeviceToHost, s));
+    ORCA_HIP_CHECK(hipStreamSynchronize(s));
+  });
+}
+
+int orca_hip_mlp_get_logits(orca_hip_mlp* mlp, float* host, size_t n) {
+  return guard([&] {
+    checked(mlp);
+    size_t want = mlp->B * mlp->dims[mlp->L];
+    if (n != want) fail(ORCA_HIP_ERR_SHAPE, "Shape mismatch during mlp_get_logits: expected " + std::to_string(want));
+    ORCA_HIP_CHECK(hipMemcpyAsync(host, mlp->logits, n * sizeof(float), hipMemcpyDeviceToHost, mlp->ctx->stream));
+    ORCA_HIP_CHECK(hipStreamSynchronize(mlp->ctx->stream));
+  });
+}
+
+int orca_hip_mlp_get_preds(orca_hip_mlp* mlp, int32_t* host, size_t n) {
+  return guard([&] {
+    checked(mlp);
+    if (n != mlp->B) fail(ORCA_HIP_ERR_SHAPE, "Shape mismatch during mlp_get_preds: expected " + std::to_string(mlp->B));
+    ORCA_HIP_CHECK(hipMemcpyAsync(host, mlp->preds, n * sizeof(int32_t), hipMemcpyDeviceToHost, mlp->ctx->stream));
+    ORCA_HIP_CHECK(hipStreamSynchronize(mlp->ctx->stream));
+  });
+}
+
+int orca_hip_mlp_get_step_count(const orca_hip_mlp* mlp, int64_t* t) {
+  return guard([&] {
+    if (!mlp || !t) fail(ORCA_HIP_ERR_INTERNAL, "null argument");
+    *t = mlp->t;
+  });
+}
+
+}  // extern "C"

@@ -1,0 +1,197 @@
+// Host runtime shared by every translation unit of liborca_hip.so: error
+// mapping onto orca_core::OrcaError codes, the per-device context with its
+// stream-ordered caching allocator, and optional per-launch event timing.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdint>
+#include <map>
+#include <memory>
+#include <mutex>
+#include <stdexcept>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "../../include/orca_hip.h"
+
+namespace orca_hip {
+
+// An error carrying one of the ORCA_HIP_ERR_* codes.
+struct Error : std::runtime_error {
+  int code;
+  Error(int c, const std::string& m) : std::runtime_error(m), code(c) {}
+};
+
+void set_last_error(const std::string& msg);
+
+[[noreturn]] inline void fail(int code, const std::string& msg) { throw Error(code, msg); }
+
+#define ORCA_HIP_CHECK(expr)                                                                   \
+  do {                                                                                         \
+    hipError_t e_ = (expr);                                                                    \
+    if (e_ != hipSuccess)                                                                      \
+      ::orca_hip::fail(ORCA_HIP_ERR_INTERNAL, std::string(#expr) + ": " + hipGetErrorString(e_)); \
+  } while (0)
+
+// Runs f, converting exceptions into a status code + thread-local message.
+template <class F>
+int guard(F&& f) {
+  try {
+    f();
+    return ORCA_HIP_OK;
+  } catch (const Error& e) {
+    set_last_error(e.what());
+    return e.code;
+  } catch (const std::exception& e) {
+    set_last_error(std::string("internal error: ") + e.what());
+    return ORCA_HIP_ERR_INTERNAL;
+  } catch (...) {
+    set_last_error("internal error: unknown exception");
+    return ORCA_HIP_ERR_INTERNAL;
+  }
+}
+
+// Size-class caching allocator.  All work of a context runs on one in-order
+// stream, so a block returned here can be handed to the next request at once:
+// any later kernel using it is ordered after every earlier kernel that used
+// it.  Blocks are 256-byte aligned (hipMalloc alignment).
+class CachingAllocator {
+ public:
+  void* allocate(size_t bytes, hipStream_t stream);
+  void release(void* p);
+  void empty(hipStream_t stream);
+  size_t size_of(void* p);
+  void stats(size_t* live, size_t* cached, size_t* mallocs);
+  ~CachingAllocator();
+
+  static size_t round_size(size_t bytes);
+
+ private:
+  std::mutex mu_;
+  std::unordered_map<void*, size_t> live_;
+  std::multimap<size_t, void*> cached_;
+  size_t live_bytes_ = 0, cached_bytes_ = 0, mallocs_ = 0;
+};
+
+// Per-kernel timing aggregation (enabled by orca_hip_prof_enable).
+struct Profiler {
+  struct Pending {
+    std::string name;
+    hipEvent_t start, stop;
+    double flops, bytes;
+  };
+  struct Agg {
+    long launches = 0;
+    double total_ms = 0, flops = 0, bytes = 0;
+  };
+  bool enabled = false;
+  std::vector<Pending> pending;
+  std::vector<hipEvent_t> pool;
+  std::map<std::string, Agg> agg;
+
+  hipEvent_t get_event();
+  void drain();  // requires the stream to be synchronised
+  ~Profiler();
+};
+
+}  // namespace orca_hip
+
+struct orca_hip_ctx {
+  int device = 0;
+  int num_cus = 256;
+  hipStream_t stream = nullptr;
+  orca_hip::CachingAllocator alloc;
+  orca_hip::Profiler prof;
+  hipEvent_t timer_start = nullptr, timer_stop = nullptr;
+  std::mutex mu;
+};
+
+namespace orca_hip {
+
+// Makes ctx's device current for the calling thread.
+void bind(orca_hip_ctx* ctx);
+
+// Brackets one launch with events when profiling is on.
+class ProfScope {
+ public:
+  ProfScope(orca_hip_ctx* ctx, const char* name, double flops, double bytes);
+  ~ProfScope();
+
+ private:
+  orca_hip_ctx* ctx_;
+  Profiler::Pending rec_;
+  bool on_;
+};
+
+// RAII device buffer from the context allocator (freed stream-ordered).
+class Scratch {
+ public:
+  Scratch(orca_hip_ctx* ctx, size_t bytes) : ctx_(ctx), p_(bytes ? ctx->alloc.allocate(bytes, ctx->stream) : nullptr) {}
+  ~Scratch() {
+    if (p_) ctx_->alloc.release(p_);
+  }
+  Scratch(const Scratch&) = delete;
+  Scratch& operator=(const Scratch&) = delete;
+  template <class T>
+  T* as() const {
+    return static_cast<T*>(p_);
+  }
+
+ private:
+  orca_hip_ctx* ctx_;
+  void* p_;
+};
+
+inline void check_ctx(const orca_hip_ctx* ctx) {
+  if (!ctx) fail(ORCA_HIP_ERR_INTERNAL, "null orca_hip_ctx");
+}
+
+inline void check_f32(int dtype, const char* op) {
+  if (dtype != ORCA_HIP_F32)
+    fail(ORCA_HIP_ERR_UNSUPPORTED_DTYPE, std::string("Unsupported dtype for ") + op + " (hip): code " +
+                                             std::to_string(dtype));
+}
+
+size_t numel(const size_t* shape, size_t rank);
+std::string shape_str(const size_t* shape, size_t rank);
+
+// Grid size for grid-stride element loops.
+inline unsigned grid_for(size_t work_items, unsigned block, unsigned max_blocks) {
+  size_t g = (work_items + block - 1) / block;
+  if (g < 1) g = 1;
+  if (g > max_blocks) g = max_blocks;
+  return static_cast<unsigned>(g);
+}
+
+// Allocates a fresh output buffer of n floats for a trait op.
+float* new_output(orca_hip_ctx* ctx, size_t n);
+
+// ---- launchers shared between translation units (device pointers, async) ----
+void launch_fill(orca_hip_ctx* ctx, float* dst, float v, size_t n);
+void launch_copy(orca_hip_ctx* ctx, float* dst, const float* src, size_t n);
+// colsum[c] = sum_r src[r*ld + c] in ascending r (the sum_to_shape order).
+void launch_colsum(orca_hip_ctx* ctx, const float* src, size_t rows, size_t cols, size_t ld, float* colsum);
+
+struct GemmEpi {
+  int kind = ORCA_HIP_EPI_NONE;
+  const float* bias = nullptr;
+  const float* mask = nullptr;
+  size_t ldmask = 0;
+  float* colsum = nullptr;
+};
+// Batched GEMM: C[b] = op(A[b]) op(B[b]) with element strides sa/sb/sc between batch entries.
+void gemm(orca_hip_ctx* ctx, bool trans_a, bool trans_b, size_t M, size_t N, size_t K, const float* A,
+          size_t lda, size_t sa, const float* B, size_t ldb, size_t sb, float* C, size_t ldc, size_t sc,
+          size_t batch, const GemmEpi& epi);
+
+void softmax_ce(orca_hip_ctx* ctx, const float* logits, size_t B, size_t C, const float* onehot,
+                const int32_t* labels, float* loss, float* dlogits, int32_t* preds, int64_t* correct);
+
+void adamw(orca_hip_ctx* ctx, float* p, const float* g, float* m, float* v, size_t n, double lr, double b1,
+           double b2, double eps, double wd, int64_t t);
+void sgd(orca_hip_ctx* ctx, float* p, const float* g, size_t n, double lr);
+
+}  // namespace orca_hip

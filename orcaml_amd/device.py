@@ -1,0 +1,112 @@
+"""HIP context and device buffers over the C ABI (include/orca_hip.h)."""
+from __future__ import annotations
+
+import ctypes
+import json
+
+import numpy as np
+
+from . import _lib
+
+
+class Context:
+    """One HIP device, its stream and its caching allocator
+    (orca_hip_ctx_create).  Plays the role of the process-global backend
+    behind global_backend_gpu() (orca-python/src/lib.rs:23-33)."""
+
+    def __init__(self, device: int = 0):
+        h = ctypes.c_void_p()
+        _lib.call("orca_hip_ctx_create", device, ctypes.byref(h))
+        self.handle = h
+        self.device = device
+
+    def close(self) -> None:
+        if self.handle:
+            _lib.call("orca_hip_ctx_destroy", self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # ---- memory ----
+    def alloc(self, nbytes: int) -> "Buffer":
+        p = ctypes.c_void_p()
+        _lib.call("orca_hip_alloc", self.handle, nbytes, ctypes.byref(p))
+        return Buffer(self, p.value, nbytes)
+
+    def upload(self, arr: np.ndarray) -> "Buffer":
+        arr = np.ascontiguousarray(arr)
+        buf = self.alloc(max(arr.nbytes, 4))
+        if arr.nbytes:
+            _lib.call("orca_hip_h2d", self.handle, buf.ptr, arr.ctypes.data_as(ctypes.c_void_p), arr.nbytes)
+        return buf
+
+    def sync(self) -> None:
+        _lib.call("orca_hip_sync", self.handle)
+
+    def mem_stats(self) -> dict:
+        live, cached, mallocs = ctypes.c_size_t(), ctypes.c_size_t(), ctypes.c_size_t()
+        _lib.call("orca_hip_mem_stats", self.handle, ctypes.byref(live), ctypes.byref(cached), ctypes.byref(mallocs))
+        return dict(live=live.value, cached=cached.value, device_allocs=mallocs.value)
+
+    def empty_cache(self) -> None:
+        _lib.call("orca_hip_empty_cache", self.handle)
+
+    # ---- timing ----
+    def prof_enable(self, on: bool = True) -> None:
+        _lib.call("orca_hip_prof_enable", self.handle, 1 if on else 0)
+
+    def prof_reset(self) -> None:
+        _lib.call("orca_hip_prof_reset", self.handle)
+
+    def prof_report(self) -> dict:
+        buf = ctypes.create_string_buffer(1 << 16)
+        _lib.call("orca_hip_prof_report", self.handle, buf, len(buf))
+        return json.loads(buf.value.decode())
+
+    def timer_start(self) -> None:
+        _lib.call("orca_hip_timer_start", self.handle)
+
+    def timer_stop(self) -> float:
+        ms = ctypes.c_float()
+        _lib.call("orca_hip_timer_stop", self.handle, ctypes.byref(ms))
+        return ms.value
+
+
+class Buffer:
+    """A device allocation owned by a Context; released on garbage collection."""
+
+    def __init__(self, ctx: Context, ptr: int, nbytes: int):
+        self.ctx = ctx
+        self.ptr = ptr
+        self.nbytes = nbytes
+
+    def free(self) -> None:
+        if self.ptr and self.ctx.handle:
+            _lib.call("orca_hip_free", self.ctx.handle, self.ptr)
+        self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+    def download(self, dtype=np.float32, count: int | None = None) -> np.ndarray:
+        dtype = np.dtype(dtype)
+        if count is None:
+            count = self.nbytes // dtype.itemsize
+        out = np.empty(count, dtype)
+        if out.nbytes:
+            _lib.call("orca_hip_d2h", self.ctx.handle, out.ctypes.data_as(ctypes.c_void_p), self.ptr, out.nbytes)
+        return out
+
+    def upload(self, arr: np.ndarray) -> None:
+        arr = np.ascontiguousarray(arr)
+        if arr.nbytes > self.nbytes:
+            raise ValueError("upload larger than the buffer")
+        if arr.nbytes:
+            _lib.call("orca_hip_h2d", self.ctx.handle, self.ptr, arr.ctypes.data_as(ctypes.c_void_p), arr.nbytes)

@@ -1,0 +1,201 @@
+"""GPU parity of the fused kernels (GEMM, softmax-CE, AdamW/SGD) and of the
+device-resident MLP training step against the CPU oracle, through the C ABI."""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from orcaml_amd import _lib, synth
+from orcaml_amd.mlp import MLPTrainer
+from tests.util import assert_close, assert_close_scaled, int_matrix
+
+pytestmark = pytest.mark.gpu
+
+
+def run_gemm(ctx, ta, tb, A, B, epi_kind=_lib.EPI_NONE, bias=None, mask=None, colsum=False):
+    """C = op(A) op(B) on the GPU; A/B are passed in their stored layout."""
+    M = A.shape[1] if ta else A.shape[0]
+    K = A.shape[0] if ta else A.shape[1]
+    N = B.shape[0] if tb else B.shape[1]
+    dA, dB = ctx.upload(A), ctx.upload(B)
+    dC = ctx.alloc(4 * M * N)
+    keep = []
+    e = _lib.Epilogue(epi_kind, None, None, 0, None)
+    if bias is not None:
+        keep.append(ctx.upload(bias))
+        e.bias = keep[-1].ptr
+    if mask is not None:
+        keep.append(ctx.upload(mask))
+        e.mask = keep[-1].ptr
+        e.ldmask = N
+    dcs = None
+    if colsum:
+        dcs = ctx.alloc(4 * N)
+        e.colsum = dcs.ptr
+    _lib.call("orca_hip_gemm", ctx.handle, int(ta), int(tb), M, N, K, dA.ptr, A.shape[1], dB.ptr, B.shape[1],
+              dC.ptr, N, ctypes.byref(e))
+    C = dC.download(count=M * N).reshape(M, N)
+    return (C, dcs.download(count=N)) if colsum else C
+
+
+def assert_gemm_error_bound(got, A, B):
+    """Forward error of an f32 dot product of length K is at most
+    gamma_K * sum_k |a_k b_k| with gamma_K ~ K * 2^-24 (any summation order);
+    checked against the fp64 product."""
+    A64, B64 = A.astype(np.float64), B.astype(np.float64)
+    exact = A64 @ B64
+    bound = A.shape[1] * 2.0 ** -24 * (np.abs(A64) @ np.abs(B64)) + 1e-30
+    err = np.abs(got.astype(np.float64) - exact)
+    assert (err <= bound).all(), f"max err/bound {float((err / bound).max()):.3f}"
+
+
+GEMM_SHAPES = [(1, 1, 1), (64, 128, 784), (130, 70, 33), (257, 129, 1000), (1024, 10, 4096), (1024, 4096, 10),
+               (784, 384, 1024), (96, 16, 4)]
+
+
+@pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False), (True, True)])
+@pytest.mark.parametrize("M,N,K", GEMM_SHAPES)
+def test_gemm_exact_on_integers(ctx, ta, tb, M, N, K):
+    rng = np.random.default_rng(M * 7 + N * 13 + K)
+    A = int_matrix(rng, (M, K))
+    B = int_matrix(rng, (K, N))
+    want = (A.astype(np.int64) @ B.astype(np.int64)).astype(np.float32)
+    got = run_gemm(ctx, ta, tb, np.ascontiguousarray(A.T) if ta else A, np.ascontiguousarray(B.T) if tb else B)
+    np.testing.assert_array_equal(got, want)
+
+
+def test_gemm_epilogues_match_composed_ops(ctx):
+    rng = np.random.default_rng(5)
+    M, N, K = 200, 300, 150
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    B = rng.standard_normal((K, N)).astype(np.float32)
+    bias = rng.standard_normal(N).astype(np.float32)
+    prod = run_gemm(ctx, False, False, A, B)
+    assert_gemm_error_bound(prod, A, B)
+    # bias: the reference adds the expanded bias in f32 after the product
+    got = run_gemm(ctx, False, False, A, B, _lib.EPI_BIAS, bias=bias)
+    np.testing.assert_array_equal(got, O.add(prod, O.expand(bias.reshape(1, N), (M, N))))
+    got = run_gemm(ctx, False, False, A, B, _lib.EPI_BIAS_RELU, bias=bias)
+    np.testing.assert_array_equal(got, O.relu(O.add(prod, O.expand(bias.reshape(1, N), (M, N)))))
+    mask = rng.standard_normal((M, N)).astype(np.float32)
+    mask[::7, ::3] = 0.0
+    got = run_gemm(ctx, False, False, A, B, _lib.EPI_RELU_MASK, mask=mask)
+    np.testing.assert_array_equal(got, O.relu_backward(prod, mask))
+
+
+@pytest.mark.parametrize("M,N,K", [(128, 256, 64), (784, 4096, 1024), (4096, 10, 1024), (33, 70, 5)])
+def test_gemm_colsum_is_bias_gradient(ctx, M, N, K):
+    """dW = X^T dY with the bias column sum fused: the column sum must equal
+    sum_to_shape(dY, [1, N]) exactly (same ascending row order)."""
+    rng = np.random.default_rng(M + N + K)
+    X = rng.standard_normal((K, M)).astype(np.float32)  # stored [B][in]
+    dY = rng.standard_normal((K, N)).astype(np.float32)
+    dW, cs = run_gemm(ctx, True, False, X, dY, colsum=True)
+    np.testing.assert_array_equal(cs, O.sum_to_shape(dY, (1, N)).reshape(N))
+    assert_gemm_error_bound(dW, X.T, dY)
+
+
+def run_ce(ctx, logits, onehot=None, labels=None, want_grad=True):
+    B, C = logits.shape
+    dl = ctx.upload(logits)
+    doh = ctx.upload(onehot) if onehot is not None else None
+    dlb = ctx.upload(labels.astype(np.int32)) if labels is not None else None
+    loss = ctx.alloc(4)
+    grad = ctx.alloc(4 * B * C) if want_grad else None
+    preds = ctx.alloc(4 * B)
+    correct = ctx.alloc(8)
+    _lib.call("orca_hip_softmax_ce", ctx.handle, dl.ptr, B, C, doh.ptr if doh else None, dlb.ptr if dlb else None,
+              loss.ptr, grad.ptr if grad else None, preds.ptr, correct.ptr)
+    return (float(loss.download(count=1)[0]), grad.download(count=B * C).reshape(B, C) if grad else None,
+            preds.download(np.int32, B), int(correct.download(np.int64, 1)[0]))
+
+
+@pytest.mark.parametrize("B,C", [(64, 10), (1024, 10), (37, 300), (16, 4096), (3, 1)])
+def test_softmax_ce_matches_composed_reference(ctx, B, C):
+    rng = np.random.default_rng(B * C)
+    logits = (2.0 * rng.standard_normal((B, C))).astype(np.float32)
+    labels = rng.integers(0, C, B)
+    onehot = synth.one_hot(labels, C)
+    loss_ref, grad_ref = O.cross_entropy(logits, onehot)
+    for kw in (dict(onehot=onehot), dict(labels=labels)):
+        loss, grad, preds, correct = run_ce(ctx, logits, **kw)
+        assert_close(loss, loss_ref, what="loss")
+        assert_close(grad, grad_ref, what="dlogits")
+        assert_close_scaled(grad, grad_ref, what="dlogits (scaled)")
+        np.testing.assert_array_equal(preds, O.argmax_rows(logits))
+        assert correct == int((O.argmax_rows(logits) == labels).sum())
+
+
+def test_softmax_ce_ties_nan_and_equal_logits(ctx):
+    B, C = 6, 10
+    logits = np.zeros((B, C), np.float32)  # equal logits: loss = ln C, ties everywhere
+    logits[1, 3] = logits[1, 7] = 5.0      # tie at the max: first index wins
+    logits[2, 0] = np.nan                  # NaN first: argmax 0 (nothing is > NaN)
+    logits[3, 4] = np.nan                  # NaN later: ignored by the max
+    logits[4, :] = -np.inf
+    logits[4, 9] = 1.0
+    logits[5, :] = np.float32(-3.0e38)
+    labels = np.array([1, 7, 0, 4, 9, 2])
+    onehot = synth.one_hot(labels, C)
+    _, grad_ref = O.cross_entropy(logits, onehot)
+    _, grad, preds, _ = run_ce(ctx, logits, onehot=onehot)
+    np.testing.assert_array_equal(preds, O.argmax_rows(logits))
+    rows = [0, 1, 4, 5]  # rows without NaN have finite gradients to compare
+    assert_close(grad[rows], grad_ref[rows], what="dlogits")
+
+
+def test_adamw_and_sgd_bit_exact(ctx):
+    rng = np.random.default_rng(11)
+    n = 100003  # odd length exercises the scalar tail
+    p = (0.02 * rng.standard_normal(n)).astype(np.float32)
+    g = (1e-3 * rng.standard_normal(n)).astype(np.float32)
+    m = np.zeros(n, np.float32)
+    v = np.zeros(n, np.float32)
+    dp, dg, dm, dv = (ctx.upload(a) for a in (p, g, m, v))
+    ref = (p, m, v)
+    for t in range(1, 4):
+        _lib.call("orca_hip_adamw_step", ctx.handle, dp.ptr, dg.ptr, dm.ptr, dv.ptr, n, 1e-3, 0.9, 0.999, 1e-8,
+                  0.01, t)
+        ref = O.adamw_update(ref[0], g, ref[1], ref[2], t)
+    np.testing.assert_array_equal(dp.download(count=n), ref[0])
+    np.testing.assert_array_equal(dm.download(count=n), ref[1])
+    np.testing.assert_array_equal(dv.download(count=n), ref[2])
+    ds = ctx.upload(p)
+    _lib.call("orca_hip_sgd_step", ctx.handle, ds.ptr, dg.ptr, n, 0.1)
+    np.testing.assert_array_equal(ds.download(count=n), O.sgd_update(p, g, 0.1))
+
+
+def _trainer_run(ctx, w, steps, use_labels=False):
+    params, x, labels, onehot = synth.mlp_problem(1, w["dims"], w["batch"])
+    o = w["opt"]
+    tr = MLPTrainer(ctx, w["dims"], w["batch"], kind=o["kind"], lr=o["lr"], weight_decay=o.get("weight_decay", 0.0),
+                    betas=o.get("betas", (0.9, 0.999)), eps=o.get("eps", 1e-8))
+    tr.set_params(params)
+    if use_labels:
+        tr.set_batch(x, labels=labels)
+    else:
+        tr.set_batch(x, onehot=onehot)
+    losses = []
+    for _ in range(steps):
+        tr.step()
+        losses.append(tr.metrics()[0])
+    ref = O.mlp_train(w["dims"], params, x, onehot, O.make_opt(o["kind"], o["lr"], o.get("weight_decay", 0.0),
+                                                            o.get("betas", (0.9, 0.999)), o.get("eps", 1e-8)),
+                      steps=steps)
+    return tr, ref, np.array(losses, np.float32)
+
+
+@pytest.mark.parametrize("use_labels", [False, True])
+def test_mlp_step_config1_sgd(ctx, use_labels):
+    tr, ref, losses = _trainer_run(ctx, synth.WORKLOADS[1], 1, use_labels)
+    assert_close(losses, ref["losses"], what="loss")
+    for i, (g, gr) in enumerate(zip(tr.grads(), ref["grads"])):
+        assert_close(g, gr, what=f"grad {i}")
+        assert_close_scaled(g, gr, rtol=1e-3, what=f"grad {i} (scaled)")
+    for i, (p, pr) in enumerate(zip(tr.params(), ref["params"])):
+        assert_close(p, pr, what=f"param {i}")
+    np.testing.assert_array_equal(tr.preds(), ref["preds"])
+    assert tr.metrics()[1] == ref["correct"]
