@@ -259,6 +259,9 @@ int orca_hip_mlp_read_metrics(orca_hip_mlp* mlp, float* loss, int64_t* correct);
 /* Logits [batch][dims[L]] and predictions [batch] of the last step (synchronises). */
 int orca_hip_mlp_get_logits(orca_hip_mlp* mlp, float* host, size_t n);
 int orca_hip_mlp_get_preds(orca_hip_mlp* mlp, int32_t* host, size_t n);
+/* Forward activations of the last step: layer l < L-1 gives the ReLU output
+ * [batch][dims[l+1]], layer L-1 the logits [batch][dims[L]] (synchronises). */
+int orca_hip_mlp_get_activation(orca_hip_mlp* mlp, size_t layer, float* host, size_t n);
 /* AdamW step counter t. */
 int orca_hip_mlp_get_step_count(const orca_hip_mlp* mlp, int64_t* t);
 

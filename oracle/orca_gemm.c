@@ -101,8 +101,31 @@ __attribute__((target("avx2,fma"))) static int sgemm_avx2(size_t M, size_t N, si
 
 static int sgemm_generic(size_t M, size_t N, size_t K, const float* A, const float* B, float* C) GEMM_BODY
 
+/* Summation-order variant used only to measure how far two valid f32 GEMMs
+ * drive a training run apart: 0 = packed/blocked f32 (default), 1 = each dot
+ * product accumulated in f64 and rounded once. */
+static int g_variant = 0;
+void orc_set_gemm_variant(int v) { g_variant = v; }
+
+static int sgemm_f64acc(size_t M, size_t N, size_t K, const float* A, const float* B, float* C) {
+  double* row = (double*)malloc(sizeof(double) * N);
+  if (!row) return -1;
+  for (size_t i = 0; i < M; ++i) {
+    for (size_t j = 0; j < N; ++j) row[j] = 0.0;
+    for (size_t k = 0; k < K; ++k) {
+      double a = A[i * K + k];
+      const float* b = B + k * N;
+      for (size_t j = 0; j < N; ++j) row[j] += a * (double)b[j];
+    }
+    for (size_t j = 0; j < N; ++j) C[i * N + j] = (float)row[j];
+  }
+  free(row);
+  return 0;
+}
+
 static int sgemm(size_t M, size_t N, size_t K, const float* A, const float* B, float* C) {
   if (M == 0 || N == 0) return 0;
+  if (g_variant == 1) return sgemm_f64acc(M, N, K, A, B, C);
   if (K == 0) {
     memset(C, 0, sizeof(float) * M * N);
     return 0;

@@ -111,7 +111,11 @@ void orc_adamw_update(float* p, const float* g, float* m, float* v, size_t n, co
                       int64_t t);
 void orc_sgd_update(float* p, const float* g, size_t n, const orc_opt* opt);
 
-/* Single-threaded GEMM rate probe used by the CPU baseline report. */
+/* Selects the GEMM summation order (0 = blocked f32, 1 = f64-accumulated
+ * dot products); used to measure the spread between two valid orders. */
+void orc_set_gemm_variant(int variant);
+
+/* Thread count of the OpenMP elementwise ops. */
 int orc_num_threads(void);
 
 #ifdef __cplusplus

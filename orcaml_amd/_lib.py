@@ -140,6 +140,7 @@ SIGNATURES = {
     "orca_hip_mlp_read_metrics": [_P, ctypes.POINTER(_F), ctypes.POINTER(ctypes.c_int64)],
     "orca_hip_mlp_get_logits": [_P, _P, _SZ],
     "orca_hip_mlp_get_preds": [_P, _P, _SZ],
+    "orca_hip_mlp_get_activation": [_P, _SZ, _P, _SZ],
     "orca_hip_mlp_get_step_count": [_P, ctypes.POINTER(ctypes.c_int64)],
     "orca_hip_prof_enable": [_P, _I],
     "orca_hip_prof_reset": [_P],

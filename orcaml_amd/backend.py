@@ -1,0 +1,256 @@
+"""HipBackend: the reference's `Backend` trait (orca-tensor/src/backend.rs:19-315)
+over the C ABI of liborca_hip.so.
+
+A storage is a `HipStorage`: a shared device buffer plus its element count
+and a view flag.  Like the trait's storages it is cheap to clone (buffers are
+reference counted by Python) and every op returns a new storage.  Two ops are
+zero-copy here, as the trait allows (orca-backend-cpu/src/backend.rs:546
+returns a clone for reshape): `reshape`, identity `expand`, and
+`transpose` of the last two dims, which returns a lazy view that `matmul`
+consumes with the transpose folded into its loads (the MatMulBackward
+pattern, orca-autograd/src/backend.rs:1467-1495).  Any other consumer of a
+view materialises it first.  Errors surface as `_lib.OrcaHipError`
+(a ValueError, as orca-python maps OrcaError).
+"""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+
+from . import _lib
+from .device import Buffer, Context
+
+
+class HipStorage:
+    __slots__ = ("buf", "n", "transposed_shape")
+
+    def __init__(self, buf: Buffer, n: int, transposed_shape=None):
+        self.buf = buf
+        self.n = n
+        # Logical shape of a lazy last-two-dims transpose (buffer holds the
+        # untransposed data), or None for contiguous storage.
+        self.transposed_shape = transposed_shape
+
+    def __len__(self) -> int:
+        return self.n
+
+    @property
+    def ptr(self) -> int:
+        return self.buf.ptr
+
+
+def _dims(shape):
+    return _lib.dims(shape)
+
+
+class HipBackend:
+    """Drop-in for `GpuBackend` (orca-backend-gpu/src/backend.rs:45-50)."""
+
+    def __init__(self, ctx: Context | None = None):
+        self.ctx = ctx if ctx is not None else Context(0)
+
+    def __repr__(self) -> str:
+        return f"HipBackend(device=gpu:{self.ctx.device})"
+
+    # ---- helpers ----
+    def _wrap(self, ptr: ctypes.c_void_p, n: int) -> HipStorage:
+        return HipStorage(Buffer(self.ctx, ptr.value, 4 * max(n, 1)), n)
+
+    def _plain(self, s: HipStorage) -> HipStorage:
+        """Materialises a lazy transpose view."""
+        if s.transposed_shape is None:
+            return s
+        shape = list(s.transposed_shape)
+        src_shape = shape[:-2] + [shape[-1], shape[-2]]
+        out = ctypes.c_void_p()
+        d, r = _dims(src_shape)
+        _lib.call("orca_hip_transpose", self.ctx.handle, s.ptr, d, r, r - 2, r - 1, _lib.F32, ctypes.byref(out))
+        return self._wrap(out, s.n)
+
+    def _op1(self, name, s, shape, dtype):
+        s = self._plain(s)
+        out = ctypes.c_void_p()
+        d, r = _dims(shape)
+        _lib.call("orca_hip_" + name, self.ctx.handle, s.ptr, d, r, dtype, ctypes.byref(out))
+        return self._wrap(out, int(np.prod(shape, dtype=np.int64)))
+
+    def _op2(self, name, a, b, shape, dtype):
+        a, b = self._plain(a), self._plain(b)
+        out = ctypes.c_void_p()
+        d, r = _dims(shape)
+        _lib.call("orca_hip_" + name, self.ctx.handle, a.ptr, b.ptr, d, r, dtype, ctypes.byref(out))
+        return self._wrap(out, int(np.prod(shape, dtype=np.int64)))
+
+    def _reshape_like(self, name, s, in_shape, out_shape, dtype):
+        s = self._plain(s)
+        out = ctypes.c_void_p()
+        di, ri = _dims(in_shape)
+        do, ro = _dims(out_shape)
+        _lib.call("orca_hip_" + name, self.ctx.handle, s.ptr, di, ri, do, ro, dtype, ctypes.byref(out))
+        return self._wrap(out, int(np.prod(out_shape, dtype=np.int64)))
+
+    # ---- trait methods (orca-tensor/src/backend.rs) ----
+    def device(self) -> str:
+        return f"gpu:{self.ctx.device}"
+
+    def zeros(self, shape, dtype=_lib.F32):
+        out = ctypes.c_void_p()
+        d, r = _dims(shape)
+        _lib.call("orca_hip_zeros", self.ctx.handle, d, r, dtype, ctypes.byref(out))
+        return self._wrap(out, int(np.prod(shape, dtype=np.int64)))
+
+    def from_f32_slice(self, shape, data):
+        data = np.ascontiguousarray(data, np.float32).reshape(-1)
+        out = ctypes.c_void_p()
+        d, r = _dims(shape)
+        _lib.call("orca_hip_from_f32_slice", self.ctx.handle, d, r, data.ctypes.data_as(ctypes.c_void_p), data.size,
+                  ctypes.byref(out))
+        return self._wrap(out, data.size)
+
+    def to_f32_vec(self, s: HipStorage) -> np.ndarray:
+        s = self._plain(s)
+        out = np.empty(s.n, np.float32)
+        _lib.call("orca_hip_to_f32_vec", self.ctx.handle, s.ptr, s.n, out.ctypes.data_as(ctypes.c_void_p))
+        return out
+
+    def from_bytes(self, shape, data: bytes, dtype=_lib.F32):
+        arr = np.frombuffer(data, np.uint8)
+        out = ctypes.c_void_p()
+        d, r = _dims(shape)
+        _lib.call("orca_hip_from_bytes", self.ctx.handle, d, r, arr.ctypes.data_as(ctypes.c_void_p), arr.size, dtype,
+                  ctypes.byref(out))
+        return self._wrap(out, int(np.prod(shape, dtype=np.int64)))
+
+    def to_bytes(self, s: HipStorage) -> bytes:
+        s = self._plain(s)
+        out = np.empty(4 * s.n, np.uint8)
+        _lib.call("orca_hip_to_bytes", self.ctx.handle, s.ptr, out.size, out.ctypes.data_as(ctypes.c_void_p))
+        return out.tobytes()
+
+    def matmul(self, lhs: HipStorage, rhs: HipStorage, lhs_shape, rhs_shape, dtype=_lib.F32):
+        out = ctypes.c_void_p()
+        dl, rl = _dims(lhs_shape)
+        dr, rr = _dims(rhs_shape)
+        lv = _lib.VIEW_TRANSPOSED if lhs.transposed_shape is not None else _lib.VIEW_CONTIGUOUS
+        rv = _lib.VIEW_TRANSPOSED if rhs.transposed_shape is not None else _lib.VIEW_CONTIGUOUS
+        _lib.call("orca_hip_matmul", self.ctx.handle, lhs.ptr, rhs.ptr, dl, rl, dr, rr, dtype, lv, rv,
+                  ctypes.byref(out))
+        n = int(np.prod(lhs_shape[:-1], dtype=np.int64)) * int(rhs_shape[-1])
+        return self._wrap(out, n)
+
+    def transpose(self, s: HipStorage, shape, dim0: int, dim1: int, dtype=_lib.F32):
+        rank = len(shape)
+        if dim0 >= rank or dim1 >= rank:
+            raise _lib.OrcaHipError(_lib.ERR_INTERNAL, "Invalid transpose dimensions")
+        out_shape = list(shape)
+        out_shape[dim0], out_shape[dim1] = out_shape[dim1], out_shape[dim0]
+        if rank >= 2 and {dim0, dim1} == {rank - 2, rank - 1} and dtype == _lib.F32:
+            if s.transposed_shape is not None:  # transposing a view gives back the buffer's own layout
+                return HipStorage(s.buf, s.n, None)
+            return HipStorage(s.buf, s.n, tuple(out_shape))
+        s = self._plain(s)
+        out = ctypes.c_void_p()
+        d, r = _dims(shape)
+        _lib.call("orca_hip_transpose", self.ctx.handle, s.ptr, d, r, dim0, dim1, dtype, ctypes.byref(out))
+        return self._wrap(out, s.n)
+
+    def add(self, a, b, shape, dtype=_lib.F32):
+        return self._op2("add", a, b, shape, dtype)
+
+    def sub(self, a, b, shape, dtype=_lib.F32):
+        return self._op2("sub", a, b, shape, dtype)
+
+    def mul(self, a, b, shape, dtype=_lib.F32):
+        return self._op2("mul", a, b, shape, dtype)
+
+    def div(self, a, b, shape, dtype=_lib.F32):
+        return self._op2("div", a, b, shape, dtype)
+
+    def mul_scalar(self, s, scalar: float, shape, dtype=_lib.F32):
+        s = self._plain(s)
+        out = ctypes.c_void_p()
+        d, r = _dims(shape)
+        _lib.call("orca_hip_mul_scalar", self.ctx.handle, s.ptr, ctypes.c_float(scalar), d, r, dtype,
+                  ctypes.byref(out))
+        return self._wrap(out, int(np.prod(shape, dtype=np.int64)))
+
+    def relu(self, s, shape, dtype=_lib.F32):
+        return self._op1("relu", s, shape, dtype)
+
+    def sigmoid(self, s, shape, dtype=_lib.F32):
+        return self._op1("sigmoid", s, shape, dtype)
+
+    def exp(self, s, shape, dtype=_lib.F32):
+        return self._op1("exp", s, shape, dtype)
+
+    def log(self, s, shape, dtype=_lib.F32):
+        return self._op1("log", s, shape, dtype)
+
+    def sqrt(self, s, shape, dtype=_lib.F32):
+        return self._op1("sqrt", s, shape, dtype)
+
+    def relu_backward(self, g, x, shape, dtype=_lib.F32):
+        return self._op2("relu_backward", g, x, shape, dtype)
+
+    def sigmoid_backward(self, g, y, shape, dtype=_lib.F32):
+        return self._op2("sigmoid_backward", g, y, shape, dtype)
+
+    def exp_backward(self, g, y, shape, dtype=_lib.F32):
+        return self._op2("exp_backward", g, y, shape, dtype)
+
+    def log_backward(self, g, x, shape, dtype=_lib.F32):
+        return self._op2("log_backward", g, x, shape, dtype)
+
+    def sqrt_backward(self, g, y, shape, dtype=_lib.F32):
+        return self._op2("sqrt_backward", g, y, shape, dtype)
+
+    def div_backward_lhs(self, g, r, shape, dtype=_lib.F32):
+        return self._op2("div_backward_lhs", g, r, shape, dtype)
+
+    def div_backward_rhs(self, g, l, r, shape, dtype=_lib.F32):
+        g, l, r = self._plain(g), self._plain(l), self._plain(r)
+        out = ctypes.c_void_p()
+        d, rk = _dims(shape)
+        _lib.call("orca_hip_div_backward_rhs", self.ctx.handle, g.ptr, l.ptr, r.ptr, d, rk, dtype, ctypes.byref(out))
+        return self._wrap(out, int(np.prod(shape, dtype=np.int64)))
+
+    def accumulate_grad(self, a, b):
+        a, b = self._plain(a), self._plain(b)
+        out = ctypes.c_void_p()
+        _lib.call("orca_hip_accumulate_grad", self.ctx.handle, a.ptr, b.ptr, a.n, ctypes.byref(out))
+        return self._wrap(out, a.n)
+
+    def expand(self, s, in_shape, out_shape, dtype=_lib.F32):
+        if tuple(in_shape) == tuple(out_shape) and dtype == _lib.F32:
+            return s  # identity broadcast: share the storage
+        return self._reshape_like("expand", s, in_shape, out_shape, dtype)
+
+    def sum_to_shape(self, s, in_shape, out_shape, dtype=_lib.F32):
+        return self._reshape_like("sum_to_shape", s, in_shape, out_shape, dtype)
+
+    def reshape(self, s, in_shape, out_shape, dtype=_lib.F32):
+        n_in = int(np.prod(in_shape, dtype=np.int64))
+        n_out = int(np.prod(out_shape, dtype=np.int64))
+        if n_in != n_out:
+            raise _lib.OrcaHipError(_lib.ERR_SHAPE, f"Shape mismatch during reshape: expected {n_in} elements, "
+                                                    f"got {n_out} elements")
+        return self._plain(s)
+
+    def max_to_shape(self, s, in_shape, out_shape, dtype=_lib.F32):
+        return self._reshape_like("max_to_shape", s, in_shape, out_shape, dtype)
+
+    def max_to_shape_backward(self, g, x, y, in_shape, out_shape, dtype=_lib.F32):
+        g, x, y = self._plain(g), self._plain(x), self._plain(y)
+        out = ctypes.c_void_p()
+        di, ri = _dims(in_shape)
+        do, ro = _dims(out_shape)
+        _lib.call("orca_hip_max_to_shape_backward", self.ctx.handle, g.ptr, x.ptr, y.ptr, di, ri, do, ro, dtype,
+                  ctypes.byref(out))
+        return self._wrap(out, int(np.prod(in_shape, dtype=np.int64)))
+
+    def has_nan_or_inf(self, s, dtype=_lib.F32) -> bool:
+        s = self._plain(s)
+        res = ctypes.c_int()
+        _lib.call("orca_hip_has_nan_or_inf", self.ctx.handle, s.ptr, s.n, dtype, ctypes.byref(res))
+        return bool(res.value)

@@ -48,7 +48,7 @@ struct GemmParams {
   const float* bias;
   const float* mask;
   int64_t ldmask;
-  float* colsum;
+  float* colsum;  // [splits][N]
   int vec_a, vec_b;
 };
 
@@ -197,7 +197,8 @@ __global__ void __launch_bounds__(NTHREADS) gemm_mfma_f32_kernel(GemmParams p) {
     __syncthreads();
   }
 
-  if (do_colsum && tid < BN && n0 + tid < p.N) p.colsum[n0 + tid] = cs;
+  // One partial per K-chunk when K is split (reduced in chunk order on the host side).
+  if (do_colsum && tid < BN && n0 + tid < p.N) p.colsum[(int64_t)split * p.N + n0 + tid] = cs;
 
   // Epilogue.  Lane (h, i), register r of block (mt, nt) holds
   // C[wm*64 + mt*32 + (r/4)*8 + h*4 + r%4][wn*64 + nt*32 + i].
@@ -262,6 +263,15 @@ __global__ void splitk_reduce_kernel(SplitReduceParams p, size_t total) {
     }
     p.C[b * p.sc + (int64_t)row * p.ldc + col] = v;
   }
+}
+
+// colsum[n] = sum over K-chunks, in chunk order, of the per-chunk column sums.
+__global__ void colsum_split_reduce_kernel(const float* __restrict__ part, int splits, int N, float* __restrict__ out) {
+  int n = blockIdx.x * blockDim.x + threadIdx.x;
+  if (n >= N) return;
+  float v = part[n];
+  for (int s = 1; s < splits; ++s) v = v + part[(int64_t)s * N + n];
+  out[n] = v;
 }
 
 inline bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; }
@@ -332,7 +342,14 @@ void gemm(orca_hip_ctx* ctx, bool trans_a, bool trans_b, size_t M, size_t N, siz
   p.bias = epi.bias;
   p.mask = epi.mask;
   p.ldmask = (int64_t)epi.ldmask;
-  p.colsum = splits == 1 && batch == 1 && !trans_b ? epi.colsum : nullptr;
+  const bool fold_colsum = epi.colsum != nullptr && batch == 1 && !trans_b;
+  std::unique_ptr<Scratch> colsum_ws;
+  if (fold_colsum && splits > 1) {
+    colsum_ws.reset(new Scratch(ctx, sizeof(float) * splits * N));
+    p.colsum = colsum_ws->as<float>();
+  } else {
+    p.colsum = fold_colsum ? epi.colsum : nullptr;
+  }
   p.vec_a = aligned16(A) && lda % 4 == 0 && (batch == 1 || sa % 4 == 0);
   p.vec_b = aligned16(B) && ldb % 4 == 0 && (batch == 1 || sb % 4 == 0);
 
@@ -377,8 +394,13 @@ void gemm(orca_hip_ctx* ctx, bool trans_a, bool trans_b, size_t M, size_t N, siz
     hipLaunchKernelGGL(splitk_reduce_kernel, dim3(g), dim3(256), 0, ctx->stream, r, total);
     ORCA_HIP_CHECK(hipGetLastError());
   }
-  // Column sums that the GEMM could not fold in (split K, batched, or B^T storage).
-  if (epi.colsum && !p.colsum) {
+  if (fold_colsum && splits > 1) {
+    hipLaunchKernelGGL(colsum_split_reduce_kernel, dim3((unsigned)((N + 255) / 256)), dim3(256), 0, ctx->stream,
+                       p.colsum, splits, (int)N, epi.colsum);
+    ORCA_HIP_CHECK(hipGetLastError());
+  }
+  // Column sums that the GEMM could not fold in (batched, or B^T storage).
+  if (epi.colsum && !fold_colsum) {
     if (batch != 1) fail(ORCA_HIP_ERR_INTERNAL, "gemm colsum epilogue requires batch == 1");
     if (trans_b) fail(ORCA_HIP_ERR_INTERNAL, "gemm colsum epilogue requires row-major B");
     launch_colsum(ctx, B, K, N, ldb, epi.colsum);

@@ -299,6 +299,18 @@ int orca_hip_mlp_get_preds(orca_hip_mlp* mlp, int32_t* host, size_t n) {
   });
 }
 
+int orca_hip_mlp_get_activation(orca_hip_mlp* mlp, size_t layer, float* host, size_t n) {
+  return guard([&] {
+    checked(mlp);
+    if (layer >= mlp->L) fail(ORCA_HIP_ERR_INTERNAL, "layer index out of range");
+    size_t want = mlp->B * mlp->dims[layer + 1];
+    if (n != want) fail(ORCA_HIP_ERR_SHAPE, "Shape mismatch during mlp_get_activation: expected " + std::to_string(want));
+    const float* src = layer + 1 < mlp->L ? mlp->H[layer] : mlp->logits;
+    ORCA_HIP_CHECK(hipMemcpyAsync(host, src, n * sizeof(float), hipMemcpyDeviceToHost, mlp->ctx->stream));
+    ORCA_HIP_CHECK(hipStreamSynchronize(mlp->ctx->stream));
+  });
+}
+
 int orca_hip_mlp_get_step_count(const orca_hip_mlp* mlp, int64_t* t) {
   return guard([&] {
     if (!mlp || !t) fail(ORCA_HIP_ERR_INTERNAL, "null argument");

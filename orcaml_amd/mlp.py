@@ -102,6 +102,12 @@ class MLPTrainer:
         _lib.call("orca_hip_mlp_get_preds", self.handle, out.ctypes.data_as(ctypes.c_void_p), out.size)
         return out
 
+    def activation(self, layer: int) -> np.ndarray:
+        """ReLU output of layer `layer` (< L-1) or the logits (layer L-1) of the last step."""
+        out = np.empty((self.batch, self.dims[layer + 1]), np.float32)
+        _lib.call("orca_hip_mlp_get_activation", self.handle, layer, out.ctypes.data_as(ctypes.c_void_p), out.size)
+        return out
+
     def step_count(self) -> int:
         t = ctypes.c_int64()
         _lib.call("orca_hip_mlp_get_step_count", self.handle, ctypes.byref(t))

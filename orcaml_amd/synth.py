@@ -53,13 +53,16 @@ def integers(seed: int, tensor_id: int, n: int, k: int) -> np.ndarray:
     return (stream(seed, tensor_id, n) % np.uint64(k)).astype(np.int32)
 
 
-def normal(seed: int, tensor_id: int, shape, mu: float = 0.0, sigma: float = 1.0) -> np.ndarray:
-    n = int(np.prod(shape))
-    out = np.empty(n, np.float32)
-    pairs = (n + 1) // 2
+def normal_range(seed: int, tensor_id: int, offset: int, count: int, mu: float = 0.0,
+                 sigma: float = 1.0) -> np.ndarray:
+    """Elements offset .. offset+count-1 of the flat normal stream (offset even)."""
+    if offset % 2:
+        raise ValueError("offset must be even (elements come in Box-Muller pairs)")
+    out = np.empty(count, np.float32)
+    pairs = (count + 1) // 2
     for p0 in range(0, pairs, _CHUNK):
         np_ = min(_CHUNK, pairs - p0)
-        raw = stream(seed, tensor_id, 2 * np_, offset=2 * p0)
+        raw = stream(seed, tensor_id, 2 * np_, offset=offset + 2 * p0)
         a, b = raw[0::2], raw[1::2]
         u1 = ((a >> np.uint64(11)).astype(np.float64) + 1.0) * 2.0 ** -53
         u2 = (b >> np.uint64(11)).astype(np.float64) * 2.0 ** -53
@@ -69,9 +72,13 @@ def normal(seed: int, tensor_id: int, shape, mu: float = 0.0, sigma: float = 1.0
         vals[0::2] = r * np.cos(th)
         vals[1::2] = r * np.sin(th)
         lo = 2 * p0
-        hi = min(n, lo + 2 * np_)
+        hi = min(count, lo + 2 * np_)
         out[lo:hi] = (mu + sigma * vals[: hi - lo]).astype(np.float32)
-    return out.reshape(shape)
+    return out
+
+
+def normal(seed: int, tensor_id: int, shape, mu: float = 0.0, sigma: float = 1.0) -> np.ndarray:
+    return normal_range(seed, tensor_id, 0, int(np.prod(shape)), mu, sigma).reshape(shape)
 
 
 def kaiming_weight(seed: int, tensor_id: int, fan_in: int, fan_out: int) -> np.ndarray:

@@ -1,0 +1,108 @@
+"""TEST INFRASTRUCTURE: the CPU oracle (orca-backend-cpu restated in C) behind
+the same method names as the `Backend` trait, so the tape in
+orcaml_amd.autodiff can run on it.  Storages are flat float32 numpy arrays."""
+from __future__ import annotations
+
+import numpy as np
+
+from oracle import oracle as O
+
+
+def _n(shape) -> int:
+    return int(np.prod(shape, dtype=np.int64))
+
+
+class OracleBackend:
+    def device(self) -> str:
+        return "cpu"
+
+    def zeros(self, shape, dtype=0):
+        return np.zeros(_n(shape), np.float32)
+
+    def from_f32_slice(self, shape, data):
+        a = np.array(data, np.float32).reshape(-1)
+        assert a.size == _n(shape)
+        return a
+
+    def to_f32_vec(self, s):
+        return np.array(s, np.float32)
+
+    def matmul(self, a, b, a_shape, b_shape, dtype=0):
+        return O.matmul(a.reshape(a_shape), b.reshape(b_shape)).reshape(-1)
+
+    def transpose(self, s, shape, d0, d1, dtype=0):
+        return O.transpose(s.reshape(shape), d0, d1).reshape(-1)
+
+    def add(self, a, b, shape, dtype=0):
+        return O.add(a, b)
+
+    def sub(self, a, b, shape, dtype=0):
+        return O.sub(a, b)
+
+    def mul(self, a, b, shape, dtype=0):
+        return O.mul(a, b)
+
+    def div(self, a, b, shape, dtype=0):
+        return O.div(a, b)
+
+    def mul_scalar(self, s, scalar, shape, dtype=0):
+        return O.mul_scalar(s, scalar)
+
+    def relu(self, s, shape, dtype=0):
+        return O.relu(s)
+
+    def sigmoid(self, s, shape, dtype=0):
+        return O.sigmoid(s)
+
+    def exp(self, s, shape, dtype=0):
+        return O.exp(s)
+
+    def log(self, s, shape, dtype=0):
+        return O.log(s)
+
+    def sqrt(self, s, shape, dtype=0):
+        return O.sqrt(s)
+
+    def relu_backward(self, g, x, shape, dtype=0):
+        return O.relu_backward(g, x)
+
+    def sigmoid_backward(self, g, y, shape, dtype=0):
+        return O.sigmoid_backward(g, y)
+
+    def exp_backward(self, g, y, shape, dtype=0):
+        return O.exp_backward(g, y)
+
+    def log_backward(self, g, x, shape, dtype=0):
+        return O.log_backward(g, x)
+
+    def sqrt_backward(self, g, y, shape, dtype=0):
+        return O.sqrt_backward(g, y)
+
+    def div_backward_lhs(self, g, r, shape, dtype=0):
+        return O.div_backward_lhs(g, r)
+
+    def div_backward_rhs(self, g, l, r, shape, dtype=0):
+        return O.div_backward_rhs(g, l, r)
+
+    def accumulate_grad(self, a, b):
+        return O.accumulate_grad(a, b)
+
+    def expand(self, s, in_shape, out_shape, dtype=0):
+        return O.expand(s.reshape(in_shape), tuple(out_shape)).reshape(-1)
+
+    def sum_to_shape(self, s, in_shape, out_shape, dtype=0):
+        return O.sum_to_shape(s.reshape(in_shape), tuple(out_shape)).reshape(-1)
+
+    def reshape(self, s, in_shape, out_shape, dtype=0):
+        if _n(in_shape) != _n(out_shape):
+            raise ValueError("Shape mismatch during reshape")
+        return s
+
+    def max_to_shape(self, s, in_shape, out_shape, dtype=0):
+        return O.max_to_shape(s.reshape(in_shape), tuple(out_shape)).reshape(-1)
+
+    def max_to_shape_backward(self, g, x, y, in_shape, out_shape, dtype=0):
+        return O.max_to_shape_backward(g.reshape(out_shape), x.reshape(in_shape), y.reshape(out_shape)).reshape(-1)
+
+    def has_nan_or_inf(self, s, dtype=0):
+        return O.has_nan_or_inf(s)

@@ -86,15 +86,23 @@ def test_gemm_epilogues_match_composed_ops(ctx):
     np.testing.assert_array_equal(got, O.relu_backward(prod, mask))
 
 
-@pytest.mark.parametrize("M,N,K", [(128, 256, 64), (784, 4096, 1024), (4096, 10, 1024), (33, 70, 5)])
-def test_gemm_colsum_is_bias_gradient(ctx, M, N, K):
-    """dW = X^T dY with the bias column sum fused: the column sum must equal
-    sum_to_shape(dY, [1, N]) exactly (same ascending row order)."""
+@pytest.mark.parametrize("M,N,K,exact", [(128, 256, 64, True), (784, 4096, 1024, True), (4096, 10, 1024, False),
+                                         (33, 70, 5, True)])
+def test_gemm_colsum_is_bias_gradient(ctx, M, N, K, exact):
+    """dW = X^T dY with the bias column sum fused.  With one K-chunk per tile
+    the column sum equals sum_to_shape(dY, [1, N]) bit for bit (same ascending
+    row order); a split-K launch (skinny N) sums per-chunk partials in chunk
+    order, so it matches to f32 rounding."""
     rng = np.random.default_rng(M + N + K)
     X = rng.standard_normal((K, M)).astype(np.float32)  # stored [B][in]
     dY = rng.standard_normal((K, N)).astype(np.float32)
     dW, cs = run_gemm(ctx, True, False, X, dY, colsum=True)
-    np.testing.assert_array_equal(cs, O.sum_to_shape(dY, (1, N)).reshape(N))
+    want = O.sum_to_shape(dY, (1, N)).reshape(N)
+    if exact:
+        np.testing.assert_array_equal(cs, want)
+    else:
+        bound = K * 2.0 ** -24 * np.abs(dY.astype(np.float64)).sum(0)
+        assert (np.abs(cs.astype(np.float64) - want) <= bound).all()
     assert_gemm_error_bound(dW, X.T, dY)
 
 

@@ -1,0 +1,282 @@
+"""Full-size workloads of the MLP hot path on the GPU against the CPU oracle:
+100 AdamW steps at H=1024 / B=256, one AdamW step of the 784-4096-4096-10 MLP
+at B=1024, the fused backward epilogue on [8192, 4096], and AdamW over 2^28
+parameters."""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from orcaml_amd import _lib, synth
+from orcaml_amd.mlp import MLPTrainer
+from tests.util import assert_close, assert_close_scaled, outside_tolerance
+
+pytestmark = pytest.mark.gpu
+
+
+def make_trainer(ctx, w, params):
+    o = w["opt"]
+    tr = MLPTrainer(ctx, w["dims"], w["batch"], kind=o["kind"], lr=o["lr"], weight_decay=o.get("weight_decay", 0.0),
+                    betas=o.get("betas", (0.9, 0.999)), eps=o.get("eps", 1e-8))
+    tr.set_params(params)
+    return tr
+
+
+def ref_opt(w):
+    o = w["opt"]
+    return O.make_opt(o["kind"], o["lr"], o.get("weight_decay", 0.0), o.get("betas", (0.9, 0.999)), o.get("eps", 1e-8))
+
+
+def near_tie_rows(logits_ref: np.ndarray, tol: float) -> np.ndarray:
+    """Rows whose top-2 margin is within rounding: their argmax may
+    legitimately differ when the logits come from differently-rounded GEMMs."""
+    s = np.sort(logits_ref, axis=1)
+    return (s[:, -1] - s[:, -2]) <= tol * np.maximum(1.0, np.abs(s[:, -1]))
+
+
+def test_config2_hundred_adamw_steps_teacher_forced(ctx):
+    """784-1024-1024-10, batch 256, 100 AdamW(1e-3, wd 0.01) steps on one fixed
+    batch.  At every step the oracle takes one step from the GPU's own state
+    (parameters, moments, t) and the step's loss, the new parameters and both
+    moments must agree to the path's tolerance (1e-5 abs + 1e-4 rel) -- the
+    same per-step agreement two valid CPU GEMM orders reach (zero outliers)."""
+    w = synth.WORKLOADS[2]
+    params, x, labels, onehot = synth.mlp_problem(2, w["dims"], w["batch"])
+    tr = make_trainer(ctx, w, params)
+    tr.set_batch(x, onehot=onehot)
+    state = dict(params=params, m=None, v=None, t=0)
+    for step in range(w["steps"]):
+        tr.step()
+        loss, _ = tr.metrics()
+        ref = O.mlp_train(w["dims"], state["params"], x, onehot, ref_opt(w), steps=1, m=state["m"], v=state["v"],
+                          t=state["t"], want_grads=False)
+        assert_close(loss, ref["losses"][0], what=f"step {step} loss")
+        got_p, got_m, got_v = tr.params(), tr.moments(0), tr.moments(1)
+        for i in range(len(got_p)):
+            assert_close(got_p[i], ref["params"][i], what=f"step {step} param {i}")
+            assert_close(got_m[i], ref["m"][i], what=f"step {step} m {i}")
+            assert_close(got_v[i], ref["v"][i], what=f"step {step} v {i}")
+        state = dict(params=got_p, m=got_m, v=got_v, t=ref["t"])
+    assert tr.step_count() == state["t"] == 100
+
+
+def test_config2_free_running_within_natural_spread(ctx):
+    """Free-running, 100 AdamW steps amplify rounding (near-zero gradients get
+    +-lr updates while t is small): two valid CPU GEMM orders (blocked f32 and
+    f64-accumulated) already differ by up to ~2.5% in the per-step loss.  The
+    GPU trajectory must stay within 4x that measured spread of the oracle's."""
+    w = synth.WORKLOADS[2]
+    params, x, labels, onehot = synth.mlp_problem(2, w["dims"], w["batch"])
+    tr = make_trainer(ctx, w, params)
+    tr.set_batch(x, onehot=onehot)
+    losses = []
+    for _ in range(w["steps"]):
+        tr.step()
+        losses.append(tr.metrics()[0])
+    gpu = np.array(losses, np.float64)
+    a = O.mlp_train(w["dims"], params, x, onehot, ref_opt(w), steps=w["steps"], want_grads=False)
+    O.lib().orc_set_gemm_variant(1)
+    try:
+        b = O.mlp_train(w["dims"], params, x, onehot, ref_opt(w), steps=w["steps"], want_grads=False)
+    finally:
+        O.lib().orc_set_gemm_variant(0)
+    ref = a["losses"].astype(np.float64)
+    spread = np.maximum.accumulate(np.abs(ref - b["losses"]) / ref)
+    dev = np.abs(gpu - ref) / ref
+    print(f"config2 free-running: max GPU deviation {dev.max():.2e}, max oracle spread {spread.max():.2e}, "
+          f"final loss gpu {gpu[-1]:.6f} oracle {ref[-1]:.6f}")
+    assert np.isfinite(gpu).all()
+    assert (dev[:3] <= 1e-4).all()  # identical until rounding differences can act
+    assert (dev <= 4 * spread + 1e-4).all()
+    assert gpu[-1] < 0.05 * gpu[0]  # the fixed batch is memorised
+
+
+def test_config3_one_adamw_step(ctx):
+    """784-4096-4096-10, batch 1024, one AdamW step against the oracle, end to end:
+    loss and logits to the path's tolerance (1e-5 abs + 1e-4 rel); gradients and
+    updated parameters to that tolerance except for a reported fraction <= 1e-5
+    of elements.  Those outliers come from ReLU masks that differ between the
+    two forward passes (pre-activations within rounding of zero: a flipped
+    dZ[b, j] moves a whole column of dW by H[b, :] * dZ[b, j]); the flip count is
+    printed, and the shared-input layer-wise test below shows the kernels agree
+    when the masks are the same.  Argmax / accuracy are exact outside rows whose
+    top-2 margin is within rounding."""
+    w = synth.WORKLOADS[3]
+    dims = w["dims"]
+    params, x, labels, onehot = synth.mlp_problem(3, dims, w["batch"])
+    tr = make_trainer(ctx, w, params)
+    tr.set_batch(x, onehot=onehot)
+    tr.step()
+    loss, correct = tr.metrics()
+    ref = O.mlp_train(dims, params, x, onehot, ref_opt(w), steps=1)
+    assert_close(loss, ref["losses"][0], what="loss")
+    assert_close(tr.logits(), ref["logits"], what="logits")
+    B = w["batch"]
+    h1 = O.relu(O.add(O.matmul(x, params[0]), O.expand(params[1], (B, dims[1]))))
+    h2 = O.relu(O.add(O.matmul(h1, params[2]), O.expand(params[3], (B, dims[2]))))
+    # ReLU outputs of the oracle's own forward pass; the last layer has no mask.
+    flips = [int(((h1 > 0) != (tr.activation(0) > 0)).sum()), int(((h2 > 0) != (tr.activation(1) > 0)).sum()), 0]
+    report, over = [], []
+    grads = tr.grads()
+    for kind, got_all, ref_all in (("grad", grads, ref["grads"]), ("param", tr.params(), ref["params"])):
+        for i, (g, r) in enumerate(zip(got_all, ref_all)):
+            bad = np.abs(g.astype(np.float64) - r) > 1e-5 + 1e-4 * np.abs(r.astype(np.float64))
+            n_out = int(bad.sum())
+            if kind == "param":
+                # AdamW's first update is lr * u(g) with u(g) = g / (|g| + eps): a
+                # normalisation that turns gradient differences well inside the tolerance
+                # (mask flips upstream perturb all of dW1 by ~1e-8, and near-zero entries
+                # can change sign) into parameter differences of up to 2 lr wherever |g| is
+                # within a few orders of eps.  Such an element is explained when the
+                # closed form alone, fed the two gradients, predicts a difference of at
+                # least half the tolerance; the AdamW kernel itself is bit-exact.
+                gg, gr = grads[i].astype(np.float64), ref["grads"][i].astype(np.float64)
+                lr, eps = w["opt"]["lr"], w["opt"]["eps"]
+                predicted = lr * np.abs(gg / (np.abs(gg) + eps) - gr / (np.abs(gr) + eps))
+                amplified = predicted >= 0.5 * (1e-5 + 1e-4 * np.abs(r.astype(np.float64)))
+                report.append(f"param{i}-from-grad:{int((bad & amplified).sum())}")
+                bad = bad & ~amplified
+                n_out = int(bad.sum())
+            # A flip at (b, j) of layer l's mask changes dZ_l[b, j]: column j of dW_l
+            # (dims[l] entries) and entry j of db_l.
+            l = i // 2
+            allowed = int(np.ceil(1e-5 * g.size)) + flips[l] * (dims[l] if i % 2 == 0 else 1)
+            report.append(f"{kind}{i}:{n_out}/{allowed}")
+            if n_out > allowed:
+                over.append(f"{kind} {i}: {n_out} of {g.size} outside tolerance (allowed {allowed})")
+    print(f"config3 end-to-end: ReLU mask flips layer1 {flips[0]}, layer2 {flips[1]}; "
+          f"elements outside 1e-5+1e-4|x| / allowed: {' '.join(report)}")
+    assert not over, over
+    for i, (gg, gr) in enumerate(zip(grads, ref["grads"])):  # sign noise itself is rare
+        assert (np.sign(gg) != np.sign(gr)).mean() <= 2e-3, f"grad {i}: too many sign disagreements"
+    ties = near_tie_rows(ref["logits"], 1e-5)
+    preds = tr.preds()
+    np.testing.assert_array_equal(preds[~ties], ref["preds"][~ties])
+    assert abs(correct - ref["correct"]) <= int(ties.sum())
+
+
+def test_config3_layerwise_on_shared_inputs(ctx):
+    """Each layer of the fused step against the oracle's ops fed the GPU's own
+    inputs to that layer (so ReLU masks are identical): forward activations,
+    the CE gradient, every dZ-driven gradient -- tight, scale-relative
+    tolerance.  End-to-end ReLU mask flips (pre-activations within rounding of
+    zero) are counted and must be rare."""
+    w = synth.WORKLOADS[3]
+    dims = w["dims"]
+    params, x, labels, onehot = synth.mlp_problem(3, dims, w["batch"])
+    tr = make_trainer(ctx, w, params)
+    tr.set_batch(x, onehot=onehot)
+    tr.step()
+    W = [params[0], params[2], params[4]]
+    b = [params[1], params[3], params[5]]
+    H1, H2, logits = tr.activation(0), tr.activation(1), tr.activation(2)
+    grads = tr.grads()
+    B = w["batch"]
+
+    def lin(a, l):
+        return O.add(O.matmul(a, W[l]), O.expand(b[l], (B, dims[l + 1])))
+
+    # forward, layer by layer from the GPU's own input to that layer
+    for name, got, want in (("H1", H1, O.relu(lin(x, 0))), ("H2", H2, O.relu(lin(H1, 1))),
+                            ("logits", logits, lin(H2, 2))):
+        assert_close_scaled(got, want, rtol=1e-5, what=name)
+    flips = [int(((O.relu(lin(x, 0)) > 0) != (H1 > 0)).sum()), int(((O.relu(lin(H1, 1)) > 0) != (H2 > 0)).sum())]
+    print(f"config3 ReLU mask flips vs the oracle's own pre-activations: layer1 {flips[0]}, layer2 {flips[1]} "
+          f"of {H1.size} each")
+    assert max(flips) <= 1e-5 * H1.size
+    # backward from the GPU's logits and activations
+    _, dlog = O.cross_entropy(logits, onehot)
+    dZ2 = O.relu_backward(O.matmul(dlog, O.transpose(W[2], 0, 1)), H2)
+    dZ1 = O.relu_backward(O.matmul(dZ2, O.transpose(W[1], 0, 1)), H1)
+    want = [O.matmul(O.transpose(x, 0, 1), dZ1), O.sum_to_shape(dZ1, (1, dims[1])),
+            O.matmul(O.transpose(H1, 0, 1), dZ2), O.sum_to_shape(dZ2, (1, dims[2])),
+            O.matmul(O.transpose(H2, 0, 1), dlog), O.sum_to_shape(dlog, (1, dims[3]))]
+    for i, (g, r) in enumerate(zip(grads, want)):
+        assert_close_scaled(g, r, rtol=1e-4, what=f"grad {i}")
+
+
+def test_config4_fused_backward_epilogue(ctx):
+    """Logits [8192, 4096] ~ N(0, 2^2) with int targets -> softmax-CE gradient;
+    then ReLU-mask backward on a N(0,1) pre-activation and the bias column sum."""
+    B, C = 8192, 4096
+    logits = synth.normal(4, 1, (B, C), 0.0, 2.0)
+    labels = synth.integers(4, 2, B, C)
+    pre = synth.normal(4, 3, (B, C))
+    dl, dlab, dpre_in = ctx.upload(logits), ctx.upload(labels), ctx.upload(pre)
+    loss, grad = ctx.alloc(4), ctx.alloc(4 * B * C)
+    _lib.call("orca_hip_softmax_ce", ctx.handle, dl.ptr, B, C, None, dlab.ptr, loss.ptr, grad.ptr, None, None)
+    dpre, colsum = ctx.alloc(4 * B * C), ctx.alloc(4 * C)
+    _lib.call("orca_hip_relu_bw_colsum", ctx.handle, grad.ptr, dpre_in.ptr, B, C, dpre.ptr, colsum.ptr)
+    g_gpu = grad.download(count=B * C).reshape(B, C)
+    d_gpu = dpre.download(count=B * C).reshape(B, C)
+    cs_gpu = colsum.download(count=C)
+
+    loss_ref, g_ref = O.cross_entropy(logits, synth.one_hot(labels, C))
+    assert_close(float(loss.download(count=1)[0]), loss_ref, what="loss")
+    assert_close(g_gpu, g_ref, what="CE grad")
+    assert_close_scaled(g_gpu, g_ref, what="CE grad (scaled)")
+    # ReLU mask on identical inputs is exact: apply it to the GPU's own gradient.
+    d_ref = O.relu_backward(g_gpu, pre)
+    np.testing.assert_array_equal(d_gpu, d_ref)
+    assert ((d_gpu != 0) <= (pre > 0)).all()
+    cs_ref = O.sum_to_shape(d_ref, (1, C)).reshape(C)
+    assert_close(cs_gpu, cs_ref, what="bias colsum")
+    # Each CE-gradient row sums to ~0 (softmax - onehot); column sums of the masked gradient are the bias grad.
+    np.testing.assert_allclose(g_gpu.astype(np.float64).sum(1), 0.0, atol=1e-9)
+
+
+@pytest.mark.timeout(600)
+def test_config5_adamw_2pow28(ctx):
+    """AdamW over one flat buffer of 2^28 f32 params, 10 steps from zero moments:
+    bit-exact against the oracle on a sample of 2^20 positions (the update is
+    elementwise), and finite everywhere."""
+    n = 1 << 28
+    chunk = 1 << 24
+    p_dev, g_dev = ctx.alloc(4 * n), ctx.alloc(4 * n)
+    m_dev, v_dev = ctx.alloc(4 * n), ctx.alloc(4 * n)
+    _lib.call("orca_hip_fill", ctx.handle, m_dev.ptr, ctypes.c_float(0.0), n)
+    _lib.call("orca_hip_fill", ctx.handle, v_dev.ptr, ctypes.c_float(0.0), n)
+    rng = np.random.default_rng(5)
+    idx = np.sort(rng.choice(n, size=1 << 20, replace=False))
+    p_s = np.empty(idx.size, np.float32)
+    g_s = np.empty(idx.size, np.float32)
+    for off in range(0, n, chunk):
+        pc = synth.normal_range(5, 1, off, chunk, 0.0, 0.02)
+        gc = synth.normal_range(5, 2, off, chunk, 0.0, 1e-3)
+        _upload_at(ctx, p_dev, off, pc)
+        _upload_at(ctx, g_dev, off, gc)
+        sel = (idx >= off) & (idx < off + chunk)
+        p_s[sel] = pc[idx[sel] - off]
+        g_s[sel] = gc[idx[sel] - off]
+    for t in range(1, 11):
+        _lib.call("orca_hip_adamw_step", ctx.handle, p_dev.ptr, g_dev.ptr, m_dev.ptr, v_dev.ptr, n, 1e-3, 0.9, 0.999,
+                  1e-8, 0.01, t)
+    ctx.sync()
+    ref_p, ref_m, ref_v = p_s, np.zeros_like(p_s), np.zeros_like(p_s)
+    for t in range(1, 11):
+        ref_p, ref_m, ref_v = O.adamw_update(ref_p, g_s, ref_m, ref_v, t)
+    got_p = _gather(ctx, p_dev, idx, n)
+    got_m = _gather(ctx, m_dev, idx, n)
+    np.testing.assert_array_equal(got_p, ref_p)
+    np.testing.assert_array_equal(got_m, ref_m)
+    assert np.isfinite(got_p).all()
+
+
+def _upload_at(ctx, buf, off, arr):
+    arr = np.ascontiguousarray(arr, np.float32)
+    _lib.call("orca_hip_h2d", ctx.handle, buf.ptr + 4 * off, arr.ctypes.data_as(ctypes.c_void_p), arr.nbytes)
+
+
+def _gather(ctx, buf, idx, n, chunk=1 << 24):
+    out = np.empty(idx.size, np.float32)
+    host = np.empty(chunk, np.float32)
+    for off in range(0, n, chunk):
+        sel = (idx >= off) & (idx < off + chunk)
+        if not sel.any():
+            continue
+        _lib.call("orca_hip_d2h", ctx.handle, host.ctypes.data_as(ctypes.c_void_p), buf.ptr + 4 * off, 4 * chunk)
+        out[sel] = host[idx[sel] - off]
+    return out

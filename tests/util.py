@@ -28,7 +28,13 @@ def assert_close_scaled(got, want, rtol: float = RTOL, what: str = "") -> None:
     scaled to the tensor's largest magnitude."""
     want = np.asarray(want, np.float64)
     scale = float(np.max(np.abs(want))) if want.size else 0.0
-    assert_close(got, want, rtol=rtol, atol=rtol * scale * 1e-2 + 1e-30, what=what)
+    assert_close(got, want, rtol=rtol, atol=rtol * scale + 1e-30, what=what)
+
+
+def outside_tolerance(got, want, rtol: float = RTOL, atol: float = ATOL) -> int:
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    return int((np.abs(got - want) > atol + rtol * np.abs(want)).sum())
 
 
 def int_matrix(rng: np.random.Generator, shape, lo: int = -8, hi: int = 8) -> np.ndarray:
