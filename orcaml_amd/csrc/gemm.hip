@@ -8,12 +8,14 @@
 // contiguous values, or "mn-fast" rows of M/N contiguous values) and the
 // MFMA fragments are read out of whichever layout it is.
 //
-// Tiling: a 256-thread block (4 wave64s as 2 x 2) owns a 128 x 128 tile of C;
-// each wave owns 64 x 64 = 2 x 2 MFMA 32x32 blocks (64 accumulator VGPRs per
-// lane).  K advances in slabs of 32 held in double-buffered LDS (72 KiB, so
-// two blocks fit in one CU's 160 KiB).  The next slab's global loads are
-// issued before the current slab's 64 MFMAs per wave and land in the other
-// LDS buffer afterwards; one barrier per slab.
+// Tiling: a 256-thread block (4 wave64s as 2 x 2) owns a 128 x 128 or
+// 128 x 64 tile of C (the smaller tile when the larger one cannot give every
+// CU two blocks); each wave owns 2 x 2 (or 2 x 1) MFMA 32x32 blocks.  K
+// advances in slabs of 32 held in double-buffered LDS (72 / 54 KiB, so two
+// blocks fit in one CU's 160 KiB).  The next slab's global loads are issued
+// before the current slab's MFMAs and land in the other LDS buffer
+// afterwards; one barrier per slab.  Interior blocks of aligned operands load
+// without bounds checks (a uniform branch); edge blocks zero-fill.
 //
 // Within a slab, MFMA step s (0..15) gives lane half h = lane/32 the k index
 // h*16 + s, for both operands, so a lane's A (or B^T) fragment for the whole
@@ -21,19 +23,22 @@
 // k-fast tiles are padded to 36 floats and k-rows 16..31 of mn-fast tiles are
 // shifted by 32 floats so both halves of a wave hit disjoint LDS banks.
 #include <cstdint>
+#include <cstdlib>
+#include <type_traits>
 
 #include "runtime.hpp"
 
 namespace orca_hip {
 namespace {
 
-constexpr int BM = 128, BN = 128, BK = 32, NTHREADS = 256;
-constexpr int LDK = BK + 4;        // pitch of k-fast tile rows (floats)
-constexpr int MN_GAP = 32;         // shift of k-rows 16..31 in mn-fast tiles
-constexpr int TILE = BM * LDK;     // floats per operand buffer (>= BK * BM + MN_GAP)
-static_assert(BK * BM + MN_GAP <= TILE, "mn-fast tile must fit the buffer");
+constexpr int BK = 32, NTHREADS = 256;
+constexpr int LDK = BK + 4;  // pitch of k-fast tile rows (floats)
+constexpr int MN_GAP = 32;   // shift of k-rows 16..31 in mn-fast tiles
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
+// Native 4-float vector: copies stay SSA values (HIP's float4 struct copies
+// lower to memcpy, which can pin a register stage in scratch).
+typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 struct GemmParams {
   const float* A;
@@ -52,87 +57,87 @@ struct GemmParams {
   int vec_a, vec_b;
 };
 
-__device__ __forceinline__ int mn_off(int k) { return k * BM + (k >= 16 ? MN_GAP : 0); }
+// Floats of one operand buffer: P rows of a k-fast tile, or BK rows of P in a mn-fast tile.
+constexpr int tile_floats(int P) { return P * LDK > BK * P + MN_GAP ? P * LDK : BK * P + MN_GAP; }
 
-// Stage one BK slab of an operand into registers.  KFAST: rows of the source
-// hold K contiguous values (row r = m or n), else rows hold M/N contiguous
-// values (row r = k).
-template <bool KFAST>
+template <int P>
+__device__ __forceinline__ int mn_off(int k) {
+  return k * P + (k >= 16 ? MN_GAP : 0);
+}
+
+// Stage one BK slab of an operand (P rows/cols of M or N) into registers.
+// KFAST: rows of the source hold K contiguous values (row = m or n), else rows
+// hold M/N contiguous values (row = k).  `fast` (uniform per block) means the
+// whole slab is in bounds and 16-byte aligned: plain float4 loads.
+template <bool KFAST, int P>
 __device__ __forceinline__ void load_slab(const float* __restrict__ src, int64_t ld, int row0_mn, int lim_mn, int k0,
-                                          int klim, bool vec, float4 (&r)[4]) {
+                                          int klim, bool fast, float4 (&r)[P / 32]) {
   const int tid = threadIdx.x;
+  constexpr int PER_ROW = P / 4;  // float4s per mn-fast row
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    int idx = tid + NTHREADS * j;
+  for (int j = 0; j < P / 32; ++j) {
+    const int idx = tid + NTHREADS * j;
     int mn, k;
     if (KFAST) {
       mn = row0_mn + (idx >> 3);
       k = k0 + (idx & 7) * 4;
     } else {
-      k = k0 + (idx >> 5);
-      mn = row0_mn + (idx & 31) * 4;
+      k = k0 + idx / PER_ROW;
+      mn = row0_mn + (idx % PER_ROW) * 4;
     }
-    if (KFAST) {
-      const float* p = src + (int64_t)mn * ld + k;
-      if (vec && mn < lim_mn && k + 4 <= klim) {
-        r[j] = *reinterpret_cast<const float4*>(p);
-      } else {
-        float t[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) t[e] = (mn < lim_mn && k + e < klim) ? p[e] : 0.0f;
-        r[j] = make_float4(t[0], t[1], t[2], t[3]);
-      }
+    const float* p = KFAST ? src + (int64_t)mn * ld + k : src + (int64_t)k * ld + mn;
+    if (fast) {
+      r[j] = *reinterpret_cast<const float4*>(p);
     } else {
-      const float* p = src + (int64_t)k * ld + mn;
-      if (vec && k < klim && mn + 4 <= lim_mn) {
-        r[j] = *reinterpret_cast<const float4*>(p);
-      } else {
-        float t[4];
+      float t[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) t[e] = (k < klim && mn + e < lim_mn) ? p[e] : 0.0f;
-        r[j] = make_float4(t[0], t[1], t[2], t[3]);
+      for (int e = 0; e < 4; ++e) {
+        const bool in = KFAST ? (mn < lim_mn && k + e < klim) : (k < klim && mn + e < lim_mn);
+        t[e] = in ? p[e] : 0.0f;
       }
+      r[j] = make_float4(t[0], t[1], t[2], t[3]);
     }
   }
 }
 
-template <bool KFAST>
-__device__ __forceinline__ void store_slab(float* __restrict__ s, const float4 (&r)[4]) {
+template <bool KFAST, int P, typename V>
+__device__ __forceinline__ void store_slab(float* __restrict__ s, const V (&r)[P / 32]) {
   const int tid = threadIdx.x;
+  constexpr int PER_ROW = P / 4;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    int idx = tid + NTHREADS * j;
-    int off = KFAST ? (idx >> 3) * LDK + (idx & 7) * 4 : mn_off(idx >> 5) + (idx & 31) * 4;
-    *reinterpret_cast<float4*>(s + off) = r[j];
+  for (int j = 0; j < P / 32; ++j) {
+    const int idx = tid + NTHREADS * j;
+    const int off = KFAST ? (idx >> 3) * LDK + (idx & 7) * 4 : mn_off<P>(idx / PER_ROW) + (idx % PER_ROW) * 4;
+    *reinterpret_cast<V*>(s + off) = r[j];
   }
 }
 
-// Fragment of one 32-row (or 32-column) MFMA block for the whole slab:
-// f[s] = operand(row = base + lane%32, k = h*16 + s).
-template <bool KFAST>
-__device__ __forceinline__ void read_frag(const float* __restrict__ s, int base, float (&f)[16]) {
+// Half a slab of one 32-row (or 32-column) MFMA block's fragment:
+// f[q] = operand(row = base + lane%32, k = h*16 + 8*half + q), q = 0..7.
+template <bool KFAST, int P>
+__device__ __forceinline__ void read_frag(const float* __restrict__ s, int base, int half, float (&f)[8]) {
   const int lane = threadIdx.x & 63, h = lane >> 5, i = lane & 31;
   if (KFAST) {
-    const float* p = s + (base + i) * LDK + h * 16;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      float4 v = *reinterpret_cast<const float4*>(p + 4 * q);
-      f[4 * q + 0] = v.x;
-      f[4 * q + 1] = v.y;
-      f[4 * q + 2] = v.z;
-      f[4 * q + 3] = v.w;
-    }
+    const float* p = s + (base + i) * LDK + h * 16 + half * 8;
+    const float4 v0 = *reinterpret_cast<const float4*>(p);
+    const float4 v1 = *reinterpret_cast<const float4*>(p + 4);
+    f[0] = v0.x; f[1] = v0.y; f[2] = v0.z; f[3] = v0.w;
+    f[4] = v1.x; f[5] = v1.y; f[6] = v1.z; f[7] = v1.w;
   } else {
-    const float* p = s + h * (16 * BM + MN_GAP) + base + i;
+    const float* p = s + h * (16 * P + MN_GAP) + half * 8 * P + base + i;
 #pragma unroll
-    for (int q = 0; q < 16; ++q) f[q] = p[q * BM];
+    for (int q = 0; q < 8; ++q) f[q] = p[q * P];
   }
 }
 
 // TA: A stored [K][lda] (A^T), else [M][lda].  TB: B stored [N][ldb] (B^T), else [K][ldb].
-template <bool TA, bool TB>
+// Block tile BM x BN, four waves as 2 x 2, wave tile (BM/2) x (BN/2) = MT x NT
+// MFMA 32x32 blocks.
+template <int BM, int BN, bool TA, bool TB>
 __global__ void __launch_bounds__(NTHREADS) gemm_mfma_f32_kernel(GemmParams p) {
-  __shared__ __attribute__((aligned(16))) float smem[2][2][TILE];  // [buffer][A|B]
+  constexpr int MT = BM / 64, NT = BN / 64;
+  constexpr int A_TILE = tile_floats(BM), B_TILE = tile_floats(BN);
+  __shared__ __attribute__((aligned(16))) float smem[2][A_TILE + B_TILE];  // [buffer][A | B]
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int wm = wave >> 1, wn = wave & 1, h = lane >> 5, i = lane & 31;
@@ -144,80 +149,313 @@ __global__ void __launch_bounds__(NTHREADS) gemm_mfma_f32_kernel(GemmParams p) {
   const int kb = split * p.k_chunk;
   const int ke = min(p.K, kb + p.k_chunk);
   const int nslabs = (ke - kb + BK - 1) / BK;
-  const bool vec_a = p.vec_a != 0, vec_b = p.vec_b != 0;
+  // Interior blocks with aligned operands take the unchecked load path.
+  const bool a_in = p.vec_a != 0 && m0 + BM <= p.M;
+  const bool b_in = p.vec_b != 0 && n0 + BN <= p.N;
   const bool do_colsum = p.colsum != nullptr && blockIdx.y == 0 && !TB;
 
-  floatx16 acc[2][2];
+  floatx16 acc[MT][NT];
 #pragma unroll
-  for (int a = 0; a < 2; ++a)
+  for (int a = 0; a < MT; ++a)
 #pragma unroll
-    for (int b = 0; b < 2; ++b)
+    for (int b = 0; b < NT; ++b)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.0f;
-  float cs = 0.0f;  // bias column sum (threads 0..127 own column n0 + tid)
+  float cs = 0.0f;  // bias column sum (threads 0..BN-1 own column n0 + tid)
 
-  float4 ra[4], rb[4];
-  // A tile: rows m (k-fast) when !TA, rows k (m-fast) when TA.
-  load_slab<!TA>(A, p.lda, m0, p.M, kb, ke, vec_a, ra);
-  load_slab<TB>(B, p.ldb, n0, p.N, kb, ke, vec_b, rb);
-  store_slab<!TA>(smem[0][0], ra);
-  store_slab<TB>(smem[0][1], rb);
-  __syncthreads();
-
-  for (int t = 0; t < nslabs; ++t) {
-    const int cur = t & 1;
+  // Global loads run two slabs ahead: slab t+2 is fetched into one register
+  // stage while slab t is multiplied out of LDS and slab t+1 (the other
+  // stage) waits to be stored into the free LDS buffer.  The loop handles two
+  // slabs per trip so each register stage is a fixed set of VGPRs.
+  auto load = [&](int t, float4 (&ra)[BM / 32], float4 (&rb)[BN / 32]) {
     const int k0 = kb + t * BK;
-    const bool more = t + 1 < nslabs;
-    if (more) {
-      load_slab<!TA>(A, p.lda, m0, p.M, k0 + BK, ke, vec_a, ra);
-      load_slab<TB>(B, p.ldb, n0, p.N, k0 + BK, ke, vec_b, rb);
-    }
-    const float* sa = smem[cur][0];
-    const float* sb = smem[cur][1];
+    const bool kfull = k0 + BK <= ke;
+    // A tile: rows m (k-fast) when !TA, rows k (m-fast) when TA.
+    load_slab<!TA, BM>(A, p.lda, m0, p.M, k0, ke, a_in && kfull, ra);
+    load_slab<TB, BN>(B, p.ldb, n0, p.N, k0, ke, b_in && kfull, rb);
+  };
+  auto store = [&](float* s, const float4 (&ra)[BM / 32], const float4 (&rb)[BN / 32]) {
+    store_slab<!TA, BM>(s, ra);
+    store_slab<TB, BN>(s + A_TILE, rb);
+  };
+  auto compute = [&](const float* s, int t) {
+    const float* sa = s;
+    const float* sb = s + A_TILE;
     if (do_colsum && tid < BN) {
-      const int kv = min(BK, ke - k0);
-      for (int k = 0; k < kv; ++k) cs = cs + sb[mn_off(k) + tid];
+      const int kv = min(BK, ke - (kb + t * BK));
+      for (int k = 0; k < kv; ++k) cs = cs + sb[mn_off<BN>(k) + tid];
     }
-    float fa[2][16], fb[2][16];
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt) read_frag<!TA>(sa, wm * 64 + mt * 32, fa[mt]);
+    for (int half = 0; half < 2; ++half) {
+      float fa[MT][8], fb[NT][8];
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt) read_frag<TB>(sb, wn * 64 + nt * 32, fb[nt]);
+      for (int mt = 0; mt < MT; ++mt) read_frag<!TA, BM>(sa, wm * (BM / 2) + mt * 32, half, fa[mt]);
 #pragma unroll
-    for (int s = 0; s < 16; ++s)
+      for (int nt = 0; nt < NT; ++nt) read_frag<TB, BN>(sb, wn * (BN / 2) + nt * 32, half, fb[nt]);
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt)
+      for (int q = 0; q < 8; ++q)
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt)
-          acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[mt][s], fb[nt][s], acc[mt][nt], 0, 0, 0);
-    if (more) {
-      store_slab<!TA>(smem[cur ^ 1][0], ra);
-      store_slab<TB>(smem[cur ^ 1][1], rb);
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int nt = 0; nt < NT; ++nt)
+            acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[mt][q], fb[nt][q], acc[mt][nt], 0, 0, 0);
+#ifdef ORCA_GEMM_IGLP
+      __builtin_amdgcn_iglp_opt(ORCA_GEMM_IGLP);
+#endif
     }
+  };
+
+  float4 ra0[BM / 32], rb0[BN / 32], ra1[BM / 32], rb1[BN / 32];
+  load(0, ra0, rb0);
+  store(smem[0], ra0, rb0);
+  if (nslabs > 1) load(1, ra1, rb1);
+  __syncthreads();
+  int t = 0;
+  for (; t + 1 < nslabs; t += 2) {
+    // LDS[0] holds slab t, stage 1 holds slab t+1.
+    if (t + 2 < nslabs) load(t + 2, ra0, rb0);
+    compute(smem[0], t);
+    store(smem[1], ra1, rb1);
+    __syncthreads();
+    // LDS[1] holds slab t+1, stage 0 holds slab t+2.
+    if (t + 3 < nslabs) load(t + 3, ra1, rb1);
+    compute(smem[1], t + 1);
+    if (t + 2 < nslabs) store(smem[0], ra0, rb0);
     __syncthreads();
   }
+  if (t < nslabs) compute(smem[0], t);  // odd slab count: the last slab sits in LDS[0]
 
   // One partial per K-chunk when K is split (reduced in chunk order on the host side).
   if (do_colsum && tid < BN && n0 + tid < p.N) p.colsum[(int64_t)split * p.N + n0 + tid] = cs;
 
   // Epilogue.  Lane (h, i), register r of block (mt, nt) holds
-  // C[wm*64 + mt*32 + (r/4)*8 + h*4 + r%4][wn*64 + nt*32 + i].
+  // C[wm*BM/2 + mt*32 + (r/4)*8 + h*4 + r%4][wn*BN/2 + nt*32 + i].
   float* C = p.C + batch * p.sc;
   if (p.splits > 1) C = p.C + (int64_t)bz * p.M * p.N;  // raw partial sums, ld = N
   const int64_t ldc = p.splits > 1 ? p.N : p.ldc;
   const int epi = p.splits > 1 ? ORCA_HIP_EPI_NONE : p.epi;
 #pragma unroll
-  for (int mt = 0; mt < 2; ++mt)
+  for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-      const int col = n0 + wn * 64 + nt * 32 + i;
+    for (int nt = 0; nt < NT; ++nt) {
+      const int col = n0 + wn * (BN / 2) + nt * 32 + i;
       if (col >= p.N) continue;
       float bias = 0.0f;
       if (epi == ORCA_HIP_EPI_BIAS || epi == ORCA_HIP_EPI_BIAS_RELU) bias = p.bias[col];
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int row = m0 + wm * 64 + mt * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
+        const int row = m0 + wm * (BM / 2) + mt * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
         if (row >= p.M) continue;
+        float v = acc[mt][nt][r];
+        if (epi == ORCA_HIP_EPI_BIAS) {
+          v = v + bias;
+        } else if (epi == ORCA_HIP_EPI_BIAS_RELU) {
+          v = v + bias;
+          v = v > 0.0f ? v : 0.0f;
+        } else if (epi == ORCA_HIP_EPI_RELU_MASK) {
+          v = p.mask[(int64_t)row * p.ldmask + col] > 0.0f ? v : 0.0f;
+        }
+        C[(int64_t)row * ldc + col] = v;
+      }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Fast path for fully tile-aligned products (M, N multiples of 128, every
+// K-chunk a multiple of 32, 16-byte aligned operands): no bounds checks,
+// global loads from a uniform per-slab base plus 32-bit per-lane offsets, and a
+// software pipeline built so each wave always has MFMAs queued while it issues
+// memory work.  Per slab t (one register stage R, two LDS buffers L0/L1):
+//   region A: store R (slab t+1, loaded one slab earlier) into L[(t+1)%2];
+//             load slab t+2 -> R; read the second half-slab fragments of t;
+//             32 MFMAs on the first half of t; barrier
+//   region B: read the first half-slab fragments of t+1 from L[(t+1)%2]; 32
+//             MFMAs on the second half of t.
+// The barrier sits between the two MFMA groups, so its wait overlaps queued
+// MFMAs, and the next slab's first fragments arrive under the current slab's
+// last MFMAs.  sched_group_barrier interleaves one memory instruction after
+// each MFMA.  L[(t+1)%2] was last read before the barrier of slab t-1, so the
+// store in region A of slab t cannot overwrite fragments still to be read.
+template <bool KFAST>
+struct BufOperand {
+  const char* base;  // uniform: the operand's first element
+  uint32_t voff[4];  // byte offsets of this thread's four float4s in slab 0
+  uint32_t slab_bytes;
+
+  __device__ __forceinline__ void init(const float* b, int64_t ld, int row0_mn, int kb) {
+    base = reinterpret_cast<const char*>(b);
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int idx = tid + NTHREADS * j;
+      int64_t off;
+      if (KFAST)
+        off = (int64_t)(row0_mn + (idx >> 3)) * ld + kb + (idx & 7) * 4;
+      else
+        off = (int64_t)(kb + (idx >> 5)) * ld + row0_mn + (idx & 31) * 4;
+      voff[j] = (uint32_t)(off * 4);
+    }
+    slab_bytes = KFAST ? (uint32_t)(BK * 4) : (uint32_t)(BK * ld * 4);
+  }
+  // Uniform slab base + 32-bit per-lane offset: global_load_dwordx4 in saddr form.
+  __device__ __forceinline__ void load(int t, floatx4 (&r)[4]) const {
+    const char* slab = base + (size_t)slab_bytes * (uint32_t)t;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) r[j] = *reinterpret_cast<const floatx4*>(slab + voff[j]);
+  }
+};
+
+template <bool TA, bool TB, bool COLSUM>
+__global__ void __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2))) gemm_mfma_f32_fast_kernel(GemmParams p) {
+  constexpr int BM = 128, BN = 128, MT = 2, NT = 2;
+  constexpr int A_TILE = tile_floats(BM), B_TILE = tile_floats(BN);
+  __shared__ __attribute__((aligned(16))) float smem[2][A_TILE + B_TILE];
+
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int wm = wave >> 1, wn = wave & 1, h = lane >> 5, i = lane & 31;
+  const int n0 = blockIdx.x * BN, m0 = blockIdx.y * BM;
+  const int bz = blockIdx.z, batch = bz / p.splits, split = bz % p.splits;
+  const int kb = split * p.k_chunk;
+  const int n = (min(p.K, kb + p.k_chunk) - kb) / BK;  // whole slabs
+  const bool do_colsum = COLSUM && blockIdx.y == 0;
+
+  BufOperand<!TA> opa;
+  BufOperand<TB> opb;
+  opa.init(p.A + batch * p.sa, p.lda, m0, kb);
+  opb.init(p.B + batch * p.sb, p.ldb, n0, kb);
+
+  floatx16 acc[MT][NT];
+#pragma unroll
+  for (int a = 0; a < MT; ++a)
+#pragma unroll
+    for (int b = 0; b < NT; ++b)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.0f;
+  float cs = 0.0f;
+
+  floatx4 ra[4], rb[4];
+  float f0a[MT][8], f0b[NT][8], f1a[MT][8], f1b[NT][8];
+
+  auto store = [&](float* s) {
+    store_slab<!TA, BM>(s, ra);
+    store_slab<TB, BN>(s + A_TILE, rb);
+  };
+  auto load = [&](int t) {
+    opa.load(t, ra);
+    opb.load(t, rb);
+  };
+  auto frags = [&](const float* s, int half, float (&fa)[MT][8], float (&fb)[NT][8]) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) read_frag<!TA, BM>(s, wm * (BM / 2) + mt * 32, half, fa[mt]);
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) read_frag<TB, BN>(s + A_TILE, wn * (BN / 2) + nt * 32, half, fb[nt]);
+  };
+  auto mfma = [&](const float (&fa)[MT][8], const float (&fb)[NT][8]) {
+#pragma unroll
+    for (int q = 0; q < 8; ++q)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+          acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[mt][q], fb[nt][q], acc[mt][nt], 0, 0, 0);
+  };
+  auto colsum = [&](const float* s) {
+    if (do_colsum && tid < BN) {
+      const float* sb = s + A_TILE;
+#pragma unroll
+      for (int k = 0; k < BK; ++k) cs = cs + sb[mn_off<BN>(k) + tid];
+    }
+  };
+  // Memory instructions of region A: 8 LDS stores, 8 VMEM loads, the
+  // half-slab fragment reads (A k-fast: 4 x b128, m-fast: 16 x b32; same for B).
+  constexpr int RD = (!TA ? 4 : 16) + (TB ? 4 : 16);
+  auto interleave_a = [&]() {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // DS write
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read
+    }
+#pragma unroll
+    for (int j = 0; j < (RD < 16 ? RD : 16); ++j) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, RD > 16 ? 2 : 1, 0);  // DS read
+    }
+  };
+  auto interleave_b = [&]() {
+#pragma unroll
+    for (int j = 0; j < (RD < 16 ? RD : 16); ++j) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, RD > 16 ? 2 : 1, 0);
+    }
+  };
+
+  // One slab; P = t % 2 selects the LDS buffer.  FULL: slabs t+1 and t+2
+  // exist (no runtime checks inside the straight-line body).
+  auto body = [&](auto P_, int t, bool full) {
+    constexpr int P = decltype(P_)::value;
+    float* lcur = smem[P];
+    float* lnxt = smem[P ^ 1];
+    if (full) {
+      store(lnxt);
+      load(t + 2);
+      frags(lcur, 1, f1a, f1b);
+      mfma(f0a, f0b);
+      interleave_a();
+    } else {
+      if (t + 1 < n) store(lnxt);
+      if (t + 2 < n) load(t + 2);
+      frags(lcur, 1, f1a, f1b);
+      mfma(f0a, f0b);
+    }
+    colsum(lcur);
+    __syncthreads();
+    if (full) {
+      frags(lnxt, 0, f0a, f0b);
+      mfma(f1a, f1b);
+      interleave_b();
+    } else {
+      if (t + 1 < n) frags(lnxt, 0, f0a, f0b);
+      mfma(f1a, f1b);
+    }
+  };
+
+  // Prologue: slab 0 into L0 and its first fragments; slab 1 in flight in R.
+  load(0);
+  store(smem[0]);
+  if (n > 1) load(1);
+  __syncthreads();
+  frags(smem[0], 0, f0a, f0b);
+
+  int t = 0;
+  for (; t + 3 < n; t += 2) {
+    body(std::integral_constant<int, 0>{}, t, true);
+    body(std::integral_constant<int, 1>{}, t + 1, true);
+  }
+  if (t < n) body(std::integral_constant<int, 0>{}, t, false);
+  if (t + 1 < n) body(std::integral_constant<int, 1>{}, t + 1, false);
+  if (t + 2 < n) body(std::integral_constant<int, 0>{}, t + 2, false);
+
+  if (do_colsum && tid < BN) p.colsum[(int64_t)split * p.N + n0 + tid] = cs;
+
+  float* C = p.C + batch * p.sc;
+  if (p.splits > 1) C = p.C + (int64_t)bz * p.M * p.N;
+  const int64_t ldc = p.splits > 1 ? p.N : p.ldc;
+  const int epi = p.splits > 1 ? ORCA_HIP_EPI_NONE : p.epi;
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      const int col = n0 + wn * (BN / 2) + nt * 32 + i;
+      float bias = 0.0f;
+      if (epi == ORCA_HIP_EPI_BIAS || epi == ORCA_HIP_EPI_BIAS_RELU) bias = p.bias[col];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = m0 + wm * (BM / 2) + mt * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
         float v = acc[mt][nt][r];
         if (epi == ORCA_HIP_EPI_BIAS) {
           v = v + bias;
@@ -276,11 +514,17 @@ __global__ void colsum_split_reduce_kernel(const float* __restrict__ part, int s
 
 inline bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; }
 
-const char* kernel_name(bool ta, bool tb) {
-  if (!ta && !tb) return "gemm_nn";
-  if (!ta && tb) return "gemm_nt";
-  if (ta && !tb) return "gemm_tn";
-  return "gemm_tt";
+// ORCA_HIP_GEMM_FAST=0 sends every product through the generic kernel (tuning / A-B runs).
+bool fast_env_off() {
+  static const char* v = std::getenv("ORCA_HIP_GEMM_FAST");
+  return v && v[0] == '0';
+}
+
+// Profiler names: "gemm_<op(A)><op(B)>", "_pipe" for the pipelined 128 x 128 kernel.
+const char* kernel_name(bool ta, bool tb, bool pipelined) {
+  static const char* names[2][4] = {{"gemm_nn", "gemm_nt", "gemm_tn", "gemm_tt"},
+                                    {"gemm_nn_pipe", "gemm_nt_pipe", "gemm_tn_pipe", "gemm_tt_pipe"}};
+  return names[pipelined ? 1 : 0][(ta ? 2 : 0) + (tb ? 1 : 0)];
 }
 
 }  // namespace
@@ -303,13 +547,30 @@ void gemm(orca_hip_ctx* ctx, bool trans_a, bool trans_b, size_t M, size_t N, siz
     if (epi.colsum) launch_fill(ctx, epi.colsum, 0.0f, N);
     return;
   }
+  const bool vec_a = aligned16(A) && lda % 4 == 0 && (batch == 1 || sa % 4 == 0);
+  const bool vec_b = aligned16(B) && ldb % 4 == 0 && (batch == 1 || sb % 4 == 0);
+  // Fully tile-aligned products take the pipelined 128 x 128 kernel, whose
+  // per-lane offsets are 32-bit byte offsets within one operand.
+  const size_t a_rows = trans_a ? K : M, b_rows = trans_b ? N : K;
+  const bool fast = M % 128 == 0 && N % 128 == 0 && K % BK == 0 && vec_a && vec_b &&
+                    a_rows * lda * 4 < 0xffffffffull && b_rows * ldb * 4 < 0xffffffffull && !fast_env_off();
+  // Generic kernel tile: 128 x 128 when that gives every CU a block, else
+  // 128 x 64 (twice the blocks).  ORCA_HIP_GEMM_TILE=128x128|128x64 overrides
+  // the generic kernel's choice (tuning).
+  const size_t target = (size_t)ctx->num_cus;
+  const size_t t128 = ((M + 127) / 128) * ((N + 127) / 128) * batch;
+  int bn = t128 >= target ? 128 : 64;
+  static const char* tile_env = std::getenv("ORCA_HIP_GEMM_TILE");
+  if (tile_env && std::string(tile_env) == "128x128") bn = 128;
+  if (tile_env && std::string(tile_env) == "128x64") bn = 64;
+  if (fast) bn = 128;
+  const size_t BM = 128, BN = (size_t)bn;
   const size_t mt = (M + BM - 1) / BM, nt = (N + BN - 1) / BN;
   if (mt > 65535) fail(ORCA_HIP_ERR_INTERNAL, "gemm: too many row tiles");
 
   // Split K when the tile grid cannot fill the CUs and K is long enough.
   int splits = 1;
   const size_t tiles = mt * nt * batch;
-  const size_t target = (size_t)ctx->num_cus;
   if (tiles < target / 2 && K >= 4 * (size_t)BK) {
     size_t want = (target + tiles - 1) / tiles;
     size_t max_by_k = K / (2 * BK);
@@ -350,8 +611,8 @@ void gemm(orca_hip_ctx* ctx, bool trans_a, bool trans_b, size_t M, size_t N, siz
   } else {
     p.colsum = fold_colsum ? epi.colsum : nullptr;
   }
-  p.vec_a = aligned16(A) && lda % 4 == 0 && (batch == 1 || sa % 4 == 0);
-  p.vec_b = aligned16(B) && ldb % 4 == 0 && (batch == 1 || sb % 4 == 0);
+  p.vec_a = vec_a;
+  p.vec_b = vec_b;
 
   std::unique_ptr<Scratch> ws;
   if (splits > 1) {
@@ -363,16 +624,34 @@ void gemm(orca_hip_ctx* ctx, bool trans_a, bool trans_b, size_t M, size_t N, siz
 
   dim3 grid((unsigned)nt, (unsigned)mt, (unsigned)(batch * splits));
   {
-    ProfScope ps(ctx, kernel_name(trans_a, trans_b), 2.0 * (double)M * N * K * batch,
+    ProfScope ps(ctx, kernel_name(trans_a, trans_b, fast), 2.0 * (double)M * N * K * batch,
                  4.0 * (double)batch * (M * K + K * N + M * N));
-    if (!trans_a && !trans_b)
-      hipLaunchKernelGGL((gemm_mfma_f32_kernel<false, false>), grid, dim3(NTHREADS), 0, ctx->stream, p);
-    else if (!trans_a && trans_b)
-      hipLaunchKernelGGL((gemm_mfma_f32_kernel<false, true>), grid, dim3(NTHREADS), 0, ctx->stream, p);
-    else if (trans_a && !trans_b)
-      hipLaunchKernelGGL((gemm_mfma_f32_kernel<true, false>), grid, dim3(NTHREADS), 0, ctx->stream, p);
-    else
-      hipLaunchKernelGGL((gemm_mfma_f32_kernel<true, true>), grid, dim3(NTHREADS), 0, ctx->stream, p);
+#define GEMM_LAUNCH(BN_, TA_, TB_) \
+  hipLaunchKernelGGL((gemm_mfma_f32_kernel<128, BN_, TA_, TB_>), grid, dim3(NTHREADS), 0, ctx->stream, p)
+#define GEMM_DISPATCH(BN_)                                      \
+  do {                                                          \
+    if (!trans_a && !trans_b) GEMM_LAUNCH(BN_, false, false);   \
+    else if (!trans_a && trans_b) GEMM_LAUNCH(BN_, false, true); \
+    else if (trans_a && !trans_b) GEMM_LAUNCH(BN_, true, false); \
+    else GEMM_LAUNCH(BN_, true, true);                          \
+  } while (0)
+#define FAST_LAUNCH(TA_, TB_, CS_) \
+  hipLaunchKernelGGL((gemm_mfma_f32_fast_kernel<TA_, TB_, CS_>), grid, dim3(NTHREADS), 0, ctx->stream, p)
+    if (fast) {
+      const bool cs = p.colsum != nullptr;
+      if (!trans_a && !trans_b) FAST_LAUNCH(false, false, false);
+      else if (!trans_a && trans_b) FAST_LAUNCH(false, true, false);
+      else if (trans_a && !trans_b && cs) FAST_LAUNCH(true, false, true);
+      else if (trans_a && !trans_b) FAST_LAUNCH(true, false, false);
+      else FAST_LAUNCH(true, true, false);
+    } else if (bn == 128) {
+      GEMM_DISPATCH(128);
+    } else {
+      GEMM_DISPATCH(64);
+    }
+#undef FAST_LAUNCH
+#undef GEMM_DISPATCH
+#undef GEMM_LAUNCH
     ORCA_HIP_CHECK(hipGetLastError());
   }
   if (splits > 1) {

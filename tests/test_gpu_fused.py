@@ -53,7 +53,10 @@ def assert_gemm_error_bound(got, A, B):
 
 
 GEMM_SHAPES = [(1, 1, 1), (64, 128, 784), (130, 70, 33), (257, 129, 1000), (1024, 10, 4096), (1024, 4096, 10),
-               (784, 384, 1024), (96, 16, 4)]
+               (784, 384, 1024), (96, 16, 4),
+               # tile-aligned: the pipelined kernel, with 1..5 and 32 slabs and a split-K launch
+               (128, 128, 32), (256, 128, 64), (128, 256, 96), (256, 256, 128), (384, 128, 160), (256, 384, 1024),
+               (128, 128, 4096)]
 
 
 @pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False), (True, True)])
@@ -65,6 +68,29 @@ def test_gemm_exact_on_integers(ctx, ta, tb, M, N, K):
     want = (A.astype(np.int64) @ B.astype(np.int64)).astype(np.float32)
     got = run_gemm(ctx, ta, tb, np.ascontiguousarray(A.T) if ta else A, np.ascontiguousarray(B.T) if tb else B)
     np.testing.assert_array_equal(got, want)
+
+
+@pytest.mark.parametrize("ta,tb,colsum", [(False, False, False), (False, True, False), (True, False, True),
+                                          (True, False, False), (True, True, False)])
+def test_gemm_aligned_shapes_take_pipelined_kernel(ctx, ta, tb, colsum):
+    """Tile-aligned products run on the pipelined 128 x 128 kernel (profiler
+    name *_pipe) and ragged ones on the generic kernel; both exact on integers."""
+    rng = np.random.default_rng(3)
+    name = "gemm_" + ("t" if ta else "n") + ("t" if tb else "n")
+    for (M, N, K), pipe in (((256, 384, 160), True), ((256, 384, 161), False), ((256, 200, 160), False)):
+        A = int_matrix(rng, (M, K))
+        B = int_matrix(rng, (K, N))
+        ctx.prof_reset()
+        ctx.prof_enable(True)
+        out = run_gemm(ctx, ta, tb, np.ascontiguousarray(A.T) if ta else A, np.ascontiguousarray(B.T) if tb else B,
+                       colsum=colsum and not tb)
+        ctx.prof_enable(False)
+        names = {k["name"] for k in ctx.prof_report()["kernels"]}
+        assert (name + "_pipe" if pipe else name) in names, names
+        C, cs = out if colsum else (out, None)
+        np.testing.assert_array_equal(C, (A.astype(np.int64) @ B.astype(np.int64)).astype(np.float32))
+        if cs is not None:
+            np.testing.assert_array_equal(cs, O.sum_to_shape(B, (1, N)).reshape(N))
 
 
 def test_gemm_epilogues_match_composed_ops(ctx):
@@ -87,7 +113,7 @@ def test_gemm_epilogues_match_composed_ops(ctx):
 
 
 @pytest.mark.parametrize("M,N,K,exact", [(128, 256, 64, True), (784, 4096, 1024, True), (4096, 10, 1024, False),
-                                         (33, 70, 5, True)])
+                                         (33, 70, 5, True), (512, 384, 96, True), (128, 128, 4096, False)])
 def test_gemm_colsum_is_bias_gradient(ctx, M, N, K, exact):
     """dW = X^T dY with the bias column sum fused.  With one K-chunk per tile
     the column sum equals sum_to_shape(dY, [1, N]) bit for bit (same ascending
