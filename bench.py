@@ -7,9 +7,11 @@ already resident in HBM.  Prints ONE JSON line (see the keys below).
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
 
-`roofline` reports the dominant kernel (largest device time per step):
-achieved = algorithmic work per launch / mean launch duration, measured with
-HIP events on the library's stream over a second pass of the same K steps.
+`roofline` reports the dominant kernel (largest device time per step; GEMMs
+are told apart by shape): achieved = algorithmic work per launch / mean launch
+duration, measured with HIP events on the library's stream over a second pass
+of the same K steps; traffic = that kernel's HBM bytes per launch from the
+rocprofv3 counter summary under profiles/.
 `cpu_baseline` times the CPU oracle (single-threaded sgemm-class GEMM, OpenMP
 elementwise ops -- the reference CPU backend's cost structure) on one step of
 the same workload on this host.
@@ -85,6 +87,9 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-probe-mib", type=int, default=0,
+                    help="first run one device-to-device copy of this many MiB (a known-size kernel that "
+                         "calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); this build has no multi-GPU path",
@@ -97,6 +102,14 @@ def main() -> int:
 
     params, x, labels, onehot = synth.mlp_problem(SEED, DIMS, BATCH)
     ctx = Context(0)
+    if args.copy_probe_mib > 0:
+        nbytes = args.copy_probe_mib << 20
+        src, dst = ctx.alloc(nbytes), ctx.alloc(nbytes)
+        ctx.fill(src, 1.0, nbytes // 4)
+        ctx.d2d(dst, src, nbytes)
+        ctx.sync()
+        src.free()
+        dst.free()
     tr = MLPTrainer(ctx, DIMS, BATCH, kind=OPT["kind"], lr=OPT["lr"], weight_decay=OPT["weight_decay"],
                     betas=OPT["betas"], eps=OPT["eps"])
     tr.set_params(params)
@@ -142,6 +155,15 @@ def main() -> int:
     roof["kernel"] = dominant["name"]
     roof["launches_per_step"] = dominant["launches"] / args.steps
     roof["mean_launch_ms"] = avg_ms
+    # HBM bytes per launch of this kernel from the committed rocprofv3 FETCH_SIZE + WRITE_SIZE passes
+    # (calibrated against a copy of known size); null when the kernel has no such record.
+    traffic_file = os.path.join("profiles", "hbm_traffic_mlp784-4096-4096-10_b1024.json")
+    if os.path.exists(os.path.join(HERE, traffic_file)):
+        with open(os.path.join(HERE, traffic_file)) as fh:
+            rec = json.load(fh)["kernels"].get(dominant["name"])
+        if rec is not None:
+            roof["traffic"] = rec["traffic_bytes"]
+            roof["traffic_source"] = traffic_file
     gemm_ms = sum(k["total_ms"] for k in kernels if k["flops"] > 0) / args.steps
     gemm_flops = sum(k["flops"] for k in kernels if k["flops"] > 0) / args.steps
 

@@ -24,6 +24,7 @@
 // shifted by 32 floats so both halves of a wave hit disjoint LDS banks.
 #include <cstdint>
 #include <cstdlib>
+#include <string>
 #include <type_traits>
 
 #include "runtime.hpp"
@@ -261,9 +262,10 @@ __global__ void __launch_bounds__(NTHREADS) gemm_mfma_f32_kernel(GemmParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// Fast path for fully tile-aligned products (M, N multiples of 128, every
-// K-chunk a multiple of 32, 16-byte aligned operands): no bounds checks,
-// global loads from a uniform per-slab base plus 32-bit per-lane offsets, and a
+// Pipelined kernel for products with M, N, K multiples of 4 and 16-byte
+// aligned operands: edge rows are clamped instead of checked, only the last,
+// partial K slab is loaded with a check (zero fill), global loads use a
+// uniform per-slab base plus 32-bit per-lane offsets, and a
 // software pipeline built so each wave always has MFMAs queued while it issues
 // memory work.  Per slab t (one register stage R, two LDS buffers L0/L1):
 //   region A: store R (slab t+1, loaded one slab earlier) into L[(t+1)%2];
@@ -282,7 +284,10 @@ struct BufOperand {
   uint32_t voff[4];  // byte offsets of this thread's four float4s in slab 0
   uint32_t slab_bytes;
 
-  __device__ __forceinline__ void init(const float* b, int64_t ld, int row0_mn, int kb) {
+  // Rows (M or N) past `lim_mn` are clamped to the last valid row (or float4),
+  // so every load stays inside the operand; they only feed rows / columns of
+  // C that are never stored.  lim_mn is a multiple of 4.
+  __device__ __forceinline__ void init(const float* b, int64_t ld, int row0_mn, int lim_mn, int kb) {
     base = reinterpret_cast<const char*>(b);
     const int tid = threadIdx.x;
 #pragma unroll
@@ -290,18 +295,29 @@ struct BufOperand {
       const int idx = tid + NTHREADS * j;
       int64_t off;
       if (KFAST)
-        off = (int64_t)(row0_mn + (idx >> 3)) * ld + kb + (idx & 7) * 4;
+        off = (int64_t)min(row0_mn + (idx >> 3), lim_mn - 1) * ld + kb + (idx & 7) * 4;
       else
-        off = (int64_t)(kb + (idx >> 5)) * ld + row0_mn + (idx & 31) * 4;
+        off = (int64_t)(kb + (idx >> 5)) * ld + min(row0_mn + (idx & 31) * 4, lim_mn - 4);
       voff[j] = (uint32_t)(off * 4);
     }
     slab_bytes = KFAST ? (uint32_t)(BK * 4) : (uint32_t)(BK * ld * 4);
   }
-  // Uniform slab base + 32-bit per-lane offset: global_load_dwordx4 in saddr form.
+  // A whole slab: uniform slab base + 32-bit lane offset (global_load_dwordx4).
   __device__ __forceinline__ void load(int t, floatx4 (&r)[4]) const {
     const char* slab = base + (size_t)slab_bytes * (uint32_t)t;
 #pragma unroll
     for (int j = 0; j < 4; ++j) r[j] = *reinterpret_cast<const floatx4*>(slab + voff[j]);
+  }
+  // The chunk's last, partial slab: k offsets >= klen (a multiple of 4) are
+  // zero-filled without touching memory.
+  __device__ __forceinline__ void load_tail(int t, int klen, floatx4 (&r)[4]) const {
+    const char* slab = base + (size_t)slab_bytes * (uint32_t)t;
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int kk = t * BK + (KFAST ? (tid & 7) * 4 : (tid >> 5) + 8 * j);
+      r[j] = kk < klen ? *reinterpret_cast<const floatx4*>(slab + voff[j]) : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
   }
 };
 
@@ -316,13 +332,15 @@ __global__ void __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2
   const int n0 = blockIdx.x * BN, m0 = blockIdx.y * BM;
   const int bz = blockIdx.z, batch = bz / p.splits, split = bz % p.splits;
   const int kb = split * p.k_chunk;
-  const int n = (min(p.K, kb + p.k_chunk) - kb) / BK;  // whole slabs
+  const int klen = min(p.K, kb + p.k_chunk) - kb;
+  const int nfull = klen / BK;            // whole slabs
+  const int n = (klen + BK - 1) / BK;     // slabs, the last one possibly partial
   const bool do_colsum = COLSUM && blockIdx.y == 0;
 
   BufOperand<!TA> opa;
   BufOperand<TB> opb;
-  opa.init(p.A + batch * p.sa, p.lda, m0, kb);
-  opb.init(p.B + batch * p.sb, p.ldb, n0, kb);
+  opa.init(p.A + batch * p.sa, p.lda, m0, p.M, kb);
+  opb.init(p.B + batch * p.sb, p.ldb, n0, p.N, kb);
 
   floatx16 acc[MT][NT];
 #pragma unroll
@@ -343,6 +361,14 @@ __global__ void __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2
   auto load = [&](int t) {
     opa.load(t, ra);
     opb.load(t, rb);
+  };
+  auto load_any = [&](int t) {  // uniform branch: whole or partial slab
+    if (t < nfull) {
+      load(t);
+    } else {
+      opa.load_tail(t, klen, ra);
+      opb.load_tail(t, klen, rb);
+    }
   };
   auto frags = [&](const float* s, int half, float (&fa)[MT][8], float (&fb)[NT][8]) {
 #pragma unroll
@@ -408,7 +434,7 @@ __global__ void __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2
       interleave_a();
     } else {
       if (t + 1 < n) store(lnxt);
-      if (t + 2 < n) load(t + 2);
+      if (t + 2 < n) load_any(t + 2);
       frags(lcur, 1, f1a, f1b);
       mfma(f0a, f0b);
     }
@@ -425,22 +451,25 @@ __global__ void __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2
   };
 
   // Prologue: slab 0 into L0 and its first fragments; slab 1 in flight in R.
-  load(0);
+  load_any(0);
   store(smem[0]);
-  if (n > 1) load(1);
+  if (n > 1) load_any(1);
   __syncthreads();
   frags(smem[0], 0, f0a, f0b);
 
+  // Full bodies load only whole slabs (t + 3 < nfull); the last slabs,
+  // including a partial one, run through the checked tail bodies.
   int t = 0;
-  for (; t + 3 < n; t += 2) {
+  for (; t + 3 < nfull; t += 2) {
     body(std::integral_constant<int, 0>{}, t, true);
     body(std::integral_constant<int, 1>{}, t + 1, true);
   }
   if (t < n) body(std::integral_constant<int, 0>{}, t, false);
   if (t + 1 < n) body(std::integral_constant<int, 1>{}, t + 1, false);
   if (t + 2 < n) body(std::integral_constant<int, 0>{}, t + 2, false);
+  if (t + 3 < n) body(std::integral_constant<int, 1>{}, t + 3, false);
 
-  if (do_colsum && tid < BN) p.colsum[(int64_t)split * p.N + n0 + tid] = cs;
+  if (do_colsum && tid < BN && n0 + tid < p.N) p.colsum[(int64_t)split * p.N + n0 + tid] = cs;
 
   float* C = p.C + batch * p.sc;
   if (p.splits > 1) C = p.C + (int64_t)bz * p.M * p.N;
@@ -451,11 +480,13 @@ __global__ void __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
       const int col = n0 + wn * (BN / 2) + nt * 32 + i;
+      if (col >= p.N) continue;
       float bias = 0.0f;
       if (epi == ORCA_HIP_EPI_BIAS || epi == ORCA_HIP_EPI_BIAS_RELU) bias = p.bias[col];
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int row = m0 + wm * (BM / 2) + mt * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
+        if (row >= p.M) continue;
         float v = acc[mt][nt][r];
         if (epi == ORCA_HIP_EPI_BIAS) {
           v = v + bias;
@@ -549,10 +580,11 @@ void gemm(orca_hip_ctx* ctx, bool trans_a, bool trans_b, size_t M, size_t N, siz
   }
   const bool vec_a = aligned16(A) && lda % 4 == 0 && (batch == 1 || sa % 4 == 0);
   const bool vec_b = aligned16(B) && ldb % 4 == 0 && (batch == 1 || sb % 4 == 0);
-  // Fully tile-aligned products take the pipelined 128 x 128 kernel, whose
-  // per-lane offsets are 32-bit byte offsets within one operand.
+  // Products with M, N, K multiples of 4 and 16-byte aligned operands take the
+  // pipelined 128 x 128 kernel, whose per-lane offsets are 32-bit byte offsets
+  // within one operand.
   const size_t a_rows = trans_a ? K : M, b_rows = trans_b ? N : K;
-  const bool fast = M % 128 == 0 && N % 128 == 0 && K % BK == 0 && vec_a && vec_b &&
+  const bool fast = M % 4 == 0 && N % 4 == 0 && K % 4 == 0 && vec_a && vec_b &&
                     a_rows * lda * 4 < 0xffffffffull && b_rows * ldb * 4 < 0xffffffffull && !fast_env_off();
   // Generic kernel tile: 128 x 128 when that gives every CU a block, else
   // 128 x 64 (twice the blocks).  ORCA_HIP_GEMM_TILE=128x128|128x64 overrides
@@ -624,7 +656,14 @@ void gemm(orca_hip_ctx* ctx, bool trans_a, bool trans_b, size_t M, size_t N, siz
 
   dim3 grid((unsigned)nt, (unsigned)mt, (unsigned)(batch * splits));
   {
-    ProfScope ps(ctx, kernel_name(trans_a, trans_b, fast), 2.0 * (double)M * N * K * batch,
+    // Profiler records carry the product's shape: "gemm_tn_pipe 4096x4096x1024".
+    std::string pname;
+    if (ctx->prof.enabled) {
+      pname = std::string(kernel_name(trans_a, trans_b, fast)) + " " + std::to_string(M) + "x" + std::to_string(N) +
+              "x" + std::to_string(K);
+      if (batch > 1) pname += "x" + std::to_string(batch);
+    }
+    ProfScope ps(ctx, pname.c_str(), 2.0 * (double)M * N * K * batch,
                  4.0 * (double)batch * (M * K + K * N + M * N));
 #define GEMM_LAUNCH(BN_, TA_, TB_) \
   hipLaunchKernelGGL((gemm_mfma_f32_kernel<128, BN_, TA_, TB_>), grid, dim3(NTHREADS), 0, ctx->stream, p)

@@ -44,6 +44,12 @@ class Context:
             _lib.call("orca_hip_h2d", self.handle, buf.ptr, arr.ctypes.data_as(ctypes.c_void_p), arr.nbytes)
         return buf
 
+    def fill(self, buf: "Buffer", value: float, count: int) -> None:
+        _lib.call("orca_hip_fill", self.handle, buf.ptr, value, count)
+
+    def d2d(self, dst: "Buffer", src: "Buffer", nbytes: int) -> None:
+        _lib.call("orca_hip_d2d", self.handle, dst.ptr, src.ptr, nbytes)
+
     def sync(self) -> None:
         _lib.call("orca_hip_sync", self.handle)
 

@@ -52,11 +52,14 @@ def assert_gemm_error_bound(got, A, B):
     assert (err <= bound).all(), f"max err/bound {float((err / bound).max()):.3f}"
 
 
-GEMM_SHAPES = [(1, 1, 1), (64, 128, 784), (130, 70, 33), (257, 129, 1000), (1024, 10, 4096), (1024, 4096, 10),
-               (784, 384, 1024), (96, 16, 4),
-               # tile-aligned: the pipelined kernel, with 1..5 and 32 slabs and a split-K launch
-               (128, 128, 32), (256, 128, 64), (128, 256, 96), (256, 256, 128), (384, 128, 160), (256, 384, 1024),
-               (128, 128, 4096)]
+GEMM_SHAPES = [
+    # generic kernel (a dimension not a multiple of 4, or N / K = 10 as in the output layer)
+    (1, 1, 1), (130, 70, 33), (257, 129, 1000), (1024, 10, 4096), (1024, 4096, 10),
+    # pipelined kernel, edge tiles and partial K slabs (K = 784 as in the input layer)
+    (64, 128, 784), (784, 384, 1024), (96, 16, 4), (4, 8, 12), (132, 260, 36), (200, 300, 152),
+    # pipelined kernel, tile-aligned: 1..5 and 32 slabs, and split-K launches
+    (128, 128, 32), (256, 128, 64), (128, 256, 96), (256, 256, 128), (384, 128, 160), (256, 384, 1024),
+    (128, 128, 4096), (128, 256, 3076)]
 
 
 @pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False), (True, True)])
@@ -73,11 +76,13 @@ def test_gemm_exact_on_integers(ctx, ta, tb, M, N, K):
 @pytest.mark.parametrize("ta,tb,colsum", [(False, False, False), (False, True, False), (True, False, True),
                                           (True, False, False), (True, True, False)])
 def test_gemm_aligned_shapes_take_pipelined_kernel(ctx, ta, tb, colsum):
-    """Tile-aligned products run on the pipelined 128 x 128 kernel (profiler
-    name *_pipe) and ragged ones on the generic kernel; both exact on integers."""
+    """Products whose M, N, K are multiples of 4 run on the pipelined 128 x 128
+    kernel (profiler name *_pipe), the rest on the generic kernel; both exact
+    on integers."""
     rng = np.random.default_rng(3)
     name = "gemm_" + ("t" if ta else "n") + ("t" if tb else "n")
-    for (M, N, K), pipe in (((256, 384, 160), True), ((256, 384, 161), False), ((256, 200, 160), False)):
+    for (M, N, K), pipe in (((256, 384, 160), True), ((260, 196, 164), True), ((256, 384, 161), False),
+                            ((256, 202, 160), False)):
         A = int_matrix(rng, (M, K))
         B = int_matrix(rng, (K, N))
         ctx.prof_reset()
@@ -86,16 +91,18 @@ def test_gemm_aligned_shapes_take_pipelined_kernel(ctx, ta, tb, colsum):
                        colsum=colsum and not tb)
         ctx.prof_enable(False)
         names = {k["name"] for k in ctx.prof_report()["kernels"]}
-        assert (name + "_pipe" if pipe else name) in names, names
+        want = f"{name}_pipe {M}x{N}x{K}" if pipe else f"{name} {M}x{N}x{K}"
+        assert want in names, names
         C, cs = out if colsum else (out, None)
         np.testing.assert_array_equal(C, (A.astype(np.int64) @ B.astype(np.int64)).astype(np.float32))
         if cs is not None:
             np.testing.assert_array_equal(cs, O.sum_to_shape(B, (1, N)).reshape(N))
 
 
-def test_gemm_epilogues_match_composed_ops(ctx):
+@pytest.mark.parametrize("M,N,K", [(200, 300, 150), (200, 300, 152), (256, 384, 128)])
+def test_gemm_epilogues_match_composed_ops(ctx, M, N, K):
+    """Generic kernel (K = 150), pipelined kernel with edge tiles (152) and aligned (128)."""
     rng = np.random.default_rng(5)
-    M, N, K = 200, 300, 150
     A = rng.standard_normal((M, K)).astype(np.float32)
     B = rng.standard_normal((K, N)).astype(np.float32)
     bias = rng.standard_normal(N).astype(np.float32)
@@ -113,7 +120,8 @@ def test_gemm_epilogues_match_composed_ops(ctx):
 
 
 @pytest.mark.parametrize("M,N,K,exact", [(128, 256, 64, True), (784, 4096, 1024, True), (4096, 10, 1024, False),
-                                         (33, 70, 5, True), (512, 384, 96, True), (128, 128, 4096, False)])
+                                         (33, 70, 5, True), (512, 384, 96, True), (128, 128, 4096, False),
+                                         (784, 4092, 1020, True), (132, 260, 36, True)])
 def test_gemm_colsum_is_bias_gradient(ctx, M, N, K, exact):
     """dW = X^T dY with the bias column sum fused.  With one K-chunk per tile
     the column sum equals sum_to_shape(dY, [1, N]) bit for bit (same ascending
