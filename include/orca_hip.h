@@ -208,6 +208,23 @@ int orca_hip_gemm(orca_hip_ctx* ctx, int trans_a, int trans_b, size_t M, size_t 
 int orca_hip_softmax_ce(orca_hip_ctx* ctx, const float* logits, size_t B, size_t C, const float* onehot,
                         const int32_t* labels, float* loss, float* dlogits, int32_t* preds, int64_t* correct);
 
+/* Fused classifier head, forward: the last nn.Linear when it has at most 16
+ * outputs, logits[B][C] = H[B][K] W[K][C] + bias (python/orca/nn/linear.py:77-86),
+ * followed by everything orca_hip_softmax_ce computes (loss, dlogits, preds,
+ * correct; each optional except logits), in one kernel that streams H once.
+ * Requires 1 <= C <= 16, K a multiple of 4, H and W 16-byte aligned. */
+int orca_hip_head_forward_ce(orca_hip_ctx* ctx, const float* H, size_t B, size_t K, const float* W,
+                             const float* bias, size_t C, const float* onehot, const int32_t* labels, float* logits,
+                             float* loss, float* dlogits, int32_t* preds, int64_t* correct);
+/* Its backward in one kernel that streams H once: dW[K][C] = H^T dlogits
+ * (MatMulBackward, orca-autograd/src/backend.rs:1449-1499), db[C] = column sums
+ * of dlogits (optional; ExpandBackward's sum_to_shape, 1684-1697) and, when
+ * dH != NULL, dH[B][K] = dlogits W^T, times [H > 0] if relu_mask (ReluBackward
+ * of the layer below, 1624-1646: H is its output).  Same shape rules as the
+ * forward; dH 16-byte aligned. */
+int orca_hip_head_backward(orca_hip_ctx* ctx, const float* H, size_t B, size_t K, const float* W, size_t C,
+                           const float* dlogits, int relu_mask, float* dH, float* dW, float* db);
+
 /* dpre = grad * [pre > 0] and, if colsum != NULL, colsum[n] = sum over rows of
  * dpre (ReluBackward + the bias ExpandBackward's sum_to_shape,
  * orca-autograd/src/backend.rs:1633-1645, 1684-1697). */

@@ -124,6 +124,8 @@ SIGNATURES = {
     "orca_hip_has_nan_or_inf": [_P, _P, _SZ, _I, ctypes.POINTER(_I)],
     "orca_hip_gemm": [_P, _I, _I, _SZ, _SZ, _SZ, _P, _SZ, _P, _SZ, _P, _SZ, ctypes.POINTER(Epilogue)],
     "orca_hip_softmax_ce": [_P, _P, _SZ, _SZ, _P, _P, _P, _P, _P, _P],
+    "orca_hip_head_forward_ce": [_P, _P, _SZ, _SZ, _P, _P, _SZ, _P, _P, _P, _P, _P, _P, _P],
+    "orca_hip_head_backward": [_P, _P, _SZ, _SZ, _P, _SZ, _P, _I, _P, _P, _P],
     "orca_hip_relu_bw_colsum": [_P, _P, _P, _SZ, _SZ, _P, _P],
     "orca_hip_adamw_step": [_P, _P, _P, _P, _P, _SZ, _D, _D, _D, _D, _D, ctypes.c_int64],
     "orca_hip_sgd_step": [_P, _P, _P, _SZ, _D],

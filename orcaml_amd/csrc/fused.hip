@@ -9,67 +9,14 @@
 #include <cfloat>
 #include <cmath>
 
+#include "ce_row.hpp"
 #include "runtime.hpp"
 
 namespace orca_hip {
 namespace {
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = v + __shfl_xor(v, o, 64);
-  return v;
-}
-
-__device__ __forceinline__ float wave_max(float v) {  // strict `>`: NaN never wins
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    float w = __shfl_xor(v, o, 64);
-    if (w > v) v = w;
-  }
-  return v;
-}
-
-// Largest value, ties to the lowest index (idx = INT_MAX marks "no candidate").
-__device__ __forceinline__ void wave_argmax(float& v, int& idx) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    float w = __shfl_xor(v, o, 64);
-    int wi = __shfl_xor(idx, o, 64);
-    if (wi != INT_MAX && (idx == INT_MAX || w > v || (w == v && wi < idx))) {
-      v = w;
-      idx = wi;
-    }
-  }
-}
-
-// Row argmax with the reference's sequential rule (python/orca/nn/model.py:65-75):
-// best starts at r[0]; a later value replaces it only if strictly greater.
-// Lanes propose their first strict maximum over c >= 1 (NaN never proposes);
-// the winner beats r[0] only if strictly greater, and a NaN r[0] is never beaten.
-template <int VPL, class Get>
-__device__ __forceinline__ int row_argmax(Get get, int C) {
-  const int lane = threadIdx.x & 63;
-  float bv = -INFINITY;
-  int bi = INT_MAX;
-#pragma unroll
-  for (int j = 0; j < VPL; ++j) {
-    int c = lane + 64 * j;
-    if (c >= 1 && c < C) {
-      float v = get(j);
-      if (v == v && (bi == INT_MAX || v > bv)) {
-        bv = v;
-        bi = c;
-      }
-    }
-  }
-  wave_argmax(bv, bi);
-  const float first = __shfl(get(0), 0, 64);
-  if (bi == INT_MAX) return 0;
-  return (bv > first) ? bi : 0;
-}
-
-// Logits and exp(logits - max) stay in registers (VPL values per lane,
-// column c = lane + 64 j); targets are re-read (one-hot) or derived (labels).
+// Logits stay in registers (VPL values per lane, column c = lane + 64 j);
+// targets are re-read (one-hot) or derived (labels).
 template <int VPL>
 __global__ void __launch_bounds__(256) softmax_ce_kernel(const float* __restrict__ logits, int B, int C,
                                                          const float* __restrict__ onehot,
@@ -87,80 +34,18 @@ __global__ void __launch_bounds__(256) softmax_ce_kernel(const float* __restrict
     if (c >= C) return 0.0f;
     return tr ? tr[c] : (c == label ? 1.0f : 0.0f);
   };
-  float x[VPL], e[VPL];
+  float x[VPL];
 #pragma unroll
   for (int j = 0; j < VPL; ++j) {
     int c = lane + 64 * j;
     x[j] = c < C ? xr[c] : 0.0f;
   }
-
-  // max_to_shape (init -FLT_MAX, strict >)
-  float mx = -FLT_MAX;
-#pragma unroll
-  for (int j = 0; j < VPL; ++j)
-    if (lane + 64 * j < C && x[j] > mx) mx = x[j];
-  mx = wave_max(mx);
-  // exp(p - max) and its row sum
-  float se = 0.0f;
-#pragma unroll
-  for (int j = 0; j < VPL; ++j) {
-    e[j] = (lane + 64 * j < C) ? expf(x[j] - mx) : 0.0f;
-    se = se + e[j];
-  }
-  se = wave_sum(se);
-  const float lg = logf(fmaxf(se, 1e-7f));
-  const float lse = mx + lg;
-  // per-row loss: sum_c -(t * (p - lse))
-  float pb = 0.0f;
-#pragma unroll
-  for (int j = 0; j < VPL; ++j)
-    if (lane + 64 * j < C) pb = pb + (tval(j) * (x[j] - lse)) * -1.0f;
-  pb = wave_sum(pb);
-
-  if (dlogits) {
-    // The tape's gradient through the composition, element by element
-    // (seed 1 * (1/B), then -1, * target, the identity expands' 0 + g, ...).
-    const float g_tm = inv_b * -1.0f;
-    float gse = 0.0f;
-#pragma unroll
-    for (int j = 0; j < VPL; ++j)
-      if (lane + 64 * j < C) {
-        float g_lse = 0.0f + ((g_tm * tval(j)) * -1.0f);
-        gse = gse + (0.0f + g_lse) / se;
-      }
-    gse = wave_sum(gse);
-    float gmx = 0.0f;
-#pragma unroll
-    for (int j = 0; j < VPL; ++j)
-      if (lane + 64 * j < C) {
-        float g_lse = 0.0f + ((g_tm * tval(j)) * -1.0f);
-        float g_sh = gse * e[j];
-        gmx = gmx + ((0.0f + g_lse) + (0.0f + (g_sh * -1.0f)));
-      }
-    gmx = wave_sum(gmx);
-    float* dr = dlogits + (int64_t)row * C;
-#pragma unroll
-    for (int j = 0; j < VPL; ++j) {
-      int c = lane + 64 * j;
-      if (c < C) {
-        float g_ls = g_tm * tval(j);
-        float g_sh = gse * e[j];
-        float d = (0.0f + g_ls) + (0.0f + g_sh);
-        float g3 = 0.0f;
-        if (x[j] == mx) g3 = g3 + gmx;
-        dr[c] = d + g3;
-      }
-    }
-  }
-
-  if (lane == 0) row_loss[row] = pb;
-  if (preds || row_correct) {
-    int pred = row_argmax<VPL>([&](int j) { return x[j]; }, C);
-    int tcls = labels ? label : row_argmax<VPL>(tval, C);
-    if (lane == 0) {
-      if (preds) preds[row] = pred;
-      if (row_correct) row_correct[row] = (pred == tcls) ? 1 : 0;
-    }
+  const CeRowOut r = ce_row<VPL>(x, C, tval, labels != nullptr, label, inv_b,
+                                 dlogits ? dlogits + (int64_t)row * C : nullptr, preds || row_correct);
+  if (lane == 0) {
+    row_loss[row] = r.loss;
+    if (preds) preds[row] = r.pred;
+    if (row_correct) row_correct[row] = (r.pred == r.target) ? 1 : 0;
   }
 }
 

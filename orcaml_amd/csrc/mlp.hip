@@ -13,8 +13,14 @@
 //   backward  L GEMMs dW = A^T dZ with the bias column sum fused in, and
 //             L-1 GEMMs dZ_prev = (dZ W^T) * [H > 0] with the mask fused in
 //   update    one AdamW or SGD pass over the whole parameter arena.
+// When the last layer has at most 16 outputs (a classifier), its three
+// products and the loss are HBM-bound rather than GEMM-shaped; they run as
+// the two fused head kernels instead (forward + loss, and backward), each
+// streaming the layer's input once.  ORCA_HIP_FUSED_HEAD=0 at creation keeps
+// the GEMM + softmax-CE path (A/B comparisons).
 // Every buffer is allocated at creation; a step allocates nothing (split-K
 // workspaces come from the context's cache) and never synchronises.
+#include <cstdlib>
 #include <cstring>
 #include <vector>
 
@@ -42,6 +48,8 @@ struct orca_hip_mlp {
   int32_t* preds = nullptr;
   std::vector<void*> owned;
   bool have_batch = false;
+  bool fused_head = false;
+  orca_hip::HeadWorkspace head;
 
   float* dev(size_t n) {
     void* p = ctx->alloc.allocate(n * sizeof(float) + 256, ctx->stream);
@@ -59,8 +67,9 @@ namespace {
 void step(orca_hip_mlp* m) {
   orca_hip_ctx* ctx = m->ctx;
   const size_t L = m->L, B = m->B, C = m->dims[L];
+  const size_t n_gemm = m->fused_head ? L - 1 : L;  // layers run as GEMMs
   // ---- forward ----
-  for (size_t l = 0; l < L; ++l) {
+  for (size_t l = 0; l < n_gemm; ++l) {
     const size_t K = m->dims[l], N = m->dims[l + 1];
     const float* a = l == 0 ? m->x : m->H[l - 1];
     GemmEpi e;
@@ -69,13 +78,30 @@ void step(orca_hip_mlp* m) {
     float* out = l + 1 < L ? m->H[l] : m->logits;
     gemm(ctx, false, false, B, N, K, a, K, 0, m->P + m->off[2 * l], N, 0, out, N, 0, 1, e);
   }
-  // ---- loss and its gradient ----
-  softmax_ce(ctx, m->logits, B, C, m->onehot, m->onehot ? nullptr : m->labels, m->loss, m->dlogits, m->preds,
-             m->correct);
+  // ---- loss and its gradient (with the last layer when it is a fused head) ----
+  const int32_t* labels = m->onehot ? nullptr : m->labels;
+  if (m->fused_head) {
+    const size_t l = L - 1;
+    head_forward(ctx, l == 0 ? m->x : m->H[l - 1], B, m->dims[l], m->P + m->off[2 * l], m->P + m->off[2 * l + 1], C,
+                 m->onehot, labels, m->logits, m->dlogits, m->preds, m->head);
+  } else {
+    softmax_ce(ctx, m->logits, B, C, m->onehot, labels, m->loss, m->dlogits, m->preds, m->correct);
+  }
   // ---- backward ----
   const float* g = m->dlogits;
   int ping = 0;
-  for (size_t l = L; l-- > 0;) {
+  if (m->fused_head) {
+    const size_t l = L - 1;
+    float* dz = l > 0 ? m->dz[ping] : nullptr;
+    // The backward kernel also adds the forward's row terms into the loss.
+    head_backward(ctx, l == 0 ? m->x : m->H[l - 1], B, m->dims[l], m->P + m->off[2 * l], C, m->dlogits, l > 0, dz,
+                  m->G + m->off[2 * l], m->G + m->off[2 * l + 1], &m->head, m->loss, m->correct);
+    if (dz) {
+      g = dz;
+      ping ^= 1;
+    }
+  }
+  for (size_t l = n_gemm; l-- > 0;) {
     const size_t K = m->dims[l], N = m->dims[l + 1];
     const float* a = l == 0 ? m->x : m->H[l - 1];
     GemmEpi ew;
@@ -173,6 +199,12 @@ int orca_hip_mlp_create(orca_hip_ctx* ctx, const size_t* dims, size_t n_layers, 
     m->loss = m->dev(1);
     m->correct = reinterpret_cast<int64_t*>(m->dev(2));
     m->preds = reinterpret_cast<int32_t*>(m->dev(batch));
+    const char* fh = std::getenv("ORCA_HIP_FUSED_HEAD");
+    m->fused_head = head_supported(batch, dims[n_layers - 1], C) && !(fh && fh[0] == '0');
+    if (m->fused_head) {
+      m->head.row_loss = m->dev(batch);
+      m->head.row_correct = reinterpret_cast<int*>(m->dev(batch));
+    }
     ORCA_HIP_CHECK(hipStreamSynchronize(ctx->stream));
     *out = m.release();
   });

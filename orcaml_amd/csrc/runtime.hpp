@@ -190,6 +190,25 @@ void gemm(orca_hip_ctx* ctx, bool trans_a, bool trans_b, size_t M, size_t N, siz
 void softmax_ce(orca_hip_ctx* ctx, const float* logits, size_t B, size_t C, const float* onehot,
                 const int32_t* labels, float* loss, float* dlogits, int32_t* preds, int64_t* correct);
 
+// Fused classifier head (last Linear with at most HEAD_MAX_CLASSES outputs +
+// softmax cross-entropy); see head.hip.
+constexpr size_t HEAD_MAX_CLASSES = 16;
+struct HeadWorkspace {
+  float* row_loss = nullptr;   // [B] per-row loss terms
+  int* row_correct = nullptr;  // [B] per-row prediction == target
+};
+bool head_supported(size_t B, size_t K, size_t C);
+// logits, dlogits, preds and the per-row terms in ws (no host sync).
+void head_forward(orca_hip_ctx* ctx, const float* H, size_t B, size_t K, const float* W, const float* bias, size_t C,
+                  const float* onehot, const int32_t* labels, float* logits, float* dlogits, int32_t* preds,
+                  const HeadWorkspace& ws);
+// loss = mean of the row terms, correct = their count (one small kernel).
+void head_finish(orca_hip_ctx* ctx, const HeadWorkspace& ws, size_t B, float* loss, int64_t* correct);
+// dW, db, dH; when `finish` is set, also what head_finish computes.
+void head_backward(orca_hip_ctx* ctx, const float* H, size_t B, size_t K, const float* W, size_t C,
+                   const float* dlogits, bool mask, float* dH, float* dW, float* db, const HeadWorkspace* finish,
+                   float* loss, int64_t* correct);
+
 void adamw(orca_hip_ctx* ctx, float* p, const float* g, float* m, float* v, size_t n, double lr, double b1,
            double b2, double eps, double wd, int64_t t);
 void sgd(orca_hip_ctx* ctx, float* p, const float* g, size_t n, double lr);
