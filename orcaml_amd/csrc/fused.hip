@@ -146,19 +146,41 @@ __device__ __forceinline__ void adamw_elem(float& p, float g, float& m, float& v
   v = vn;
 }
 
+// Each thread owns ADAMW_UNROLL float4s of every array per grid-stride step
+// and issues all of their loads before any arithmetic, so a modest grid
+// keeps enough bytes in flight to stream at HBM speed (and leaves CU slots
+// to a concurrently running GEMM).
+constexpr int ADAMW_UNROLL = 4;
+
 __global__ void __launch_bounds__(256) adamw_vec_kernel(float4* __restrict__ p, const float4* __restrict__ g,
                                                         float4* __restrict__ m, float4* __restrict__ v, size_t n4,
                                                         AdamWScalars k) {
-  size_t stride = (size_t)gridDim.x * blockDim.x;
-  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += stride) {
-    float4 pp = p[i], gg = g[i], mm = m[i], vv = v[i];
-    adamw_elem(pp.x, gg.x, mm.x, vv.x, k);
-    adamw_elem(pp.y, gg.y, mm.y, vv.y, k);
-    adamw_elem(pp.z, gg.z, mm.z, vv.z, k);
-    adamw_elem(pp.w, gg.w, mm.w, vv.w, k);
-    p[i] = pp;
-    m[i] = mm;
-    v[i] = vv;
+  const size_t stride = (size_t)gridDim.x * blockDim.x * ADAMW_UNROLL;
+  for (size_t base = (size_t)blockIdx.x * blockDim.x * ADAMW_UNROLL + threadIdx.x; base < n4; base += stride) {
+    float4 pp[ADAMW_UNROLL], gg[ADAMW_UNROLL], mm[ADAMW_UNROLL], vv[ADAMW_UNROLL];
+#pragma unroll
+    for (int u = 0; u < ADAMW_UNROLL; ++u) {
+      const size_t i = base + (size_t)u * blockDim.x;
+      if (i < n4) {
+        pp[u] = p[i];
+        gg[u] = g[i];
+        mm[u] = m[i];
+        vv[u] = v[i];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < ADAMW_UNROLL; ++u) {
+      const size_t i = base + (size_t)u * blockDim.x;
+      if (i < n4) {
+        adamw_elem(pp[u].x, gg[u].x, mm[u].x, vv[u].x, k);
+        adamw_elem(pp[u].y, gg[u].y, mm[u].y, vv[u].y, k);
+        adamw_elem(pp[u].z, gg[u].z, mm[u].z, vv[u].z, k);
+        adamw_elem(pp[u].w, gg[u].w, mm[u].w, vv[u].w, k);
+        p[i] = pp[u];
+        m[i] = mm[u];
+        v[i] = vv[u];
+      }
+    }
   }
 }
 
@@ -228,7 +250,9 @@ void softmax_ce(orca_hip_ctx* ctx, const float* logits, size_t B, size_t C, cons
 }
 
 void adamw(orca_hip_ctx* ctx, float* p, const float* g, float* m, float* v, size_t n, double lr, double b1, double b2,
-           double eps, double wd, int64_t t) {
+           double eps, double wd, int64_t t, hipStream_t stream, unsigned max_blocks) {
+  if (!stream) stream = ctx->stream;
+  if (!max_blocks) max_blocks = ctx->num_cus * 8;
   if (n == 0) return;
   if (t < 1) fail(ORCA_HIP_ERR_INTERNAL, "adamw step count must be >= 1");
   AdamWScalars k;
@@ -241,13 +265,13 @@ void adamw(orca_hip_ctx* ctx, float* p, const float* g, float* m, float* v, size
   k.c2 = (float)(1.0 / (1.0 - std::pow(b2, (double)t)));
   k.eps = (float)eps;
   k.lr = (float)lr;
-  ProfScope ps(ctx, "adamw", 0.0, 28.0 * (double)n);
+  ProfScope ps(ctx, "adamw", 0.0, 28.0 * (double)n, stream);
   size_t done = 0;
   if (aligned16(p) && aligned16(g) && aligned16(m) && aligned16(v)) {
     size_t n4 = n / 4;
     if (n4) {
-      unsigned gsz = grid_for(n4, 256, ctx->num_cus * 8);
-      hipLaunchKernelGGL(adamw_vec_kernel, dim3(gsz), dim3(256), 0, ctx->stream, reinterpret_cast<float4*>(p),
+      unsigned gsz = grid_for((n4 + ADAMW_UNROLL - 1) / ADAMW_UNROLL, 256, max_blocks);
+      hipLaunchKernelGGL(adamw_vec_kernel, dim3(gsz), dim3(256), 0, stream, reinterpret_cast<float4*>(p),
                          reinterpret_cast<const float4*>(g), reinterpret_cast<float4*>(m),
                          reinterpret_cast<float4*>(v), n4, k);
     }
@@ -255,28 +279,29 @@ void adamw(orca_hip_ctx* ctx, float* p, const float* g, float* m, float* v, size
   }
   if (done < n) {
     unsigned gsz = grid_for(n - done, 256, ctx->num_cus * 8);
-    hipLaunchKernelGGL(adamw_scalar_kernel, dim3(gsz), dim3(256), 0, ctx->stream, p, g, m, v, done, n, k);
+    hipLaunchKernelGGL(adamw_scalar_kernel, dim3(gsz), dim3(256), 0, stream, p, g, m, v, done, n, k);
   }
   ORCA_HIP_CHECK(hipGetLastError());
 }
 
-void sgd(orca_hip_ctx* ctx, float* p, const float* g, size_t n, double lr) {
+void sgd(orca_hip_ctx* ctx, float* p, const float* g, size_t n, double lr, hipStream_t stream) {
+  if (!stream) stream = ctx->stream;
   if (n == 0) return;
   const float flr = (float)lr;
-  ProfScope ps(ctx, "sgd", 0.0, 12.0 * (double)n);
+  ProfScope ps(ctx, "sgd", 0.0, 12.0 * (double)n, stream);
   size_t done = 0;
   if (aligned16(p) && aligned16(g)) {
     size_t n4 = n / 4;
     if (n4) {
       unsigned gsz = grid_for(n4, 256, ctx->num_cus * 8);
-      hipLaunchKernelGGL(sgd_vec_kernel, dim3(gsz), dim3(256), 0, ctx->stream, reinterpret_cast<float4*>(p),
+      hipLaunchKernelGGL(sgd_vec_kernel, dim3(gsz), dim3(256), 0, stream, reinterpret_cast<float4*>(p),
                          reinterpret_cast<const float4*>(g), n4, flr);
     }
     done = 4 * n4;
   }
   if (done < n) {
     unsigned gsz = grid_for(n - done, 256, ctx->num_cus * 8);
-    hipLaunchKernelGGL(sgd_scalar_kernel, dim3(gsz), dim3(256), 0, ctx->stream, p, g, done, n, flr);
+    hipLaunchKernelGGL(sgd_scalar_kernel, dim3(gsz), dim3(256), 0, stream, p, g, done, n, flr);
   }
   ORCA_HIP_CHECK(hipGetLastError());
 }

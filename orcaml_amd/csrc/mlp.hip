@@ -17,7 +17,8 @@
 // products and the loss are HBM-bound rather than GEMM-shaped; they run as
 // the two fused head kernels instead (forward + loss, and backward), each
 // streaming the layer's input once.  ORCA_HIP_FUSED_HEAD=0 at creation keeps
-// the GEMM + softmax-CE path (A/B comparisons).
+// the GEMM + softmax-CE path, ORCA_HIP_OVERLAP_UPDATE=0 runs the whole update
+// on the context stream after the backward (A/B comparisons).
 // Every buffer is allocated at creation; a step allocates nothing (split-K
 // workspaces come from the context's cache) and never synchronises.
 #include <cstdlib>
@@ -50,6 +51,10 @@ struct orca_hip_mlp {
   bool have_batch = false;
   bool fused_head = false;
   orca_hip::HeadWorkspace head;
+  // Second stream (default priority) for the update of layers >= 1, which
+  // overlaps the first layer's weight-gradient GEMM; fork / join events.
+  hipStream_t side = nullptr;
+  hipEvent_t fork = nullptr, join = nullptr;
 
   float* dev(size_t n) {
     void* p = ctx->alloc.allocate(n * sizeof(float) + 256, ctx->stream);
@@ -58,6 +63,9 @@ struct orca_hip_mlp {
   }
   ~orca_hip_mlp() {
     for (void* p : owned) ctx->alloc.release(p);
+    if (fork) (void)hipEventDestroy(fork);
+    if (join) (void)hipEventDestroy(join);
+    if (side) (void)hipStreamDestroy(side);
   }
 };
 
@@ -101,9 +109,32 @@ void step(orca_hip_mlp* m) {
       ping ^= 1;
     }
   }
+  // Layers >= 1 are final once the GEMMs of layer 1 have run: their gradients
+  // are complete and no later kernel of the step reads their weights.  With
+  // a side stream, their update then runs concurrently with layer 0's
+  // weight-gradient GEMM (memory-bound beside compute-bound); the step ends
+  // when both streams have finished.
+  const size_t split = L > 1 ? m->off[2] : 0;  // arena offset of W_1
+  bool forked = false;
+  auto update = [&](size_t begin, size_t end, hipStream_t stream) {
+    if (end <= begin) return;
+    if (m->opt.kind == 1)
+      adamw(ctx, m->P + begin, m->G + begin, m->Mo + begin, m->Vo + begin, end - begin, m->opt.lr, m->opt.beta1,
+            m->opt.beta2, m->opt.eps, m->opt.weight_decay, m->t, stream);
+    else
+      sgd(ctx, m->P + begin, m->G + begin, end - begin, m->opt.lr, stream);
+  };
+  if (m->opt.kind == 1) m->t += 1;
   for (size_t l = n_gemm; l-- > 0;) {
     const size_t K = m->dims[l], N = m->dims[l + 1];
     const float* a = l == 0 ? m->x : m->H[l - 1];
+    if (l == 0 && m->side && split > 0) {
+      ORCA_HIP_CHECK(hipEventRecord(m->fork, ctx->stream));
+      ORCA_HIP_CHECK(hipStreamWaitEvent(m->side, m->fork, 0));
+      update(split, m->arena, m->side);
+      ORCA_HIP_CHECK(hipEventRecord(m->join, m->side));
+      forked = true;
+    }
     GemmEpi ew;
     ew.colsum = m->G + m->off[2 * l + 1];  // bias gradient
     gemm(ctx, true, false, K, N, B, a, K, 0, g, N, 0, m->G + m->off[2 * l], N, 0, 1, ew);
@@ -118,13 +149,12 @@ void step(orca_hip_mlp* m) {
       ping ^= 1;
     }
   }
-  // ---- update (parameter order W_0, b_0, W_1, ...; one pass over the arena) ----
-  if (m->opt.kind == 1) {
-    m->t += 1;
-    adamw(ctx, m->P, m->G, m->Mo, m->Vo, m->arena, m->opt.lr, m->opt.beta1, m->opt.beta2, m->opt.eps,
-          m->opt.weight_decay, m->t);
+  // ---- update (parameter order W_0, b_0, W_1, ...; flat passes over the arena) ----
+  if (forked) {
+    update(0, split, ctx->stream);
+    ORCA_HIP_CHECK(hipStreamWaitEvent(ctx->stream, m->join, 0));
   } else {
-    sgd(ctx, m->P, m->G, m->arena, m->opt.lr);
+    update(0, m->arena, ctx->stream);
   }
 }
 
@@ -199,6 +229,12 @@ int orca_hip_mlp_create(orca_hip_ctx* ctx, const size_t* dims, size_t n_layers, 
     m->loss = m->dev(1);
     m->correct = reinterpret_cast<int64_t*>(m->dev(2));
     m->preds = reinterpret_cast<int32_t*>(m->dev(batch));
+    const char* ov = std::getenv("ORCA_HIP_OVERLAP_UPDATE");
+    if (n_layers > 1 && !(ov && ov[0] == '0')) {
+      ORCA_HIP_CHECK(hipStreamCreateWithFlags(&m->side, hipStreamNonBlocking));
+      ORCA_HIP_CHECK(hipEventCreateWithFlags(&m->fork, hipEventDisableTiming));
+      ORCA_HIP_CHECK(hipEventCreateWithFlags(&m->join, hipEventDisableTiming));
+    }
     const char* fh = std::getenv("ORCA_HIP_FUSED_HEAD");
     m->fused_head = head_supported(batch, dims[n_layers - 1], C) && !(fh && fh[0] == '0');
     if (m->fused_head) {

@@ -148,20 +148,20 @@ Profiler::~Profiler() {
   for (auto e : pool) (void)hipEventDestroy(e);
 }
 
-ProfScope::ProfScope(orca_hip_ctx* ctx, const char* name, double flops, double bytes)
-    : ctx_(ctx), on_(ctx->prof.enabled) {
+ProfScope::ProfScope(orca_hip_ctx* ctx, const char* name, double flops, double bytes, hipStream_t stream)
+    : ctx_(ctx), stream_(stream ? stream : ctx->stream), on_(ctx->prof.enabled) {
   if (!on_) return;
   rec_.name = name;
   rec_.flops = flops;
   rec_.bytes = bytes;
   rec_.start = ctx->prof.get_event();
   rec_.stop = ctx->prof.get_event();
-  ORCA_HIP_CHECK(hipEventRecord(rec_.start, ctx->stream));
+  ORCA_HIP_CHECK(hipEventRecord(rec_.start, stream_));
 }
 
 ProfScope::~ProfScope() {
   if (!on_) return;
-  if (hipEventRecord(rec_.stop, ctx_->stream) == hipSuccess) ctx_->prof.pending.push_back(rec_);
+  if (hipEventRecord(rec_.stop, stream_) == hipSuccess) ctx_->prof.pending.push_back(rec_);
 }
 
 // ------------------------------------------------------------ small kernels

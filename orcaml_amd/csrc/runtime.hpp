@@ -114,14 +114,16 @@ namespace orca_hip {
 // Makes ctx's device current for the calling thread.
 void bind(orca_hip_ctx* ctx);
 
-// Brackets one launch with events when profiling is on.
+// Brackets one launch with events when profiling is on (on `stream`, the
+// context stream when null).
 class ProfScope {
  public:
-  ProfScope(orca_hip_ctx* ctx, const char* name, double flops, double bytes);
+  ProfScope(orca_hip_ctx* ctx, const char* name, double flops, double bytes, hipStream_t stream = nullptr);
   ~ProfScope();
 
  private:
   orca_hip_ctx* ctx_;
+  hipStream_t stream_;
   Profiler::Pending rec_;
   bool on_;
 };
@@ -209,8 +211,10 @@ void head_backward(orca_hip_ctx* ctx, const float* H, size_t B, size_t K, const 
                    const float* dlogits, bool mask, float* dH, float* dW, float* db, const HeadWorkspace* finish,
                    float* loss, int64_t* correct);
 
+// Optimizer passes over flat buffers, on `stream` (the context stream when null).
+// max_blocks caps the grid-stride grid (0: 8 blocks per CU).
 void adamw(orca_hip_ctx* ctx, float* p, const float* g, float* m, float* v, size_t n, double lr, double b1,
-           double b2, double eps, double wd, int64_t t);
-void sgd(orca_hip_ctx* ctx, float* p, const float* g, size_t n, double lr);
+           double b2, double eps, double wd, int64_t t, hipStream_t stream = nullptr, unsigned max_blocks = 0);
+void sgd(orca_hip_ctx* ctx, float* p, const float* g, size_t n, double lr, hipStream_t stream = nullptr);
 
 }  // namespace orca_hip

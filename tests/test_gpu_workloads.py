@@ -37,29 +37,74 @@ def near_tie_rows(logits_ref: np.ndarray, tol: float) -> np.ndarray:
     return (s[:, -1] - s[:, -2]) <= tol * np.maximum(1.0, np.abs(s[:, -1]))
 
 
+def oracle_hidden(params, x, dims):
+    """The oracle's ReLU outputs of layers 0..L-2 (its own forward pass)."""
+    B = x.shape[0]
+    hs, a = [], x
+    for l in range(len(dims) - 2):
+        a = O.relu(O.add(O.matmul(a, params[2 * l]), O.expand(params[2 * l + 1], (B, dims[l + 1]))))
+        hs.append(a)
+    return hs
+
+
+def mask_flips(tr, hidden):
+    """Per layer, entries whose ReLU mask differs between the GPU's forward and
+    the oracle's (pre-activations within rounding of zero); 0 for the last
+    layer, which has no mask."""
+    return [int(((h > 0) != (tr.activation(l) > 0)).sum()) for l, h in enumerate(hidden)] + [0]
+
+
+def allowed_outliers(i, size, flips, dims):
+    """A flip at (b, j) of layer l's mask changes dZ_l[b, j]: column j of dW_l
+    (dims[l] entries) and entry j of db_l; plus a 1e-5 fraction of slack."""
+    l = i // 2
+    return int(np.ceil(1e-5 * size)) + flips[l] * (dims[l] if i % 2 == 0 else 1)
+
+
 def test_config2_hundred_adamw_steps_teacher_forced(ctx):
     """784-1024-1024-10, batch 256, 100 AdamW(1e-3, wd 0.01) steps on one fixed
     batch.  At every step the oracle takes one step from the GPU's own state
-    (parameters, moments, t) and the step's loss, the new parameters and both
-    moments must agree to the path's tolerance (1e-5 abs + 1e-4 rel) -- the
-    same per-step agreement two valid CPU GEMM orders reach (zero outliers)."""
+    (parameters, moments, t):
+      * the loss agrees to the path's tolerance (1e-5 abs + 1e-4 rel);
+      * every gradient agrees to that tolerance, except entries attributed to
+        counted ReLU mask flips between the two forward passes;
+      * the new parameters and both moments are bit-identical to the oracle's
+        AdamW applied to the GPU's own gradients from the same state (AdamW
+        normalises gradients, so near-cancelling moments would turn rounding-
+        level gradient differences into parameter differences of order lr;
+        the update itself has no rounding freedom)."""
     w = synth.WORKLOADS[2]
-    params, x, labels, onehot = synth.mlp_problem(2, w["dims"], w["batch"])
+    dims = w["dims"]
+    o = w["opt"]
+    params, x, labels, onehot = synth.mlp_problem(2, dims, w["batch"])
     tr = make_trainer(ctx, w, params)
     tr.set_batch(x, onehot=onehot)
-    state = dict(params=params, m=None, v=None, t=0)
+    zeros = [np.zeros_like(p) for p in params]
+    state = dict(params=params, m=zeros, v=zeros, t=0)
+    total_flips = 0
     for step in range(w["steps"]):
         tr.step()
         loss, _ = tr.metrics()
-        ref = O.mlp_train(w["dims"], state["params"], x, onehot, ref_opt(w), steps=1, m=state["m"], v=state["v"],
-                          t=state["t"], want_grads=False)
+        ref = O.mlp_train(dims, state["params"], x, onehot, ref_opt(w), steps=1, m=state["m"], v=state["v"],
+                          t=state["t"], want_grads=True)
         assert_close(loss, ref["losses"][0], what=f"step {step} loss")
-        got_p, got_m, got_v = tr.params(), tr.moments(0), tr.moments(1)
+        flips = mask_flips(tr, oracle_hidden(state["params"], x, dims))
+        total_flips += sum(flips)
+        got_g, got_p, got_m, got_v = tr.grads(), tr.params(), tr.moments(0), tr.moments(1)
+        t = state["t"] + 1
         for i in range(len(got_p)):
-            assert_close(got_p[i], ref["params"][i], what=f"step {step} param {i}")
-            assert_close(got_m[i], ref["m"][i], what=f"step {step} m {i}")
-            assert_close(got_v[i], ref["v"][i], what=f"step {step} v {i}")
-        state = dict(params=got_p, m=got_m, v=got_v, t=ref["t"])
+            n_out = outside_tolerance(got_g[i], ref["grads"][i])
+            allowed = allowed_outliers(i, got_g[i].size, flips, dims)
+            assert n_out <= allowed, (f"step {step} grad {i}: {n_out} of {got_g[i].size} outside tolerance "
+                                      f"(ReLU mask flips {flips}, allowed {allowed})")
+            p1, m1, v1 = O.adamw_update(state["params"][i], got_g[i], state["m"][i], state["v"][i], t, lr=o["lr"],
+                                        weight_decay=o["weight_decay"], betas=o.get("betas", (0.9, 0.999)),
+                                        eps=o.get("eps", 1e-8))
+            np.testing.assert_array_equal(got_p[i], p1, err_msg=f"step {step} param {i}")
+            np.testing.assert_array_equal(got_m[i], m1, err_msg=f"step {step} m {i}")
+            np.testing.assert_array_equal(got_v[i], v1, err_msg=f"step {step} v {i}")
+        state = dict(params=got_p, m=got_m, v=got_v, t=t)
+    print(f"config2 teacher-forced: {total_flips} ReLU mask flips over {w['steps']} steps")
     assert tr.step_count() == state["t"] == 100
 
 
