@@ -212,9 +212,8 @@ void head_backward(orca_hip_ctx* ctx, const float* H, size_t B, size_t K, const 
                    float* loss, int64_t* correct);
 
 // Optimizer passes over flat buffers, on `stream` (the context stream when null).
-// max_blocks caps the grid-stride grid (0: 8 blocks per CU).
 void adamw(orca_hip_ctx* ctx, float* p, const float* g, float* m, float* v, size_t n, double lr, double b1,
-           double b2, double eps, double wd, int64_t t, hipStream_t stream = nullptr, unsigned max_blocks = 0);
+           double b2, double eps, double wd, int64_t t, hipStream_t stream = nullptr);
 void sgd(orca_hip_ctx* ctx, float* p, const float* g, size_t n, double lr, hipStream_t stream = nullptr);
 
 }  // namespace orca_hip
