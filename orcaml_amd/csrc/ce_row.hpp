@@ -13,47 +13,90 @@
 
 namespace orca_hip {
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = v + __shfl_xor(v, o, 64);
-  return v;
+// ---- wave64 reductions on the DPP network (no LDS round trips) ----
+// Steps: quad_perm [1,0,3,2] and [2,3,0,1], row_half_mirror and row_mirror
+// leave every lane of a 16-lane row holding the row's result; row_bcast:15
+// into rows 1 and 3 and row_bcast:31 into rows 2 and 3 then complete it in
+// lane 63, which is broadcast.  Lanes a masked step does not write get `old`,
+// the operation's identity.
+template <int CTRL, int ROWS = 0xf>
+__device__ __forceinline__ int dpp_i(int old, int v) {
+  return __builtin_amdgcn_update_dpp(old, v, CTRL, ROWS, 0xf, false);
+}
+template <int CTRL, int ROWS = 0xf>
+__device__ __forceinline__ float dpp_f(float old, float v) {
+  return __int_as_float(dpp_i<CTRL, ROWS>(__float_as_int(old), __float_as_int(v)));
 }
 
-__device__ __forceinline__ float wave_max(float v) {  // strict `>`: NaN never wins
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    float w = __shfl_xor(v, o, 64);
-    if (w > v) v = w;
-  }
-  return v;
+template <class Op>
+__device__ __forceinline__ float wave_reduce_f(float v, float identity, Op op) {
+  v = op(v, dpp_f<0xb1>(identity, v));
+  v = op(v, dpp_f<0x4e>(identity, v));
+  v = op(v, dpp_f<0x141>(identity, v));
+  v = op(v, dpp_f<0x140>(identity, v));
+  v = op(v, dpp_f<0x142, 0xa>(identity, v));
+  v = op(v, dpp_f<0x143, 0xc>(identity, v));
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+  return wave_reduce_f(v, 0.0f, [](float a, float b) { return a + b; });
+}
+
+// strict `>`: NaN never wins
+__device__ __forceinline__ float wave_max(float v) {
+  return wave_reduce_f(v, -INFINITY, [](float a, float b) { return b > a ? b : a; });
+}
+
+__device__ __forceinline__ int wave_sum_i(int v) {
+  v = v + dpp_i<0xb1>(0, v);
+  v = v + dpp_i<0x4e>(0, v);
+  v = v + dpp_i<0x141>(0, v);
+  v = v + dpp_i<0x140>(0, v);
+  v = v + dpp_i<0x142, 0xa>(0, v);
+  v = v + dpp_i<0x143, 0xc>(0, v);
+  return __builtin_amdgcn_readlane(v, 63);
 }
 
 // Largest value, ties to the lowest index (idx = INT_MAX marks "no candidate").
-__device__ __forceinline__ void wave_argmax(float& v, int& idx) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    float w = __shfl_xor(v, o, 64);
-    int wi = __shfl_xor(idx, o, 64);
-    if (wi != INT_MAX && (idx == INT_MAX || w > v || (w == v && wi < idx))) {
-      v = w;
-      idx = wi;
-    }
+// The combine is a total-order maximum, so any reduction tree gives the same pair.
+__device__ __forceinline__ void argmax_combine(float& v, int& idx, float w, int wi) {
+  if (wi != INT_MAX && (idx == INT_MAX || w > v || (w == v && wi < idx))) {
+    v = w;
+    idx = wi;
   }
+}
+template <int CTRL, int ROWS = 0xf>
+__device__ __forceinline__ void argmax_step(float& v, int& idx) {
+  const float w = dpp_f<CTRL, ROWS>(-INFINITY, v);
+  const int wi = dpp_i<CTRL, ROWS>(INT_MAX, idx);
+  argmax_combine(v, idx, w, wi);
+}
+__device__ __forceinline__ void wave_argmax(float& v, int& idx) {
+  argmax_step<0xb1>(v, idx);
+  argmax_step<0x4e>(v, idx);
+  argmax_step<0x141>(v, idx);
+  argmax_step<0x140>(v, idx);
+  argmax_step<0x142, 0xa>(v, idx);
+  argmax_step<0x143, 0xc>(v, idx);
+  v = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+  idx = __builtin_amdgcn_readlane(idx, 63);
 }
 
 // Row argmax with the reference's sequential rule (python/orca/nn/model.py:65-75):
 // best starts at r[0]; a later value replaces it only if strictly greater.
 // Lanes propose their first strict maximum over c >= 1 (NaN never proposes);
 // the winner beats r[0] only if strictly greater, and a NaN r[0] is never beaten.
-template <int VPL, class Get>
-__device__ __forceinline__ int row_argmax(Get get, int C) {
-  const int lane = threadIdx.x & 63;
+// col(j) is the column of the lane's j-th value, increasing in j; column 0 is
+// lane 0's value 0.
+template <int VPL, class Get, class Col, class Valid>
+__device__ __forceinline__ int row_argmax(Get get, Col col, Valid valid) {
   float bv = -INFINITY;
   int bi = INT_MAX;
 #pragma unroll
   for (int j = 0; j < VPL; ++j) {
-    int c = lane + 64 * j;
-    if (c >= 1 && c < C) {
+    const int c = col(j);
+    if (c >= 1 && valid(j)) {
       float v = get(j);
       if (v == v && (bi == INT_MAX || v > bv)) {
         bv = v;
@@ -62,7 +105,7 @@ __device__ __forceinline__ int row_argmax(Get get, int C) {
     }
   }
   wave_argmax(bv, bi);
-  const float first = __shfl(get(0), 0, 64);
+  const float first = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(get(0)), 0));
   if (bi == INT_MAX) return 0;
   return (bv > first) ? bi : 0;
 }
@@ -73,29 +116,33 @@ struct CeRowOut {
   int target;  // target class (label, or argmax of the one-hot row)
 };
 
-// One row held by one wave64: x[j] is the logit of column lane + 64 j
-// (columns >= C are ignored), tval(j) its target.  Writes the row of
-// dL/dlogits to `dr` when non-null.  Every lane returns the same values.
+// One row held by one wave64: x[j] is the logit of column col(j), used where
+// valid(j) (the column is < C), tval(j) its target.  Writes element j of the row of
+// dL/dlogits through store(j, value) when `grad`.  Every lane returns the
+// same values.
 //
 // The gradient is the tape's, element by element, through the 22-node
 // composition (seed * (1/B), * -1, * target, the identity expands' 0 + g,
 // the g / see of LogBackward, the full-gradient-to-ties MaxToShapeBackward).
-template <int VPL, class TVal>
-__device__ __forceinline__ CeRowOut ce_row(const float (&x)[VPL], int C, TVal tval, bool labels, int label, float inv_b,
-                                           float* __restrict__ dr, bool want_argmax) {
-  const int lane = threadIdx.x & 63;
+// LogBackward's row sum sum_c (0 + g_lse_c) / se is taken as
+// (sum_c (0 + g_lse_c)) / se when se is finite and positive: for one-hot
+// targets only the target's term is nonzero, so the two are the same f32
+// value; other rows keep one division per element.
+template <int VPL, class TVal, class Col, class Valid, class Store>
+__device__ __forceinline__ CeRowOut ce_row(const float (&x)[VPL], Valid valid, TVal tval, Col col, bool labels,
+                                           int label, float inv_b, bool grad, Store store, bool want_argmax) {
   float e[VPL];
   // max_to_shape (init -FLT_MAX, strict >)
   float mx = -FLT_MAX;
 #pragma unroll
   for (int j = 0; j < VPL; ++j)
-    if (lane + 64 * j < C && x[j] > mx) mx = x[j];
+    if (valid(j) && x[j] > mx) mx = x[j];
   mx = wave_max(mx);
   // exp(p - max) and its row sum
   float se = 0.0f;
 #pragma unroll
   for (int j = 0; j < VPL; ++j) {
-    e[j] = (lane + 64 * j < C) ? expf(x[j] - mx) : 0.0f;
+    e[j] = valid(j) ? expf(x[j] - mx) : 0.0f;
     se = se + e[j];
   }
   se = wave_sum(se);
@@ -105,23 +152,30 @@ __device__ __forceinline__ CeRowOut ce_row(const float (&x)[VPL], int C, TVal tv
   float pb = 0.0f;
 #pragma unroll
   for (int j = 0; j < VPL; ++j)
-    if (lane + 64 * j < C) pb = pb + (tval(j) * (x[j] - lse)) * -1.0f;
+    if (valid(j)) pb = pb + (tval(j) * (x[j] - lse)) * -1.0f;
   pb = wave_sum(pb);
 
-  if (dr) {
+  if (grad) {
     const float g_tm = inv_b * -1.0f;
     float gse = 0.0f;
+    if (se > 0.0f && se <= FLT_MAX) {
 #pragma unroll
-    for (int j = 0; j < VPL; ++j)
-      if (lane + 64 * j < C) {
-        float g_lse = 0.0f + ((g_tm * tval(j)) * -1.0f);
-        gse = gse + (0.0f + g_lse) / se;
-      }
-    gse = wave_sum(gse);
+      for (int j = 0; j < VPL; ++j)
+        if (valid(j)) gse = gse + (0.0f + (0.0f + ((g_tm * tval(j)) * -1.0f)));
+      gse = wave_sum(gse) / se;
+    } else {
+#pragma unroll
+      for (int j = 0; j < VPL; ++j)
+        if (valid(j)) {
+          float g_lse = 0.0f + ((g_tm * tval(j)) * -1.0f);
+          gse = gse + (0.0f + g_lse) / se;
+        }
+      gse = wave_sum(gse);
+    }
     float gmx = 0.0f;
 #pragma unroll
     for (int j = 0; j < VPL; ++j)
-      if (lane + 64 * j < C) {
+      if (valid(j)) {
         float g_lse = 0.0f + ((g_tm * tval(j)) * -1.0f);
         float g_sh = gse * e[j];
         gmx = gmx + ((0.0f + g_lse) + (0.0f + (g_sh * -1.0f)));
@@ -129,22 +183,21 @@ __device__ __forceinline__ CeRowOut ce_row(const float (&x)[VPL], int C, TVal tv
     gmx = wave_sum(gmx);
 #pragma unroll
     for (int j = 0; j < VPL; ++j) {
-      int c = lane + 64 * j;
-      if (c < C) {
+      if (valid(j)) {
         float g_ls = g_tm * tval(j);
         float g_sh = gse * e[j];
         float d = (0.0f + g_ls) + (0.0f + g_sh);
         float g3 = 0.0f;
         if (x[j] == mx) g3 = g3 + gmx;
-        dr[c] = d + g3;
+        store(j, d + g3);
       }
     }
   }
 
   CeRowOut out{pb, 0, 0};
   if (want_argmax) {
-    out.pred = row_argmax<VPL>([&](int j) { return x[j]; }, C);
-    out.target = labels ? label : row_argmax<VPL>(tval, C);
+    out.pred = row_argmax<VPL>([&](int j) { return x[j]; }, col, valid);
+    out.target = labels ? label : row_argmax<VPL>(tval, col, valid);
   }
   return out;
 }

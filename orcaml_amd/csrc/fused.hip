@@ -17,9 +17,13 @@ namespace {
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
-// Logits stay in registers (VPL values per lane, column c = lane + 64 j);
-// targets are re-read (one-hot) or derived (labels).
-template <int VPL>
+// One wave per row.  Logits stay in registers, VPL values per lane: column
+// c = lane + 64 j (scalar loads), or, when VEC (C a multiple of 4 and 16-byte
+// aligned rows), c = 256 (j / 4) + 4 lane + j % 4 so that logits and the
+// gradient move as float4s with non-temporal loads / stores (each is touched
+// once).  FULL: C == 64 VPL, every slot is a column (no bounds checks).
+// LABELS: class-index targets (compared), else one-hot rows (read where used).
+template <int VPL, bool VEC, bool FULL, bool LABELS>
 __global__ void __launch_bounds__(256) softmax_ce_kernel(const float* __restrict__ logits, int B, int C,
                                                          const float* __restrict__ onehot,
                                                          const int32_t* __restrict__ labels, float inv_b,
@@ -29,21 +33,44 @@ __global__ void __launch_bounds__(256) softmax_ce_kernel(const float* __restrict
   const int row = blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6);
   if (row >= B) return;
   const float* xr = logits + (int64_t)row * C;
-  const float* tr = onehot ? onehot + (int64_t)row * C : nullptr;
-  const int label = labels ? labels[row] : -1;
+  const float* tr = LABELS ? nullptr : onehot + (int64_t)row * C;
+  float* dr = dlogits ? dlogits + (int64_t)row * C : nullptr;
+  const int label = LABELS ? labels[row] : -1;
+  auto col = [&](int j) -> int { return VEC ? (j >> 2) * 256 + lane * 4 + (j & 3) : lane + 64 * j; };
+  auto valid = [&](int j) -> bool { return FULL || col(j) < C; };
   auto tval = [&](int j) -> float {
-    int c = lane + 64 * j;
-    if (c >= C) return 0.0f;
-    return tr ? tr[c] : (c == label ? 1.0f : 0.0f);
+    if (!valid(j)) return 0.0f;
+    return LABELS ? (col(j) == label ? 1.0f : 0.0f) : tr[col(j)];
   };
   float x[VPL];
+  if (VEC) {
 #pragma unroll
-  for (int j = 0; j < VPL; ++j) {
-    int c = lane + 64 * j;
-    x[j] = c < C ? xr[c] : 0.0f;
+    for (int q = 0; q < VPL / 4; ++q) {
+      const int c0 = q * 256 + lane * 4;
+      floatx4 v = {0.0f, 0.0f, 0.0f, 0.0f};
+      if (FULL || c0 < C) v = __builtin_nontemporal_load(reinterpret_cast<const floatx4*>(xr + c0));
+      x[4 * q] = v.x;
+      x[4 * q + 1] = v.y;
+      x[4 * q + 2] = v.z;
+      x[4 * q + 3] = v.w;
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) x[j] = valid(j) ? xr[col(j)] : 0.0f;
   }
-  const CeRowOut r = ce_row<VPL>(x, C, tval, labels != nullptr, label, inv_b,
-                                 dlogits ? dlogits + (int64_t)row * C : nullptr, preds || row_correct);
+  float buf[4];
+  auto store = [&](int j, float v) {
+    if (VEC) {
+      buf[j & 3] = v;
+      if ((j & 3) == 3)
+        __builtin_nontemporal_store(floatx4{buf[0], buf[1], buf[2], buf[3]},
+                                    reinterpret_cast<floatx4*>(dr + col(j) - 3));
+    } else {
+      dr[col(j)] = v;
+    }
+  };
+  const CeRowOut r = ce_row<VPL>(x, valid, tval, col, LABELS, label, inv_b, dr != nullptr, store,
+                                 preds || row_correct);
   if (lane == 0) {
     row_loss[row] = r.loss;
     if (preds) preds[row] = r.pred;
@@ -84,7 +111,11 @@ __global__ void __launch_bounds__(1024) ce_finish_kernel(const float* __restrict
   }
 }
 
-// dpre = pre > 0 ? g : 0 and per-chunk column partial sums (4 columns per thread).
+// dpre = pre > 0 ? g : 0 and per-chunk column partial sums (4 columns per
+// thread).  Rows go RB_UNROLL at a time, all loads issued before any use;
+// g, pre and dpre are streamed with non-temporal accesses.
+constexpr int RB_UNROLL = 8;
+
 __global__ void __launch_bounds__(256) relu_bw_colsum_vec_kernel(const float4* __restrict__ g, const float4* __restrict__ pre,
                                                                  size_t rows, size_t cols4, int rows_per_chunk,
                                                                  float4* __restrict__ dpre, float4* __restrict__ partial) {
@@ -92,16 +123,34 @@ __global__ void __launch_bounds__(256) relu_bw_colsum_vec_kernel(const float4* _
   if (c >= cols4) return;
   size_t r0 = (size_t)blockIdx.y * rows_per_chunk;
   size_t r1 = r0 + rows_per_chunk < rows ? r0 + rows_per_chunk : rows;
+  const floatx4* gv = reinterpret_cast<const floatx4*>(g);
+  const floatx4* pv = reinterpret_cast<const floatx4*>(pre);
+  floatx4* dv = reinterpret_cast<floatx4*>(dpre);
   float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
-  for (size_t r = r0; r < r1; ++r) {
-    float4 gv = g[r * cols4 + c], pv = pre[r * cols4 + c];
-    float4 d = make_float4(pv.x > 0.0f ? gv.x : 0.0f, pv.y > 0.0f ? gv.y : 0.0f, pv.z > 0.0f ? gv.z : 0.0f,
-                           pv.w > 0.0f ? gv.w : 0.0f);
-    dpre[r * cols4 + c] = d;
-    s.x = s.x + d.x;
-    s.y = s.y + d.y;
-    s.z = s.z + d.z;
-    s.w = s.w + d.w;
+  for (size_t rb = r0; rb < r1; rb += RB_UNROLL) {
+    floatx4 ga[RB_UNROLL], pa[RB_UNROLL];
+#pragma unroll
+    for (int u = 0; u < RB_UNROLL; ++u) {
+      const size_t r = rb + u;
+      if (r < r1) {
+        ga[u] = __builtin_nontemporal_load(gv + r * cols4 + c);
+        pa[u] = __builtin_nontemporal_load(pv + r * cols4 + c);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < RB_UNROLL; ++u) {
+      const size_t r = rb + u;
+      if (r < r1) {
+        const floatx4 gg = ga[u], pp = pa[u];
+        const floatx4 d = {pp.x > 0.0f ? gg.x : 0.0f, pp.y > 0.0f ? gg.y : 0.0f, pp.z > 0.0f ? gg.z : 0.0f,
+                           pp.w > 0.0f ? gg.w : 0.0f};
+        __builtin_nontemporal_store(d, dv + r * cols4 + c);
+        s.x = s.x + d.x;
+        s.y = s.y + d.y;
+        s.z = s.z + d.z;
+        s.w = s.w + d.w;
+      }
+    }
   }
   if (partial) partial[(size_t)blockIdx.y * cols4 + c] = s;
 }
@@ -122,12 +171,20 @@ __global__ void __launch_bounds__(256) relu_bw_colsum_scalar_kernel(const float*
   if (partial) partial[(size_t)blockIdx.y * cols + c] = s;
 }
 
-// colsum[c] = sum over chunks (in chunk order) of partial[chunk][c].
+// colsum[c] = sum over chunks (in chunk order) of partial[chunk][c]; the
+// loads of RB_UNROLL chunks are issued before their adds.
 __global__ void chunk_reduce_kernel(const float* __restrict__ partial, int chunks, size_t cols, float* __restrict__ out) {
   size_t c = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (c >= cols) return;
   float s = 0.0f;
-  for (int k = 0; k < chunks; ++k) s = s + partial[(size_t)k * cols + c];
+  for (int k0 = 0; k0 < chunks; k0 += RB_UNROLL) {
+    float v[RB_UNROLL];
+#pragma unroll
+    for (int u = 0; u < RB_UNROLL; ++u) v[u] = k0 + u < chunks ? partial[(size_t)(k0 + u) * cols + c] : 0.0f;
+#pragma unroll
+    for (int u = 0; u < RB_UNROLL; ++u)
+      if (k0 + u < chunks) s = s + v[u];
+  }
   out[c] = s;
 }
 
@@ -219,13 +276,30 @@ void softmax_ce(orca_hip_ctx* ctx, const float* logits, size_t B, size_t C, cons
   int* rc = correct ? row_correct.as<int>() : nullptr;
   {
     ProfScope ps(ctx, "softmax_ce", 0.0, 4.0 * (double)B * C * (dlogits ? 2 : 1) + 4.0 * B);
-#define CE_LAUNCH(VPL)                                                                                      \
-  hipLaunchKernelGGL(softmax_ce_kernel<VPL>, grid, dim3(256), 0, ctx->stream, logits, (int)B, (int)C, onehot, \
-                     labels, inv_b, row_loss.as<float>(), dlogits, preds, rc)
-    if (C <= 64) CE_LAUNCH(1);
-    else if (C <= 256) CE_LAUNCH(4);
-    else if (C <= 1024) CE_LAUNCH(16);
-    else CE_LAUNCH(64);
+#define CE_LAUNCH(VPL, VEC, FULL)                                                                           \
+  do {                                                                                                      \
+    if (labels)                                                                                             \
+      hipLaunchKernelGGL((softmax_ce_kernel<VPL, VEC, FULL, true>), grid, dim3(256), 0, ctx->stream, logits, \
+                         (int)B, (int)C, onehot, labels, inv_b, row_loss.as<float>(), dlogits, preds, rc);   \
+    else                                                                                                    \
+      hipLaunchKernelGGL((softmax_ce_kernel<VPL, VEC, FULL, false>), grid, dim3(256), 0, ctx->stream, logits, \
+                         (int)B, (int)C, onehot, labels, inv_b, row_loss.as<float>(), dlogits, preds, rc);   \
+  } while (0)
+    const bool vec = C % 4 == 0 && aligned16(logits) && (!dlogits || aligned16(dlogits));
+    if (C <= 64) {
+      if (C == 64) CE_LAUNCH(1, false, true);
+      else CE_LAUNCH(1, false, false);
+    } else if (C <= 256) {
+      if (vec) CE_LAUNCH(4, true, false);
+      else CE_LAUNCH(4, false, false);
+    } else if (C <= 1024) {
+      if (vec) CE_LAUNCH(16, true, false);
+      else CE_LAUNCH(16, false, false);
+    } else {
+      if (vec && C == 4096) CE_LAUNCH(64, true, true);
+      else if (vec) CE_LAUNCH(64, true, false);
+      else CE_LAUNCH(64, false, false);
+    }
 #undef CE_LAUNCH
     ORCA_HIP_CHECK(hipGetLastError());
   }

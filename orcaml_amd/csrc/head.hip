@@ -98,8 +98,7 @@ __device__ void finish_rows(const float* __restrict__ row_loss, const int* __res
     }
   }
   s = wave_sum(s);
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) n += __shfl_xor(n, o, 64);
+  n = wave_sum_i(n);
   if (lane == 0) {
     red_f[wave] = s;
     red_i[wave] = n;
@@ -238,8 +237,10 @@ __global__ void __launch_bounds__(HEAD_THREADS) head_forward_kernel(HeadFwdParam
       if (c >= C) return 0.0f;
       return tr ? tr[c] : (c == label ? 1.0f : 0.0f);
     };
-    const CeRowOut o = ce_row<1>(x, C, tval, p.labels != nullptr, label, p.inv_b,
-                                 p.dlogits ? p.dlogits + (int64_t)row * C : nullptr, true);
+    float* dr = p.dlogits ? p.dlogits + (int64_t)row * C : nullptr;
+    const CeRowOut o = ce_row<1>(
+        x, [&](int) { return lane < C; }, tval, [&](int j) { return lane + 64 * j; }, p.labels != nullptr, label,
+        p.inv_b, dr != nullptr, [&](int, float v) { dr[lane] = v; }, true);
     if (lane == 0) {
       p.row_loss[row] = o.loss;
       p.row_correct[row] = o.pred == o.target ? 1 : 0;
