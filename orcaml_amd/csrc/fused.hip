@@ -378,6 +378,13 @@ int orca_hip_softmax_ce(orca_hip_ctx* ctx, const float* logits, size_t B, size_t
                         const int32_t* labels, float* loss, float* dlogits, int32_t* preds, int64_t* correct) {
   return guard([&] {
     bind(ctx);
+    check_extent(ctx, logits, B * C * sizeof(float), "softmax_ce (logits)");
+    check_extent(ctx, onehot, B * C * sizeof(float), "softmax_ce (onehot)");
+    check_extent(ctx, labels, B * sizeof(int32_t), "softmax_ce (labels)");
+    check_extent(ctx, dlogits, B * C * sizeof(float), "softmax_ce (dlogits)");
+    check_extent(ctx, preds, B * sizeof(int32_t), "softmax_ce (preds)");
+    check_extent(ctx, loss, sizeof(float), "softmax_ce (loss)");
+    check_extent(ctx, correct, sizeof(int64_t), "softmax_ce (correct)");
     softmax_ce(ctx, logits, B, C, onehot, labels, loss, dlogits, preds, correct);
   });
 }
@@ -386,6 +393,10 @@ int orca_hip_relu_bw_colsum(orca_hip_ctx* ctx, const float* grad, const float* p
                             float* dpre, float* colsum) {
   return guard([&] {
     bind(ctx);
+    check_extent(ctx, grad, rows * cols * sizeof(float), "relu_bw_colsum (grad)");
+    check_extent(ctx, pre, rows * cols * sizeof(float), "relu_bw_colsum (pre)");
+    check_extent(ctx, dpre, rows * cols * sizeof(float), "relu_bw_colsum (dpre)");
+    check_extent(ctx, colsum, cols * sizeof(float), "relu_bw_colsum (colsum)");
     if (rows == 0 || cols == 0) {
       if (colsum) launch_fill(ctx, colsum, 0.0f, cols);
       return;
@@ -424,6 +435,8 @@ int orca_hip_adamw_step(orca_hip_ctx* ctx, float* p, const float* g, float* m, f
                         double beta1, double beta2, double eps, double weight_decay, int64_t t) {
   return guard([&] {
     bind(ctx);
+    for (const void* a : {(const void*)p, (const void*)g, (const void*)m, (const void*)v})
+      check_extent(ctx, a, n * sizeof(float), "adamw_step");
     adamw(ctx, p, g, m, v, n, lr, beta1, beta2, eps, weight_decay, t);
   });
 }
@@ -431,6 +444,8 @@ int orca_hip_adamw_step(orca_hip_ctx* ctx, float* p, const float* g, float* m, f
 int orca_hip_sgd_step(orca_hip_ctx* ctx, float* p, const float* g, size_t n, double lr) {
   return guard([&] {
     bind(ctx);
+    check_extent(ctx, p, n * sizeof(float), "sgd_step");
+    check_extent(ctx, g, n * sizeof(float), "sgd_step");
     sgd(ctx, p, g, n, lr);
   });
 }

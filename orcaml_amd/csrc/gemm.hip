@@ -737,6 +737,9 @@ int orca_hip_gemm(orca_hip_ctx* ctx, int trans_a, int trans_b, size_t M, size_t 
     bind(ctx);
     if ((trans_a ? lda < M : lda < K) || (trans_b ? ldb < K : ldb < N) || ldc < N)
       fail(ORCA_HIP_ERR_SHAPE, "Shape mismatch during gemm: leading dimension smaller than the row length");
+    check_extent(ctx, A, matrix_bytes(trans_a ? K : M, trans_a ? M : K, lda), "gemm (A)");
+    check_extent(ctx, B, matrix_bytes(trans_b ? N : K, trans_b ? K : N, ldb), "gemm (B)");
+    check_extent(ctx, C, matrix_bytes(M, N, ldc), "gemm (C)");
     GemmEpi e;
     if (epi) {
       e.kind = epi->kind;
@@ -750,6 +753,10 @@ int orca_hip_gemm(orca_hip_ctx* ctx, int trans_a, int trans_b, size_t M, size_t 
         fail(ORCA_HIP_ERR_INTERNAL, "bias epilogue without a bias pointer");
       if (e.kind == ORCA_HIP_EPI_RELU_MASK && (!e.mask || e.ldmask < N))
         fail(ORCA_HIP_ERR_INTERNAL, "mask epilogue without a valid mask");
+      if (e.kind == ORCA_HIP_EPI_BIAS || e.kind == ORCA_HIP_EPI_BIAS_RELU)
+        check_extent(ctx, e.bias, N * sizeof(float), "gemm (bias)");
+      if (e.kind == ORCA_HIP_EPI_RELU_MASK) check_extent(ctx, e.mask, matrix_bytes(M, N, e.ldmask), "gemm (mask)");
+      check_extent(ctx, e.colsum, N * sizeof(float), "gemm (colsum)");
     }
     gemm(ctx, trans_a != 0, trans_b != 0, M, N, K, A, lda, 0, B, ldb, 0, C, ldc, 0, 1, e);
   });
@@ -777,6 +784,8 @@ int orca_hip_matmul(orca_hip_ctx* ctx, const void* lhs, const void* rhs, const s
                                    std::to_string(K) + " == " + std::to_string(K2) + ", got " + std::to_string(K) +
                                    " != " + std::to_string(K2));
     const bool ta = lhs_view == ORCA_HIP_VIEW_TRANSPOSED, tb = rhs_view == ORCA_HIP_VIEW_TRANSPOSED;
+    check_extent(ctx, lhs, batch * M * K * sizeof(float), "matmul (lhs)");
+    check_extent(ctx, rhs, batch * K * N * sizeof(float), "matmul (rhs)");
     float* o = new_output(ctx, batch * M * N);
     GemmEpi e;
     gemm(ctx, ta, tb, M, N, K, static_cast<const float*>(lhs), ta ? M : K, M * K, static_cast<const float*>(rhs),

@@ -542,6 +542,16 @@ int orca_hip_head_forward_ce(orca_hip_ctx* ctx, const float* H, size_t B, size_t
     if (!head_supported(B, K, C))
       fail(ORCA_HIP_ERR_SHAPE, "Shape mismatch during head_forward_ce: expected 1..16 classes and K a multiple of 4, got K=" +
                                    std::to_string(K) + " C=" + std::to_string(C));
+    check_extent(ctx, H, B * K * sizeof(float), "head_forward_ce (H)");
+    check_extent(ctx, W, K * C * sizeof(float), "head_forward_ce (W)");
+    check_extent(ctx, bias, C * sizeof(float), "head_forward_ce (bias)");
+    check_extent(ctx, onehot, B * C * sizeof(float), "head_forward_ce (onehot)");
+    check_extent(ctx, labels, B * sizeof(int32_t), "head_forward_ce (labels)");
+    check_extent(ctx, logits, B * C * sizeof(float), "head_forward_ce (logits)");
+    check_extent(ctx, dlogits, B * C * sizeof(float), "head_forward_ce (dlogits)");
+    check_extent(ctx, preds, B * sizeof(int32_t), "head_forward_ce (preds)");
+    check_extent(ctx, loss, sizeof(float), "head_forward_ce (loss)");
+    check_extent(ctx, correct, sizeof(int64_t), "head_forward_ce (correct)");
     Scratch rows_f(ctx, sizeof(float) * B), rows_i(ctx, sizeof(int) * B);
     HeadWorkspace ws{rows_f.as<float>(), rows_i.as<int>()};
     head_forward(ctx, H, B, K, W, bias, C, onehot, labels, logits, dlogits, preds, ws);
@@ -557,6 +567,12 @@ int orca_hip_head_backward(orca_hip_ctx* ctx, const float* H, size_t B, size_t K
     if (!head_supported(B, K, C))
       fail(ORCA_HIP_ERR_SHAPE, "Shape mismatch during head_backward: expected 1..16 classes and K a multiple of 4, got K=" +
                                    std::to_string(K) + " C=" + std::to_string(C));
+    check_extent(ctx, H, B * K * sizeof(float), "head_backward (H)");
+    check_extent(ctx, W, K * C * sizeof(float), "head_backward (W)");
+    check_extent(ctx, dlogits, B * C * sizeof(float), "head_backward (dlogits)");
+    check_extent(ctx, dH, B * K * sizeof(float), "head_backward (dH)");
+    check_extent(ctx, dW, K * C * sizeof(float), "head_backward (dW)");
+    check_extent(ctx, db, C * sizeof(float), "head_backward (db)");
     head_backward(ctx, H, B, K, W, C, dlogits, relu_mask != 0, dH, dW, db, nullptr, nullptr, nullptr);
   });
 }

@@ -94,6 +94,7 @@ inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 template <class Op>
 void run_ew1(orca_hip_ctx* ctx, const char* name, const float* a, float* out, size_t n, Op op) {
   if (n == 0) return;
+  check_extent(ctx, a, n * sizeof(float), name);
   ProfScope ps(ctx, name, 0.0, 8.0 * n);
   if (aligned16(a) && aligned16(out)) {
     unsigned g = grid_for((n + 3) / 4, kBlock, ctx->num_cus * 16);
@@ -108,6 +109,8 @@ void run_ew1(orca_hip_ctx* ctx, const char* name, const float* a, float* out, si
 template <class Op>
 void run_ew2(orca_hip_ctx* ctx, const char* name, const float* a, const float* b, float* out, size_t n, Op op) {
   if (n == 0) return;
+  check_extent(ctx, a, n * sizeof(float), name);
+  check_extent(ctx, b, n * sizeof(float), name);
   ProfScope ps(ctx, name, 0.0, 12.0 * n);
   if (aligned16(a) && aligned16(b) && aligned16(out)) {
     unsigned g = grid_for((n + 3) / 4, kBlock, ctx->num_cus * 16);
@@ -400,6 +403,7 @@ int orca_hip_div_backward_rhs(orca_hip_ctx* ctx, const void* g, const void* l, c
     bind(ctx);
     check_f32(dtype, "div_backward_rhs");
     size_t n = numel(shape, rank);
+    for (const void* a : {g, l, r}) check_extent(ctx, a, n * sizeof(float), "div_backward_rhs");
     float* o = new_output(ctx, n);
     if (n) {
       unsigned gsz = grid_for(n, kBlock, ctx->num_cus * 16);
@@ -456,6 +460,7 @@ int orca_hip_to_f32_vec(orca_hip_ctx* ctx, const void* s, size_t n, float* host_
   return guard([&] {
     bind(ctx);
     if (!n) return;
+    check_extent(ctx, s, n * sizeof(float), "to_f32_vec");
     ORCA_HIP_CHECK(hipMemcpyAsync(host_out, s, n * sizeof(float), hipMemcpyDeviceToHost, ctx->stream));
     ORCA_HIP_CHECK(hipStreamSynchronize(ctx->stream));
   });
@@ -483,6 +488,7 @@ int orca_hip_to_bytes(orca_hip_ctx* ctx, const void* s, size_t n_bytes, uint8_t*
   return guard([&] {
     bind(ctx);
     if (!n_bytes) return;
+    check_extent(ctx, s, n_bytes, "to_bytes");
     ORCA_HIP_CHECK(hipMemcpyAsync(host_out, s, n_bytes, hipMemcpyDeviceToHost, ctx->stream));
     ORCA_HIP_CHECK(hipStreamSynchronize(ctx->stream));
   });
@@ -509,6 +515,7 @@ int orca_hip_expand(orca_hip_ctx* ctx, const void* s, const size_t* in_shape, si
       a.out_dims[d] = (int64_t)out_shape[d];
       a.in_strides[d] = pin[d] == 1 ? 0 : st[d];
     }
+    check_extent(ctx, s, numel(in_shape, in_rank) * sizeof(float), "expand");
     size_t n = numel(out_shape, out_rank);
     float* o = new_output(ctx, n);
     if (n) {
@@ -530,6 +537,7 @@ static int reduce_entry(orca_hip_ctx* ctx, bool is_max, const void* s, const siz
     if (is_max && out_rank > in_rank)
       fail(ORCA_HIP_ERR_SHAPE, std::string("Shape mismatch during ") + op + ": output rank exceeds input rank");
     ReduceArgs a = make_reduce(in_shape, in_rank, out_shape, out_rank, op);
+    check_extent(ctx, s, numel(in_shape, in_rank) * sizeof(float), op);
     size_t n_out = numel(out_shape, out_rank);
     float* o = new_output(ctx, n_out);
     if (n_out) {
@@ -574,6 +582,9 @@ int orca_hip_max_to_shape_backward(orca_hip_ctx* ctx, const void* g, const void*
     check_f32(dtype, "max_to_shape_backward");
     if (out_rank > in_rank) fail(ORCA_HIP_ERR_SHAPE, "Shape mismatch during max_to_shape_backward: output rank exceeds input rank");
     check_rank(in_rank, "max_to_shape_backward");
+    check_extent(ctx, g, numel(out_shape, out_rank) * sizeof(float), "max_to_shape_backward (grad)");
+    check_extent(ctx, x, numel(in_shape, in_rank) * sizeof(float), "max_to_shape_backward (input)");
+    check_extent(ctx, y, numel(out_shape, out_rank) * sizeof(float), "max_to_shape_backward (output)");
     int64_t pout[kMaxRank], st[kMaxRank];
     pad_left(out_shape, out_rank, in_rank, pout);
     for (size_t d = 0; d < in_rank; ++d)
@@ -625,6 +636,7 @@ int orca_hip_transpose(orca_hip_ctx* ctx, const void* s, const size_t* shape, si
     if (d0 >= rank || d1 >= rank) fail(ORCA_HIP_ERR_INTERNAL, "Invalid transpose dimensions");
     check_rank(rank, "transpose");
     size_t n = numel(shape, rank);
+    check_extent(ctx, s, n * sizeof(float), "transpose");
     float* o = new_output(ctx, n);
     if (n) {
       ProfScope ps(ctx, "transpose", 0.0, 8.0 * n);

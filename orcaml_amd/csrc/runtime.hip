@@ -93,6 +93,26 @@ size_t CachingAllocator::size_of(void* p) {
   return it == live_.end() ? 0 : it->second;
 }
 
+size_t CachingAllocator::extent_from(const void* p) {
+  std::lock_guard<std::mutex> lk(mu_);
+  auto it = live_.upper_bound(const_cast<void*>(p));
+  if (it == live_.begin()) return 0;
+  --it;
+  const char* base = static_cast<const char*>(it->first);
+  const char* q = static_cast<const char*>(p);
+  if (q >= base && q < base + it->second) return static_cast<size_t>(base + it->second - q);
+  return 0;
+}
+
+void check_extent(orca_hip_ctx* ctx, const void* p, size_t bytes, const char* what) {
+  if (!p || !bytes) return;
+  const size_t have = ctx->alloc.extent_from(p);
+  if (have && bytes > have)
+    fail(ORCA_HIP_ERR_SHAPE, std::string("Shape mismatch during ") + what + ": the access spans " +
+                                 std::to_string(bytes) + " bytes but the buffer has " + std::to_string(have) +
+                                 " from this pointer");
+}
+
 void CachingAllocator::empty(hipStream_t stream) {
   if (stream) (void)hipStreamSynchronize(stream);
   std::lock_guard<std::mutex> lk(mu_);
@@ -301,6 +321,7 @@ int orca_hip_h2d(orca_hip_ctx* ctx, void* dst, const void* src, size_t bytes) {
   return guard([&] {
     bind(ctx);
     if (!bytes) return;
+    check_extent(ctx, dst, bytes, "h2d");
     ORCA_HIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream));
     ORCA_HIP_CHECK(hipStreamSynchronize(ctx->stream));
   });
@@ -310,6 +331,7 @@ int orca_hip_d2h(orca_hip_ctx* ctx, void* dst, const void* src, size_t bytes) {
   return guard([&] {
     bind(ctx);
     if (!bytes) return;
+    check_extent(ctx, src, bytes, "d2h");
     ORCA_HIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream));
     ORCA_HIP_CHECK(hipStreamSynchronize(ctx->stream));
   });
@@ -319,6 +341,8 @@ int orca_hip_d2d(orca_hip_ctx* ctx, void* dst, const void* src, size_t bytes) {
   return guard([&] {
     bind(ctx);
     if (!bytes) return;
+    check_extent(ctx, dst, bytes, "d2d");
+    check_extent(ctx, src, bytes, "d2d");
     ORCA_HIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, ctx->stream));
   });
 }
@@ -326,6 +350,7 @@ int orca_hip_d2d(orca_hip_ctx* ctx, void* dst, const void* src, size_t bytes) {
 int orca_hip_fill(orca_hip_ctx* ctx, float* dst, float value, size_t n) {
   return guard([&] {
     bind(ctx);
+    check_extent(ctx, dst, n * sizeof(float), "fill");
     launch_fill(ctx, dst, value, n);
   });
 }

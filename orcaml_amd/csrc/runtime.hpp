@@ -64,6 +64,8 @@ class CachingAllocator {
   void release(void* p);
   void empty(hipStream_t stream);
   size_t size_of(void* p);
+  // Bytes from p to the end of the live allocation containing p (0 if none does).
+  size_t extent_from(const void* p);
   void stats(size_t* live, size_t* cached, size_t* mallocs);
   ~CachingAllocator();
 
@@ -71,7 +73,7 @@ class CachingAllocator {
 
  private:
   std::mutex mu_;
-  std::unordered_map<void*, size_t> live_;
+  std::map<void*, size_t> live_;  // ordered: extent_from finds the block around an interior pointer
   std::multimap<size_t, void*> cached_;
   size_t live_bytes_ = 0, cached_bytes_ = 0, mallocs_ = 0;
 };
@@ -146,6 +148,16 @@ class Scratch {
   orca_hip_ctx* ctx_;
   void* p_;
 };
+
+// Fails with ShapeMismatch when [p, p + bytes) runs past the end of the
+// context allocation that contains p, so a wrong size or leading dimension
+// is reported instead of launching out of bounds.  Memory the context did
+// not allocate is not checked.
+void check_extent(orca_hip_ctx* ctx, const void* p, size_t bytes, const char* what);
+// Extent of a row-major [rows][ld] operand whose rows hold `cols` used values.
+inline size_t matrix_bytes(size_t rows, size_t cols, size_t ld) {
+  return rows == 0 || cols == 0 ? 0 : ((rows - 1) * ld + cols) * sizeof(float);
+}
 
 inline void check_ctx(const orca_hip_ctx* ctx) {
   if (!ctx) fail(ORCA_HIP_ERR_INTERNAL, "null orca_hip_ctx");

@@ -3,12 +3,14 @@ and of the unchanged composed training step (reference frontend replayed
 through the tape) on HipBackend."""
 from __future__ import annotations
 
+import ctypes
+
 import numpy as np
 import pytest
 
 from oracle import oracle as O
 from orcaml_amd import autodiff as A
-from orcaml_amd import synth
+from orcaml_amd import _lib, synth
 from orcaml_amd._lib import OrcaHipError
 from tests.util import assert_close, assert_close_scaled
 
@@ -220,3 +222,21 @@ def test_composed_step_allocates_nothing_in_steady_state(hb, ctx):
     before = ctx.mem_stats()["device_allocs"]
     composed(ad, w["dims"], params, x, onehot, "sgd", 3, lr=0.1)
     assert ctx.mem_stats()["device_allocs"] == before
+
+
+def test_extent_guard_rejects_overruns_before_any_launch(ctx):
+    """A size that runs past the end of a context allocation is a
+    ShapeMismatch raised on the host.  Only copies are used here: even
+    unguarded, the runtime bounds-checks them, so nothing can reach the GPU
+    out of bounds."""
+    buf = ctx.alloc(4096)
+    host = np.empty(2048, np.float32)
+    hp = host.ctypes.data_as(ctypes.c_void_p)
+    for ptr, nbytes in ((buf.ptr, 8192), (buf.ptr + 1024, 4096)):
+        with pytest.raises(_lib.OrcaHipError) as e:
+            _lib.call("orca_hip_d2h", ctx.handle, hp, ptr, nbytes)
+        assert e.value.code == _lib.ERR_SHAPE
+        with pytest.raises(_lib.OrcaHipError) as e:
+            _lib.call("orca_hip_h2d", ctx.handle, ptr, hp, nbytes)
+        assert e.value.code == _lib.ERR_SHAPE
+    _lib.call("orca_hip_d2h", ctx.handle, hp, buf.ptr + 1024, 3072)  # fits exactly
