@@ -188,10 +188,6 @@ __global__ void chunk_reduce_kernel(const float* __restrict__ partial, int chunk
   out[c] = s;
 }
 
-struct AdamWScalars {
-  float decay, b1, omb1, b2, omb2, c1, c2, eps, lr;
-};
-
 __device__ __forceinline__ void adamw_elem(float& p, float g, float& m, float& v, const AdamWScalars& k) {
   float d = p * k.decay;                // p * (1 - lr*wd)
   float mn = (m * k.b1) + (g * k.omb1); // m*b1 + g*(1-b1)
@@ -209,11 +205,13 @@ __device__ __forceinline__ void adamw_elem(float& p, float g, float& m, float& v
 // and stores: the arrays are streamed once per step, so they bypass cache
 // allocation.  (Measured on 2^28 parameters: 6.2 TB/s, against 5.2 TB/s for
 // a grid-stride loop with ordinary accesses.)
+template <bool DEV>
 __global__ void __launch_bounds__(256) adamw_vec_kernel(float4* __restrict__ p, const float4* __restrict__ g,
                                                         float4* __restrict__ m, float4* __restrict__ v, size_t n4,
-                                                        AdamWScalars k) {
+                                                        AdamWScalars ka, const AdamWScalars* __restrict__ kd) {
   const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n4) return;
+  const AdamWScalars k = DEV ? *kd : ka;
   floatx4 pp = __builtin_nontemporal_load(reinterpret_cast<const floatx4*>(p) + i);
   const floatx4 gg = __builtin_nontemporal_load(reinterpret_cast<const floatx4*>(g) + i);
   floatx4 mm = __builtin_nontemporal_load(reinterpret_cast<const floatx4*>(m) + i);
@@ -227,8 +225,11 @@ __global__ void __launch_bounds__(256) adamw_vec_kernel(float4* __restrict__ p, 
   __builtin_nontemporal_store(floatx4{va[0], va[1], va[2], va[3]}, reinterpret_cast<floatx4*>(v) + i);
 }
 
+template <bool DEV>
 __global__ void adamw_scalar_kernel(float* __restrict__ p, const float* __restrict__ g, float* __restrict__ m,
-                                    float* __restrict__ v, size_t begin, size_t n, AdamWScalars k) {
+                                    float* __restrict__ v, size_t begin, size_t n, AdamWScalars ka,
+                                    const AdamWScalars* __restrict__ kd) {
+  const AdamWScalars k = DEV ? *kd : ka;
   size_t stride = (size_t)gridDim.x * blockDim.x;
   for (size_t i = begin + (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
     float pp = p[i], mm = m[i], vv = v[i];
@@ -238,6 +239,8 @@ __global__ void adamw_scalar_kernel(float* __restrict__ p, const float* __restri
     v[i] = vv;
   }
 }
+
+__global__ void adamw_store_scalars_kernel(AdamWScalars* dst, AdamWScalars s) { *dst = s; }
 
 __global__ void __launch_bounds__(256) sgd_vec_kernel(float4* __restrict__ p, const float4* __restrict__ g, size_t n4, float lr) {
   const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -262,28 +265,31 @@ inline bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr
 }  // namespace
 
 void softmax_ce(orca_hip_ctx* ctx, const float* logits, size_t B, size_t C, const float* onehot, const int32_t* labels,
-                float* loss, float* dlogits, int32_t* preds, int64_t* correct) {
+                float* loss, float* dlogits, int32_t* preds, int64_t* correct, float* ws_row_loss,
+                int* ws_row_correct) {
   if ((onehot == nullptr) == (labels == nullptr))
     fail(ORCA_HIP_ERR_INTERNAL, "softmax_ce needs exactly one of one-hot targets or labels");
   if (B == 0 || C == 0) fail(ORCA_HIP_ERR_SHAPE, "Shape mismatch during softmax_ce: empty logits");
   if (C > 4096) fail(ORCA_HIP_ERR_SHAPE, "Shape mismatch during softmax_ce: expected at most 4096 classes, got " + std::to_string(C));
   if (B > (size_t)INT32_MAX) fail(ORCA_HIP_ERR_SHAPE, "softmax_ce: too many rows");
-  Scratch row_loss(ctx, sizeof(float) * B);
-  Scratch row_correct(ctx, sizeof(int) * B);
+  Scratch row_loss_s(ctx, ws_row_loss ? 0 : sizeof(float) * B);
+  Scratch row_correct_s(ctx, ws_row_correct ? 0 : sizeof(int) * B);
+  float* row_loss = ws_row_loss ? ws_row_loss : row_loss_s.as<float>();
+  int* row_correct = ws_row_correct ? ws_row_correct : row_correct_s.as<int>();
   const float inv_b = 1.0f / (float)B;
   const int rows_per_block = 4;
   dim3 grid((unsigned)((B + rows_per_block - 1) / rows_per_block));
-  int* rc = correct ? row_correct.as<int>() : nullptr;
+  int* rc = correct ? row_correct : nullptr;
   {
     ProfScope ps(ctx, "softmax_ce", 0.0, 4.0 * (double)B * C * (dlogits ? 2 : 1) + 4.0 * B);
 #define CE_LAUNCH(VPL, VEC, FULL)                                                                           \
   do {                                                                                                      \
     if (labels)                                                                                             \
       hipLaunchKernelGGL((softmax_ce_kernel<VPL, VEC, FULL, true>), grid, dim3(256), 0, ctx->stream, logits, \
-                         (int)B, (int)C, onehot, labels, inv_b, row_loss.as<float>(), dlogits, preds, rc);   \
+                         (int)B, (int)C, onehot, labels, inv_b, row_loss, dlogits, preds, rc);                 \
     else                                                                                                    \
       hipLaunchKernelGGL((softmax_ce_kernel<VPL, VEC, FULL, false>), grid, dim3(256), 0, ctx->stream, logits, \
-                         (int)B, (int)C, onehot, labels, inv_b, row_loss.as<float>(), dlogits, preds, rc);   \
+                         (int)B, (int)C, onehot, labels, inv_b, row_loss, dlogits, preds, rc);                 \
   } while (0)
     const bool vec = C % 4 == 0 && aligned16(logits) && (!dlogits || aligned16(dlogits));
     if (C <= 64) {
@@ -304,16 +310,13 @@ void softmax_ce(orca_hip_ctx* ctx, const float* logits, size_t B, size_t C, cons
     ORCA_HIP_CHECK(hipGetLastError());
   }
   if (loss || correct) {
-    hipLaunchKernelGGL(ce_finish_kernel, dim3(1), dim3(1024), 0, ctx->stream, row_loss.as<float>(), rc, (int)B,
+    hipLaunchKernelGGL(ce_finish_kernel, dim3(1), dim3(1024), 0, ctx->stream, row_loss, rc, (int)B,
                        inv_b, loss, correct);
     ORCA_HIP_CHECK(hipGetLastError());
   }
 }
 
-void adamw(orca_hip_ctx* ctx, float* p, const float* g, float* m, float* v, size_t n, double lr, double b1, double b2,
-           double eps, double wd, int64_t t, hipStream_t stream) {
-  if (!stream) stream = ctx->stream;
-  if (n == 0) return;
+AdamWScalars adamw_scalars(double lr, double b1, double b2, double eps, double wd, int64_t t) {
   if (t < 1) fail(ORCA_HIP_ERR_INTERNAL, "adamw step count must be >= 1");
   AdamWScalars k;
   k.decay = (float)(1.0 - lr * wd);
@@ -325,6 +328,19 @@ void adamw(orca_hip_ctx* ctx, float* p, const float* g, float* m, float* v, size
   k.c2 = (float)(1.0 / (1.0 - std::pow(b2, (double)t)));
   k.eps = (float)eps;
   k.lr = (float)lr;
+  return k;
+}
+
+void adamw_store_scalars(orca_hip_ctx* ctx, AdamWScalars* dst, const AdamWScalars& s, hipStream_t stream) {
+  hipLaunchKernelGGL(adamw_store_scalars_kernel, dim3(1), dim3(1), 0, stream ? stream : ctx->stream, dst, s);
+  ORCA_HIP_CHECK(hipGetLastError());
+}
+
+void adamw(orca_hip_ctx* ctx, float* p, const float* g, float* m, float* v, size_t n, double lr, double b1, double b2,
+           double eps, double wd, int64_t t, hipStream_t stream, const AdamWScalars* dev_scalars) {
+  if (!stream) stream = ctx->stream;
+  if (n == 0) return;
+  const AdamWScalars k = dev_scalars ? AdamWScalars{} : adamw_scalars(lr, b1, b2, eps, wd, t);
   ProfScope ps(ctx, "adamw", 0.0, 28.0 * (double)n, stream);
   size_t done = 0;
   if (aligned16(p) && aligned16(g) && aligned16(m) && aligned16(v)) {
@@ -332,15 +348,27 @@ void adamw(orca_hip_ctx* ctx, float* p, const float* g, float* m, float* v, size
     if (n4) {
       const size_t gsz = (n4 + 255) / 256;
       if (gsz > 0x7fffffffu) fail(ORCA_HIP_ERR_INTERNAL, "adamw: buffer too large for one launch");
-      hipLaunchKernelGGL(adamw_vec_kernel, dim3((unsigned)gsz), dim3(256), 0, stream, reinterpret_cast<float4*>(p),
-                         reinterpret_cast<const float4*>(g), reinterpret_cast<float4*>(m),
-                         reinterpret_cast<float4*>(v), n4, k);
+      auto* p4 = reinterpret_cast<float4*>(p);
+      auto* g4 = reinterpret_cast<const float4*>(g);
+      auto* m4 = reinterpret_cast<float4*>(m);
+      auto* v4 = reinterpret_cast<float4*>(v);
+      if (dev_scalars)
+        hipLaunchKernelGGL(adamw_vec_kernel<true>, dim3((unsigned)gsz), dim3(256), 0, stream, p4, g4, m4, v4, n4, k,
+                           dev_scalars);
+      else
+        hipLaunchKernelGGL(adamw_vec_kernel<false>, dim3((unsigned)gsz), dim3(256), 0, stream, p4, g4, m4, v4, n4,
+                           k, dev_scalars);
     }
     done = 4 * n4;
   }
   if (done < n) {
     unsigned gsz = grid_for(n - done, 256, ctx->num_cus * 8);
-    hipLaunchKernelGGL(adamw_scalar_kernel, dim3(gsz), dim3(256), 0, stream, p, g, m, v, done, n, k);
+    if (dev_scalars)
+      hipLaunchKernelGGL(adamw_scalar_kernel<true>, dim3(gsz), dim3(256), 0, stream, p, g, m, v, done, n, k,
+                         dev_scalars);
+    else
+      hipLaunchKernelGGL(adamw_scalar_kernel<false>, dim3(gsz), dim3(256), 0, stream, p, g, m, v, done, n, k,
+                         dev_scalars);
   }
   ORCA_HIP_CHECK(hipGetLastError());
 }

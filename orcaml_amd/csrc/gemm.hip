@@ -560,6 +560,75 @@ const char* kernel_name(bool ta, bool tb, bool pipelined) {
 
 }  // namespace
 
+namespace {
+
+// Kernel, tile and K split of one product.
+struct GemmPlan {
+  bool fast;
+  size_t BN, mt, nt;
+  int splits, k_chunk;
+};
+
+GemmPlan plan_gemm(orca_hip_ctx* ctx, bool trans_a, bool trans_b, size_t M, size_t N, size_t K, const float* A,
+                   size_t lda, size_t sa, const float* B, size_t ldb, size_t sb, size_t batch) {
+  GemmPlan g{};
+  const bool vec_a = aligned16(A) && lda % 4 == 0 && (batch == 1 || sa % 4 == 0);
+  const bool vec_b = aligned16(B) && ldb % 4 == 0 && (batch == 1 || sb % 4 == 0);
+  // Products with M, N, K multiples of 4 and 16-byte aligned operands take the
+  // pipelined 128 x 128 kernel, whose per-lane offsets are 32-bit byte offsets
+  // within one operand.
+  const size_t a_rows = trans_a ? K : M, b_rows = trans_b ? N : K;
+  g.fast = M % 4 == 0 && N % 4 == 0 && K % 4 == 0 && vec_a && vec_b && a_rows * lda * 4 < 0xffffffffull &&
+           b_rows * ldb * 4 < 0xffffffffull && !fast_env_off();
+  // Generic kernel tile: 128 x 128 when that gives every CU a block, else
+  // 128 x 64 (twice the blocks).  ORCA_HIP_GEMM_TILE=128x128|128x64 overrides
+  // the generic kernel's choice (tuning).
+  const size_t target = (size_t)ctx->num_cus;
+  const size_t t128 = ((M + 127) / 128) * ((N + 127) / 128) * batch;
+  int bn = t128 >= target ? 128 : 64;
+  static const char* tile_env = std::getenv("ORCA_HIP_GEMM_TILE");
+  if (tile_env && std::string(tile_env) == "128x128") bn = 128;
+  if (tile_env && std::string(tile_env) == "128x64") bn = 64;
+  if (g.fast) bn = 128;
+  const size_t BM = 128;
+  g.BN = (size_t)bn;
+  g.mt = (M + BM - 1) / BM;
+  g.nt = (N + g.BN - 1) / g.BN;
+  // Split K when the tile grid cannot fill the CUs and K is long enough.
+  g.splits = 1;
+  const size_t tiles = g.mt * g.nt * batch;
+  if (tiles < target / 2 && K >= 4 * (size_t)BK) {
+    size_t want = (target + tiles - 1) / tiles;
+    size_t max_by_k = K / (2 * BK);
+    g.splits = (int)std::min<size_t>(std::min<size_t>(want, max_by_k), 64);
+    if (g.splits < 1) g.splits = 1;
+  }
+  g.k_chunk = (int)K;
+  if (g.splits > 1) {
+    size_t per = (K + g.splits - 1) / g.splits;
+    per = (per + BK - 1) / BK * BK;
+    g.splits = (int)((K + per - 1) / per);
+    g.k_chunk = (int)per;
+  }
+  return g;
+}
+
+// Workspace floats of a planned product: split-K partials, then per-split column sums.
+size_t plan_workspace_floats(const GemmPlan& g, size_t M, size_t N, size_t batch, bool colsum) {
+  if (g.splits <= 1) return 0;
+  return batch * (size_t)g.splits * M * N + (colsum ? (size_t)g.splits * N : 0);
+}
+
+}  // namespace
+
+size_t gemm_workspace_floats(orca_hip_ctx* ctx, bool trans_a, bool trans_b, size_t M, size_t N, size_t K,
+                             const float* A, size_t lda, size_t sa, const float* B, size_t ldb, size_t sb,
+                             size_t batch, bool colsum) {
+  if (M == 0 || N == 0 || batch == 0 || K == 0) return 0;
+  const GemmPlan g = plan_gemm(ctx, trans_a, trans_b, M, N, K, A, lda, sa, B, ldb, sb, batch);
+  return plan_workspace_floats(g, M, N, batch, colsum && batch == 1 && !trans_b);
+}
+
 void gemm(orca_hip_ctx* ctx, bool trans_a, bool trans_b, size_t M, size_t N, size_t K, const float* A, size_t lda,
           size_t sa, const float* B, size_t ldb, size_t sb, float* C, size_t ldc, size_t sc, size_t batch,
           const GemmEpi& epi) {
@@ -578,44 +647,14 @@ void gemm(orca_hip_ctx* ctx, bool trans_a, bool trans_b, size_t M, size_t N, siz
     if (epi.colsum) launch_fill(ctx, epi.colsum, 0.0f, N);
     return;
   }
+  const GemmPlan plan = plan_gemm(ctx, trans_a, trans_b, M, N, K, A, lda, sa, B, ldb, sb, batch);
+  const bool fast = plan.fast;
+  const int bn = (int)plan.BN;
+  const size_t mt = plan.mt, nt = plan.nt;
+  if (mt > 65535) fail(ORCA_HIP_ERR_INTERNAL, "gemm: too many row tiles");
+  const int splits = plan.splits, k_chunk = plan.k_chunk;
   const bool vec_a = aligned16(A) && lda % 4 == 0 && (batch == 1 || sa % 4 == 0);
   const bool vec_b = aligned16(B) && ldb % 4 == 0 && (batch == 1 || sb % 4 == 0);
-  // Products with M, N, K multiples of 4 and 16-byte aligned operands take the
-  // pipelined 128 x 128 kernel, whose per-lane offsets are 32-bit byte offsets
-  // within one operand.
-  const size_t a_rows = trans_a ? K : M, b_rows = trans_b ? N : K;
-  const bool fast = M % 4 == 0 && N % 4 == 0 && K % 4 == 0 && vec_a && vec_b &&
-                    a_rows * lda * 4 < 0xffffffffull && b_rows * ldb * 4 < 0xffffffffull && !fast_env_off();
-  // Generic kernel tile: 128 x 128 when that gives every CU a block, else
-  // 128 x 64 (twice the blocks).  ORCA_HIP_GEMM_TILE=128x128|128x64 overrides
-  // the generic kernel's choice (tuning).
-  const size_t target = (size_t)ctx->num_cus;
-  const size_t t128 = ((M + 127) / 128) * ((N + 127) / 128) * batch;
-  int bn = t128 >= target ? 128 : 64;
-  static const char* tile_env = std::getenv("ORCA_HIP_GEMM_TILE");
-  if (tile_env && std::string(tile_env) == "128x128") bn = 128;
-  if (tile_env && std::string(tile_env) == "128x64") bn = 64;
-  if (fast) bn = 128;
-  const size_t BM = 128, BN = (size_t)bn;
-  const size_t mt = (M + BM - 1) / BM, nt = (N + BN - 1) / BN;
-  if (mt > 65535) fail(ORCA_HIP_ERR_INTERNAL, "gemm: too many row tiles");
-
-  // Split K when the tile grid cannot fill the CUs and K is long enough.
-  int splits = 1;
-  const size_t tiles = mt * nt * batch;
-  if (tiles < target / 2 && K >= 4 * (size_t)BK) {
-    size_t want = (target + tiles - 1) / tiles;
-    size_t max_by_k = K / (2 * BK);
-    splits = (int)std::min<size_t>(std::min<size_t>(want, max_by_k), 64);
-    if (splits < 1) splits = 1;
-  }
-  int k_chunk = (int)K;
-  if (splits > 1) {
-    size_t per = (K + splits - 1) / splits;
-    per = (per + BK - 1) / BK * BK;
-    splits = (int)((K + per - 1) / per);
-    k_chunk = (int)per;
-  }
 
   GemmParams p{};
   p.A = A;
@@ -636,23 +675,24 @@ void gemm(orca_hip_ctx* ctx, bool trans_a, bool trans_b, size_t M, size_t N, siz
   p.mask = epi.mask;
   p.ldmask = (int64_t)epi.ldmask;
   const bool fold_colsum = epi.colsum != nullptr && batch == 1 && !trans_b;
-  std::unique_ptr<Scratch> colsum_ws;
-  if (fold_colsum && splits > 1) {
-    colsum_ws.reset(new Scratch(ctx, sizeof(float) * splits * N));
-    p.colsum = colsum_ws->as<float>();
-  } else {
-    p.colsum = fold_colsum ? epi.colsum : nullptr;
+  // Split-K partials (and per-split column sums) go to the caller's workspace
+  // when it provides one, else to blocks from the context cache.
+  const size_t ws_need = plan_workspace_floats(plan, M, N, batch, fold_colsum);
+  std::unique_ptr<Scratch> scratch;
+  float* ws = nullptr;
+  if (ws_need) {
+    if (epi.ws) {
+      if (epi.ws_floats < ws_need) fail(ORCA_HIP_ERR_INTERNAL, "gemm: workspace too small for the planned split");
+      ws = epi.ws;
+    } else {
+      scratch.reset(new Scratch(ctx, sizeof(float) * ws_need));
+      ws = scratch->as<float>();
+    }
   }
+  p.colsum = fold_colsum ? (splits > 1 ? ws + batch * (size_t)splits * M * N : epi.colsum) : nullptr;
   p.vec_a = vec_a;
   p.vec_b = vec_b;
-
-  std::unique_ptr<Scratch> ws;
-  if (splits > 1) {
-    ws.reset(new Scratch(ctx, sizeof(float) * batch * splits * M * N));
-    p.C = ws->as<float>();
-  } else {
-    p.C = C;
-  }
+  p.C = splits > 1 ? ws : C;
 
   dim3 grid((unsigned)nt, (unsigned)mt, (unsigned)(batch * splits));
   {

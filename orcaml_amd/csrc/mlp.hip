@@ -19,8 +19,12 @@
 // streaming the layer's input once.  ORCA_HIP_FUSED_HEAD=0 at creation keeps
 // the GEMM + softmax-CE path, ORCA_HIP_OVERLAP_UPDATE=0 runs the whole update
 // on the context stream after the backward (A/B comparisons).
-// Every buffer is allocated at creation; a step allocates nothing (split-K
-// workspaces come from the context's cache) and never synchronises.
+// Every buffer, split-K workspaces included, is allocated at creation: a step
+// allocates nothing and never synchronises.  With ORCA_HIP_GRAPH=1 the step is
+// captured into a HIP graph at its first call (forward, loss, backward and the
+// optimizer passes on both streams) and replayed; the only per-step host work
+// is then one launch storing the step's AdamW scalars, which the graph reads
+// from device memory.
 #include <cstdlib>
 #include <cstring>
 #include <vector>
@@ -55,6 +59,13 @@ struct orca_hip_mlp {
   // overlaps the first layer's weight-gradient GEMM; fork / join events.
   hipStream_t side = nullptr;
   hipEvent_t fork = nullptr, join = nullptr;
+  // Persistent workspaces: a step makes no allocator call, so it can be
+  // captured once into a HIP graph and replayed.
+  orca_hip::AdamWScalars* kdev = nullptr;  // this step's AdamW scalars (device)
+  float* gemm_ws = nullptr;                // split-K partials of the step's GEMMs
+  size_t gemm_ws_floats = 0;
+  bool use_graph = false;
+  hipGraphExec_t exec = nullptr;
 
   float* dev(size_t n) {
     void* p = ctx->alloc.allocate(n * sizeof(float) + 256, ctx->stream);
@@ -62,6 +73,7 @@ struct orca_hip_mlp {
     return static_cast<float*>(p);
   }
   ~orca_hip_mlp() {
+    if (exec) (void)hipGraphExecDestroy(exec);
     for (void* p : owned) ctx->alloc.release(p);
     if (fork) (void)hipEventDestroy(fork);
     if (join) (void)hipEventDestroy(join);
@@ -75,7 +87,10 @@ namespace {
 // Smallest update (parameters of layers >= 1) worth a second stream.
 constexpr size_t kMinOverlapParams = size_t(1) << 22;
 
-void step(orca_hip_mlp* m) {
+// Everything a step enqueues.  With kdev set, AdamW reads its scalars from
+// that device buffer, so the enqueued work is identical from step to step and
+// is what a captured graph replays; without it they are kernel arguments.
+void step_body(orca_hip_mlp* m, const AdamWScalars* kdev) {
   orca_hip_ctx* ctx = m->ctx;
   const size_t L = m->L, B = m->B, C = m->dims[L];
   const size_t n_gemm = m->fused_head ? L - 1 : L;  // layers run as GEMMs
@@ -84,6 +99,8 @@ void step(orca_hip_mlp* m) {
     const size_t K = m->dims[l], N = m->dims[l + 1];
     const float* a = l == 0 ? m->x : m->H[l - 1];
     GemmEpi e;
+    e.ws = m->gemm_ws;
+    e.ws_floats = m->gemm_ws_floats;
     e.kind = l + 1 < L ? ORCA_HIP_EPI_BIAS_RELU : ORCA_HIP_EPI_BIAS;
     e.bias = m->P + m->off[2 * l + 1];
     float* out = l + 1 < L ? m->H[l] : m->logits;
@@ -96,7 +113,8 @@ void step(orca_hip_mlp* m) {
     head_forward(ctx, l == 0 ? m->x : m->H[l - 1], B, m->dims[l], m->P + m->off[2 * l], m->P + m->off[2 * l + 1], C,
                  m->onehot, labels, m->logits, m->dlogits, m->preds, m->head);
   } else {
-    softmax_ce(ctx, m->logits, B, C, m->onehot, labels, m->loss, m->dlogits, m->preds, m->correct);
+    softmax_ce(ctx, m->logits, B, C, m->onehot, labels, m->loss, m->dlogits, m->preds, m->correct,
+               m->head.row_loss, m->head.row_correct);
   }
   // ---- backward ----
   const float* g = m->dlogits;
@@ -123,11 +141,10 @@ void step(orca_hip_mlp* m) {
     if (end <= begin) return;
     if (m->opt.kind == 1)
       adamw(ctx, m->P + begin, m->G + begin, m->Mo + begin, m->Vo + begin, end - begin, m->opt.lr, m->opt.beta1,
-            m->opt.beta2, m->opt.eps, m->opt.weight_decay, m->t, stream);
+            m->opt.beta2, m->opt.eps, m->opt.weight_decay, m->t, stream, kdev);
     else
       sgd(ctx, m->P + begin, m->G + begin, end - begin, m->opt.lr, stream);
   };
-  if (m->opt.kind == 1) m->t += 1;
   for (size_t l = n_gemm; l-- > 0;) {
     const size_t K = m->dims[l], N = m->dims[l + 1];
     const float* a = l == 0 ? m->x : m->H[l - 1];
@@ -139,10 +156,14 @@ void step(orca_hip_mlp* m) {
       forked = true;
     }
     GemmEpi ew;
+    ew.ws = m->gemm_ws;
+    ew.ws_floats = m->gemm_ws_floats;
     ew.colsum = m->G + m->off[2 * l + 1];  // bias gradient
     gemm(ctx, true, false, K, N, B, a, K, 0, g, N, 0, m->G + m->off[2 * l], N, 0, 1, ew);
     if (l > 0) {
       GemmEpi ex;
+      ex.ws = m->gemm_ws;
+      ex.ws_floats = m->gemm_ws_floats;
       ex.kind = ORCA_HIP_EPI_RELU_MASK;
       ex.mask = m->H[l - 1];
       ex.ldmask = K;
@@ -159,6 +180,47 @@ void step(orca_hip_mlp* m) {
   } else {
     update(0, m->arena, ctx->stream);
   }
+}
+
+// Captures step_body into m->exec (the stream leaves capture mode on failure).
+void capture(orca_hip_mlp* m) {
+  hipStream_t s = m->ctx->stream;
+  ORCA_HIP_CHECK(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+  try {
+    step_body(m, m->kdev);
+  } catch (...) {
+    hipGraph_t g = nullptr;
+    (void)hipStreamEndCapture(s, &g);
+    if (g) (void)hipGraphDestroy(g);
+    throw;
+  }
+  hipGraph_t g = nullptr;
+  ORCA_HIP_CHECK(hipStreamEndCapture(s, &g));
+  const hipError_t e = hipGraphInstantiate(&m->exec, g, nullptr, nullptr, 0);
+  (void)hipGraphDestroy(g);
+  if (e != hipSuccess) m->exec = nullptr;
+  ORCA_HIP_CHECK(e);
+}
+
+void invalidate_graph(orca_hip_mlp* m) {
+  if (m->exec) ORCA_HIP_CHECK(hipGraphExecDestroy(m->exec));
+  m->exec = nullptr;
+}
+
+void step(orca_hip_mlp* m) {
+  orca_hip_ctx* ctx = m->ctx;
+  if (m->opt.kind == 1) m->t += 1;
+  // Per-kernel timing needs events around each launch: run eagerly then.
+  if (!m->use_graph || ctx->prof.enabled) {
+    step_body(m, nullptr);
+    return;
+  }
+  if (m->opt.kind == 1)
+    adamw_store_scalars(ctx, m->kdev,
+                        adamw_scalars(m->opt.lr, m->opt.beta1, m->opt.beta2, m->opt.eps, m->opt.weight_decay, m->t),
+                        ctx->stream);
+  if (!m->exec) capture(m);
+  ORCA_HIP_CHECK(hipGraphLaunch(m->exec, ctx->stream));
 }
 
 orca_hip_mlp* checked(orca_hip_mlp* m) {
@@ -243,10 +305,32 @@ int orca_hip_mlp_create(orca_hip_ctx* ctx, const size_t* dims, size_t n_layers, 
     }
     const char* fh = std::getenv("ORCA_HIP_FUSED_HEAD");
     m->fused_head = head_supported(batch, dims[n_layers - 1], C) && !(fh && fh[0] == '0');
-    if (m->fused_head) {
-      m->head.row_loss = m->dev(batch);
-      m->head.row_correct = reinterpret_cast<int*>(m->dev(batch));
+    m->head.row_loss = m->dev(batch);
+    m->head.row_correct = reinterpret_cast<int*>(m->dev(batch));
+    if (opt->kind == 1) m->kdev = reinterpret_cast<AdamWScalars*>(m->dev(sizeof(AdamWScalars) / sizeof(float)));
+    // The largest split-K workspace among the step's GEMMs (they run one after another on one stream).
+    size_t ws = 0;
+    const size_t n_gemm = m->fused_head ? n_layers - 1 : n_layers;
+    for (size_t l = 0; l < n_gemm; ++l) {
+      const size_t K = dims[l], N = dims[l + 1];
+      const float* a = l == 0 ? m->x : m->H[l - 1];
+      const float* g = l + 1 == n_layers ? m->dlogits : m->dz[0];
+      ws = std::max(ws, gemm_workspace_floats(ctx, false, false, batch, N, K, a, K, 0, m->P + m->off[2 * l], N, 0, 1,
+                                              false));
+      ws = std::max(ws, gemm_workspace_floats(ctx, true, false, K, N, batch, a, K, 0, g, N, 0, 1, true));
+      if (l > 0)
+        ws = std::max(ws, gemm_workspace_floats(ctx, false, true, batch, K, N, g, N, 0, m->P + m->off[2 * l], N, 0,
+                                                1, false));
     }
+    if (ws) {
+      m->gemm_ws = m->dev(ws);
+      m->gemm_ws_floats = ws;
+    }
+    // Replaying the captured step measured slower than launching its kernels
+    // on this runtime (784-4096-4096-10: 1.083 against 1.000 ms per step), so
+    // it is opt-in.
+    const char* eg = std::getenv("ORCA_HIP_GRAPH");
+    m->use_graph = eg && eg[0] == '1';
     ORCA_HIP_CHECK(hipStreamSynchronize(ctx->stream));
     *out = m.release();
   });
@@ -310,6 +394,8 @@ int orca_hip_mlp_set_batch(orca_hip_mlp* mlp, const float* x, const float* oneho
     hipStream_t s = mlp->ctx->stream;
     const size_t B = mlp->B, C = mlp->dims[mlp->L];
     ORCA_HIP_CHECK(hipMemcpyAsync(mlp->x, x, B * mlp->dims[0] * sizeof(float), hipMemcpyHostToDevice, s));
+    // The captured step bakes in which target buffer it reads.
+    if ((onehot != nullptr) != (mlp->onehot != nullptr)) invalidate_graph(mlp);
     if (onehot) {
       if (!mlp->onehot) mlp->onehot = mlp->dev(B * C);
       ORCA_HIP_CHECK(hipMemcpyAsync(mlp->onehot, onehot, B * C * sizeof(float), hipMemcpyHostToDevice, s));

@@ -195,14 +195,24 @@ struct GemmEpi {
   const float* mask = nullptr;
   size_t ldmask = 0;
   float* colsum = nullptr;
+  // Optional caller-owned workspace for split-K partials (see
+  // gemm_workspace_floats); without it they come from the context cache.
+  float* ws = nullptr;
+  size_t ws_floats = 0;
 };
+// Workspace floats gemm() needs for this product (0 when K is not split).
+size_t gemm_workspace_floats(orca_hip_ctx* ctx, bool trans_a, bool trans_b, size_t M, size_t N, size_t K,
+                             const float* A, size_t lda, size_t sa, const float* B, size_t ldb, size_t sb,
+                             size_t batch, bool colsum);
 // Batched GEMM: C[b] = op(A[b]) op(B[b]) with element strides sa/sb/sc between batch entries.
 void gemm(orca_hip_ctx* ctx, bool trans_a, bool trans_b, size_t M, size_t N, size_t K, const float* A,
           size_t lda, size_t sa, const float* B, size_t ldb, size_t sb, float* C, size_t ldc, size_t sc,
           size_t batch, const GemmEpi& epi);
 
+// row_loss / row_correct: optional caller-owned [B] workspaces (else from the context cache).
 void softmax_ce(orca_hip_ctx* ctx, const float* logits, size_t B, size_t C, const float* onehot,
-                const int32_t* labels, float* loss, float* dlogits, int32_t* preds, int64_t* correct);
+                const int32_t* labels, float* loss, float* dlogits, int32_t* preds, int64_t* correct,
+                float* row_loss = nullptr, int* row_correct = nullptr);
 
 // Fused classifier head (last Linear with at most HEAD_MAX_CLASSES outputs +
 // softmax cross-entropy); see head.hip.
@@ -223,9 +233,21 @@ void head_backward(orca_hip_ctx* ctx, const float* H, size_t B, size_t K, const 
                    const float* dlogits, bool mask, float* dH, float* dW, float* db, const HeadWorkspace* finish,
                    float* loss, int64_t* correct);
 
+// AdamW's per-step f32 scalars: the f64 expressions of python/orca/optim/adamw.py:64-94
+// rounded to f32 as PyO3 passes them.
+struct AdamWScalars {
+  float decay, b1, omb1, b2, omb2, c1, c2, eps, lr;
+};
+AdamWScalars adamw_scalars(double lr, double b1, double b2, double eps, double wd, int64_t t);
+// Writes s to device memory `dst` with a one-thread kernel on `stream` (by-value
+// argument: a captured graph that reads dst sees each step's values).
+void adamw_store_scalars(orca_hip_ctx* ctx, AdamWScalars* dst, const AdamWScalars& s, hipStream_t stream);
+
 // Optimizer passes over flat buffers, on `stream` (the context stream when null).
+// adamw: the scalars come from (lr, ..., t), or from device memory when dev_scalars is set.
 void adamw(orca_hip_ctx* ctx, float* p, const float* g, float* m, float* v, size_t n, double lr, double b1,
-           double b2, double eps, double wd, int64_t t, hipStream_t stream = nullptr);
+           double b2, double eps, double wd, int64_t t, hipStream_t stream = nullptr,
+           const AdamWScalars* dev_scalars = nullptr);
 void sgd(orca_hip_ctx* ctx, float* p, const float* g, size_t n, double lr, hipStream_t stream = nullptr);
 
 }  // namespace orca_hip
