@@ -171,8 +171,12 @@ __global__ void __launch_bounds__(HEAD_THREADS) head_forward_kernel(HeadFwdParam
       wn[j] = i < ng * C ? src[i] : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
     }
   };
-  load_chunk(0);
-  for (int ch = 0; ch < nchunks; ++ch) {
+  // Blocks start at different chunks so they do not all read the same rows
+  // of W from L2 at the same moment.
+  const int rot = blockIdx.x % nchunks;
+  load_chunk(rot);
+  for (int i = 0; i < nchunks; ++i) {
+    const int ch = (i + rot) % nchunks;
     const int ng = min(G, K4 - ch * G);
     __syncthreads();  // the previous chunk's W slices have been read
 #pragma unroll
@@ -184,7 +188,7 @@ __global__ void __launch_bounds__(HEAD_THREADS) head_forward_kernel(HeadFwdParam
 #pragma unroll
     for (int r = 0; r < R; ++r) h[r] = hn[r];
     __syncthreads();
-    if (ch + 1 < nchunks) load_chunk(ch + 1);
+    if (i + 1 < nchunks) load_chunk((ch + 1) % nchunks);
     if (tid < ng) {
       const floatx4* ws = reinterpret_cast<const floatx4*>(smem + tid * 4 * C);
       float w[4 * C];
@@ -345,7 +349,13 @@ __global__ void __launch_bounds__(HEAD_THREADS) head_backward_kernel(HeadBwdPara
 #pragma unroll
   for (int c = 0; c < C; ++c) adb[c] = 0.0f;
 
-  for (int base = rl; base < p.B; base += ROW_LANES * BWD_UNROLL) {
+  // Blocks start at different row groups so they do not all read the same
+  // rows of dlogits at the same moment.
+  constexpr int GROUP = ROW_LANES * BWD_UNROLL;
+  const int ngroups = (p.B + GROUP - 1) / GROUP;
+  const int rot = blockIdx.x % ngroups;
+  for (int gi = 0; gi < ngroups; ++gi) {
+    const int base = ((gi + rot) % ngroups) * GROUP + rl;
     float d[BWD_UNROLL][C];
     floatx4 h[BWD_UNROLL];
 #pragma unroll

@@ -241,3 +241,31 @@ def test_mlp_step_config1_sgd(ctx, use_labels):
         assert_close(p, pr, what=f"param {i}")
     np.testing.assert_array_equal(tr.preds(), ref["preds"])
     assert tr.metrics()[1] == ref["correct"]
+
+
+@pytest.mark.parametrize("dims,batch,kind", [
+    ((20, 7), 33, "sgd"),              # one layer: the fused head reads the input, no ReLU below it
+    ((37, 50, 19), 33, "adamw"),       # 19 classes (GEMM head), widths not multiples of 4 (generic GEMM)
+    ((784, 128, 128, 10), 1, "adamw"), # batch of one
+    ((64, 96, 64, 32, 16), 70, "sgd"), # four layers, 16 classes (widest fused head), ragged batch
+    ((33, 41, 5), 129, "adamw"),       # head input width 41 (not a multiple of 4: GEMM head path)
+])
+def test_mlp_step_odd_shapes(ctx, dims, batch, kind):
+    """The trainer on shapes off the BASELINE grid, two steps against the oracle."""
+    params, x, labels, onehot = synth.mlp_problem(7, dims, batch)
+    opt = dict(kind=kind, lr=0.05 if kind == "sgd" else 1e-3, weight_decay=0.0 if kind == "sgd" else 0.01)
+    tr = MLPTrainer(ctx, dims, batch, kind=kind, lr=opt["lr"], weight_decay=opt["weight_decay"])
+    tr.set_params(params)
+    tr.set_batch(x, onehot=onehot)
+    losses = []
+    for _ in range(2):
+        tr.step()
+        losses.append(tr.metrics()[0])
+    ref = O.mlp_train(dims, params, x, onehot, O.make_opt(kind, opt["lr"], opt["weight_decay"]), steps=2)
+    assert_close(np.array(losses, np.float32), ref["losses"], what="loss")
+    for i, (g, gr) in enumerate(zip(tr.grads(), ref["grads"])):
+        assert_close(g, gr, what=f"grad {i}")
+    for i, (p, pr) in enumerate(zip(tr.params(), ref["params"])):
+        assert_close(p, pr, what=f"param {i}")
+    np.testing.assert_array_equal(tr.preds(), ref["preds"])
+    tr.close()
