@@ -131,6 +131,76 @@ __device__ __forceinline__ void read_frag(const float* __restrict__ s, int base,
   }
 }
 
+// Epilogue of one wave: MT x NT accumulator blocks, lane (h, i), register r
+// of block (mt, nt) holding C[row0 + mt*32 + (r/4)*8 + h*4 + r%4][col0 + nt*32 + i].
+// EPI is a compile-time constant and FULL (every row < M, every column < N)
+// drops the per-element checks, so the stores are straight-line code: all
+// mask loads are issued before the first store and no store waits on another
+// (vmcnt counts stores as well as loads, so a load between two stores would
+// make each store wait for the one before it).
+template <int EPI, bool FULL, int MT, int NT>
+__device__ __forceinline__ void store_acc(const floatx16 (&acc)[MT][NT], float* __restrict__ C, int64_t ldc, int row0,
+                                          int col0, int M, int N, const float* __restrict__ bias,
+                                          const float* __restrict__ mask, int64_t ldmask) {
+  const int lane = threadIdx.x & 63, h = lane >> 5, i = lane & 31;
+  auto row_of = [&](int mt, int r) { return row0 + mt * 32 + (r >> 2) * 8 + h * 4 + (r & 3); };
+  auto col_of = [&](int nt) { return col0 + nt * 32 + i; };
+  auto in = [&](int mt, int nt, int r) { return FULL || (row_of(mt, r) < M && col_of(nt) < N); };
+  float bv[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt)
+    bv[nt] = (EPI == ORCA_HIP_EPI_BIAS || EPI == ORCA_HIP_EPI_BIAS_RELU) && (FULL || col_of(nt) < N) ? bias[col_of(nt)]
+                                                                                                   : 0.0f;
+  float mk[MT][NT][EPI == ORCA_HIP_EPI_RELU_MASK ? 16 : 1];
+  if (EPI == ORCA_HIP_EPI_RELU_MASK) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          mk[mt][nt][r & (EPI == ORCA_HIP_EPI_RELU_MASK ? 15 : 0)] =
+              in(mt, nt, r) ? mask[(int64_t)row_of(mt, r) * ldmask + col_of(nt)] : 0.0f;
+  }
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        float v = acc[mt][nt][r];
+        if (EPI == ORCA_HIP_EPI_BIAS) {
+          v = v + bv[nt];
+        } else if (EPI == ORCA_HIP_EPI_BIAS_RELU) {
+          v = v + bv[nt];
+          v = v > 0.0f ? v : 0.0f;
+        } else if (EPI == ORCA_HIP_EPI_RELU_MASK) {
+          v = mk[mt][nt][r & (EPI == ORCA_HIP_EPI_RELU_MASK ? 15 : 0)] > 0.0f ? v : 0.0f;
+        }
+        if (in(mt, nt, r)) C[(int64_t)row_of(mt, r) * ldc + col_of(nt)] = v;
+      }
+}
+
+// The block's epilogue: the kind is uniform, so one specialised store path runs.
+template <int MT, int NT>
+__device__ __forceinline__ void write_tile(const floatx16 (&acc)[MT][NT], float* C, int64_t ldc, int epi, int row0,
+                                           int col0, bool full, const GemmParams& p) {
+#define ORCA_STORE_ACC(E)                                                                          \
+  do {                                                                                             \
+    if (full)                                                                                      \
+      store_acc<E, true>(acc, C, ldc, row0, col0, p.M, p.N, p.bias, p.mask, p.ldmask);             \
+    else                                                                                           \
+      store_acc<E, false>(acc, C, ldc, row0, col0, p.M, p.N, p.bias, p.mask, p.ldmask);            \
+  } while (0)
+  switch (epi) {
+    case ORCA_HIP_EPI_BIAS: ORCA_STORE_ACC(ORCA_HIP_EPI_BIAS); break;
+    case ORCA_HIP_EPI_BIAS_RELU: ORCA_STORE_ACC(ORCA_HIP_EPI_BIAS_RELU); break;
+    case ORCA_HIP_EPI_RELU_MASK: ORCA_STORE_ACC(ORCA_HIP_EPI_RELU_MASK); break;
+    default: ORCA_STORE_ACC(ORCA_HIP_EPI_NONE); break;
+  }
+#undef ORCA_STORE_ACC
+}
+
 // TA: A stored [K][lda] (A^T), else [M][lda].  TB: B stored [N][ldb] (B^T), else [K][ldb].
 // Block tile BM x BN, four waves as 2 x 2, wave tile (BM/2) x (BN/2) = MT x NT
 // MFMA 32x32 blocks.
@@ -200,9 +270,6 @@ __global__ void __launch_bounds__(NTHREADS) gemm_mfma_f32_kernel(GemmParams p) {
 #pragma unroll
           for (int nt = 0; nt < NT; ++nt)
             acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[mt][q], fb[nt][q], acc[mt][nt], 0, 0, 0);
-#ifdef ORCA_GEMM_IGLP
-      __builtin_amdgcn_iglp_opt(ORCA_GEMM_IGLP);
-#endif
     }
   };
 
@@ -229,36 +296,11 @@ __global__ void __launch_bounds__(NTHREADS) gemm_mfma_f32_kernel(GemmParams p) {
   // One partial per K-chunk when K is split (reduced in chunk order on the host side).
   if (do_colsum && tid < BN && n0 + tid < p.N) p.colsum[(int64_t)split * p.N + n0 + tid] = cs;
 
-  // Epilogue.  Lane (h, i), register r of block (mt, nt) holds
-  // C[wm*BM/2 + mt*32 + (r/4)*8 + h*4 + r%4][wn*BN/2 + nt*32 + i].
   float* C = p.C + batch * p.sc;
   if (p.splits > 1) C = p.C + (int64_t)bz * p.M * p.N;  // raw partial sums, ld = N
   const int64_t ldc = p.splits > 1 ? p.N : p.ldc;
   const int epi = p.splits > 1 ? ORCA_HIP_EPI_NONE : p.epi;
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-      const int col = n0 + wn * (BN / 2) + nt * 32 + i;
-      if (col >= p.N) continue;
-      float bias = 0.0f;
-      if (epi == ORCA_HIP_EPI_BIAS || epi == ORCA_HIP_EPI_BIAS_RELU) bias = p.bias[col];
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = m0 + wm * (BM / 2) + mt * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
-        if (row >= p.M) continue;
-        float v = acc[mt][nt][r];
-        if (epi == ORCA_HIP_EPI_BIAS) {
-          v = v + bias;
-        } else if (epi == ORCA_HIP_EPI_BIAS_RELU) {
-          v = v + bias;
-          v = v > 0.0f ? v : 0.0f;
-        } else if (epi == ORCA_HIP_EPI_RELU_MASK) {
-          v = p.mask[(int64_t)row * p.ldmask + col] > 0.0f ? v : 0.0f;
-        }
-        C[(int64_t)row * ldc + col] = v;
-      }
-    }
+  write_tile(acc, C, ldc, epi, m0 + wm * (BM / 2), n0 + wn * (BN / 2), m0 + BM <= p.M && n0 + BN <= p.N, p);
 }
 
 // ---------------------------------------------------------------------------
@@ -475,30 +517,7 @@ __global__ void __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2
   if (p.splits > 1) C = p.C + (int64_t)bz * p.M * p.N;
   const int64_t ldc = p.splits > 1 ? p.N : p.ldc;
   const int epi = p.splits > 1 ? ORCA_HIP_EPI_NONE : p.epi;
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-      const int col = n0 + wn * (BN / 2) + nt * 32 + i;
-      if (col >= p.N) continue;
-      float bias = 0.0f;
-      if (epi == ORCA_HIP_EPI_BIAS || epi == ORCA_HIP_EPI_BIAS_RELU) bias = p.bias[col];
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = m0 + wm * (BM / 2) + mt * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
-        if (row >= p.M) continue;
-        float v = acc[mt][nt][r];
-        if (epi == ORCA_HIP_EPI_BIAS) {
-          v = v + bias;
-        } else if (epi == ORCA_HIP_EPI_BIAS_RELU) {
-          v = v + bias;
-          v = v > 0.0f ? v : 0.0f;
-        } else if (epi == ORCA_HIP_EPI_RELU_MASK) {
-          v = p.mask[(int64_t)row * p.ldmask + col] > 0.0f ? v : 0.0f;
-        }
-        C[(int64_t)row * ldc + col] = v;
-      }
-    }
+  write_tile(acc, C, ldc, epi, m0 + wm * (BM / 2), n0 + wn * (BN / 2), m0 + BM <= p.M && n0 + BN <= p.N, p);
 }
 
 // Sums split-K partials in split order and applies the epilogue.
