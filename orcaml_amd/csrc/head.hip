@@ -8,9 +8,7 @@
 //   head_forward_kernel   logits = H W + b (python/orca/nn/linear.py:77-86),
 //                         then per row the loss term, dL/dlogits and the
 //                         argmax of the composed CrossEntropyLoss
-//                         (python/orca/nn/loss.py:59-100); the block that
-//                         finishes last adds the row terms into the mean loss
-//                         and the correct-prediction count.
+//                         (python/orca/nn/loss.py:59-100).
 //   head_backward_kernel  dW = H^T dlogits, db = colsum(dlogits) and
 //                         dH = (dlogits W^T) * [H > 0] (MatMulBackward,
 //                         ExpandBackward's sum_to_shape and ReluBackward,
@@ -29,29 +27,27 @@
 namespace orca_hip {
 namespace {
 
-constexpr int HEAD_THREADS = 256;  // 4 waves
-constexpr int HEAD_PANEL = 16;     // columns of H per backward block
-constexpr int BWD_UNROLL = 4;      // rows per thread whose loads are in flight together
+constexpr int FWD_THREADS = 512;  // 8 waves
+constexpr int FWD_GPT = 2;        // float4 column groups of H per thread per pass
+constexpr int BWD_THREADS = 512;  // 8 waves: 4 column groups x 128 row lanes
+constexpr int BWD_ROW_LANES = BWD_THREADS / 4;
+constexpr int HEAD_PANEL = 16;                            // columns of H per backward block
+constexpr int FINISH_THREADS = 256;
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef float floatx2 __attribute__((ext_vector_type(2)));
 
 // Rows per forward block (one wave per row in the loss phase): 4, or 2 for
-// C > 10 so that the accumulators and W's slice stay in registers.
+// C > 10 so that a thread's W slices and accumulators stay in registers.
 template <int C>
 constexpr int fwd_rows() {
   return C <= 10 ? 4 : 2;
 }
-// Float4 column groups of H per forward W chunk: the chunk's 4 x groups rows
-// of W (groups x C float4s) are staged in LDS, at most 40 KiB.
+// Rows per backward thread per row group (a group is 128 x that many rows):
+// 8, or 4 for C > 10, again to stay in registers.
 template <int C>
-constexpr int fwd_chunk_groups() {
-  return C <= 10 ? 256 : 128;
-}
-template <int C>
-constexpr int fwd_smem_floats() {
-  return fwd_chunk_groups<C>() * 4 * C > fwd_rows<C>() * C * HEAD_THREADS ? fwd_chunk_groups<C>() * 4 * C
-                                                                            : fwd_rows<C>() * C * HEAD_THREADS;
+constexpr int bwd_rows() {
+  return C <= 10 ? 8 : 4;
 }
 
 // Blocks are handed to the 8 XCDs round-robin; with nb a multiple of 8 this
@@ -62,32 +58,71 @@ __device__ __forceinline__ int xcd_local_index(int b, int nb) {
   return (nb & 7) ? b : (b & 7) * (nb >> 3) + (b >> 3);
 }
 
-// Sum of n_out columns of a [n_out][256] LDS array, one output per 4 threads:
-// thread t < 4 n_out adds the 64 values of quarter t % 4 of row t / 4 in
-// index order, then the 4 quarters combine as (q0 + q1) + (q2 + q3).  Every
-// thread of the block must call it; the result is valid on threads with
-// t % 4 == 0.
-__device__ __forceinline__ float sum_rows_256(const float* red, int n_out) {
-  const int t = threadIdx.x;
-  float v = 0.0f;
-  if (t < 4 * n_out) {
-    const floatx4* src = reinterpret_cast<const floatx4*>(red + (t >> 2) * HEAD_THREADS + (t & 3) * 64);
-    floatx4 a[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) a[i] = src[i];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) v = (((v + a[i].x) + a[i].y) + a[i].z) + a[i].w;
-  }
-  v = v + __shfl_xor(v, 1, 64);
-  v = v + __shfl_xor(v, 2, 64);
-  return v;
+// ---- wave folds: sums over groups of lanes without LDS ----
+// The lanes that differ only in lane bits M, M/2, ..., LO (powers of two)
+// form a group, and wave_fold adds each of N values over the group.  While
+// the count is even a step halves it: the lane with bit M clear keeps the
+// first half (adding its partner's copy), the partner the second half, so
+// the group's lanes end up with different slices.  Once the count is odd a
+// step adds the partner's whole set and both lanes hold the same sums.  A
+// lane's slice starts at `base`; fold_shared(N, M, LO) is the mask of the
+// lane bits whose lanes hold identical slices.  Every sum has an order fixed
+// by the lane indices.
+constexpr int fold_len(int n, int m, int lo) {
+  return m < lo ? n : (n % 2 == 0 ? fold_len(n / 2, m / 2, lo) : fold_len(n, m / 2, lo));
+}
+constexpr int fold_shared(int n, int m, int lo) {
+  return m < lo ? 0 : (n % 2 == 0 ? fold_shared(n / 2, m / 2, lo) : (m | fold_shared(n, m / 2, lo)));
 }
 
-// loss = (sum of row terms) * (1/B) and the correct-row count, by one block.
+template <int N, int M, int LO>
+__device__ __forceinline__ void wave_fold(const float (&v)[N], float (&out)[fold_len(N, M, LO)], int& base) {
+  if constexpr (M < LO) {
+#pragma unroll
+    for (int j = 0; j < N; ++j) out[j] = v[j];
+  } else if constexpr (N % 2 == 0) {
+    constexpr int HN = N / 2;
+    const bool up = (threadIdx.x & M) != 0;
+    float nv[HN];
+#pragma unroll
+    for (int j = 0; j < HN; ++j) {
+      const float send = up ? v[j] : v[j + HN];
+      const float keep = up ? v[j + HN] : v[j];
+      nv[j] = keep + __shfl_xor(send, M, 64);
+    }
+    if (up) base += HN;
+    wave_fold<HN, M / 2, LO>(nv, out, base);
+  } else {
+    float nv[N];
+#pragma unroll
+    for (int j = 0; j < N; ++j) nv[j] = v[j] + __shfl_xor(v[j], M, 64);
+    wave_fold<N, M / 2, LO>(nv, out, base);
+  }
+}
+
+// Adds N per-lane values over the lanes of each wave that differ in lane
+// bits M..LO, then over the block's waves: part receives one row of N sums
+// per wave (and per value of the lane bits below LO), and thread t < n_out
+// later adds the rows of its column in wave order.
+template <int N, int M, int LO>
+__device__ __forceinline__ void fold_to_lds(const float (&v)[N], float* part, int row_stride, int row) {
+  constexpr int NF = fold_len(N, M, LO);
+  constexpr int SHARED = fold_shared(N, M, LO);
+  float out[NF];
+  int base = 0;
+  wave_fold<N, M, LO>(v, out, base);
+  if ((threadIdx.x & SHARED) == 0) {
+#pragma unroll
+    for (int j = 0; j < NF; ++j) part[row * row_stride + base + j] = out[j];
+  }
+}
+
+// loss = (sum of row terms) * (1/B) and the correct-row count, by one block
+// (any multiple of 64 threads up to 1024).
 __device__ void finish_rows(const float* __restrict__ row_loss, const int* __restrict__ row_correct, int B, float inv_b,
                             float* loss, int64_t* correct, float* red_f, int* red_i) {
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int per = (B + HEAD_THREADS - 1) / HEAD_THREADS;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, nt = blockDim.x;
+  const int per = (B + nt - 1) / nt;
   float s = 0.0f;
   int n = 0;
   for (int k = 0; k < per; ++k) {
@@ -107,7 +142,7 @@ __device__ void finish_rows(const float* __restrict__ row_loss, const int* __res
   if (tid == 0) {
     float t = red_f[0];
     int64_t c = red_i[0];
-    for (int w = 1; w < HEAD_THREADS / 64; ++w) {
+    for (int w = 1; w < nt / 64; ++w) {
       t = t + red_f[w];
       c += red_i[w];
     }
@@ -131,98 +166,76 @@ struct HeadFwdParams {
   float inv_b;
 };
 
-// Block = fwd_rows<C>() rows x all of K.  K is walked in chunks of G float4
-// column groups; chunk i+1's H and W are loaded into registers while chunk i
-// is multiplied out.  The chunk's rows of W go through LDS (coalesced float4
-// loads in, a 4C-float slice per thread out); thread t multiplies column
-// group t of the chunk for every row.  The 256 partial sums of each logit
-// are added up by sum_rows_256 (fixed order); the bias is added after the
-// product, as a separate f32 operation.
+// Block = fwd_rows<C>() rows x all of K, 512 threads.  Thread t multiplies
+// the float4 column groups t, t + 512 (then t + 1024, ... for K > 4096) of
+// every row: the rows' H values and W's 4 x C slice for those columns come
+// straight from memory, all of a pass's loads issued before the first use,
+// so a block waits for memory once per pass (once in all for K <= 4096).
+// The per-thread partial logits are added over each wave's lanes by a wave
+// fold and over the 8 waves in wave order; the bias is added after the
+// product, as a separate f32 operation.  Then one wave per row runs the
+// softmax cross-entropy.
 template <int C>
-__global__ void __launch_bounds__(HEAD_THREADS) head_forward_kernel(HeadFwdParams p) {
-  constexpr int R = fwd_rows<C>(), G = fwd_chunk_groups<C>();
-  constexpr int WPT = (G * C + HEAD_THREADS - 1) / HEAD_THREADS;  // staged float4s per thread
-  __shared__ __attribute__((aligned(16))) float smem[fwd_smem_floats<C>()];
-  __shared__ float logit[R * C];
+__global__ void __launch_bounds__(FWD_THREADS) head_forward_kernel(HeadFwdParams p) {
+  constexpr int R = fwd_rows<C>(), NV = R * C;
+  constexpr int NW = FWD_THREADS / 64;
+  __shared__ float part[NW * NV];
+  __shared__ float logit[NV];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int r0 = blockIdx.x * R;
   const int nrows = min(R, p.B - r0);
   const int K4 = p.K >> 2;
-  const int nchunks = (K4 + G - 1) / G;
+  const floatx4* W4 = reinterpret_cast<const floatx4*>(p.W);
 
-  float acc[R][C];
+  float acc[NV];
 #pragma unroll
-  for (int r = 0; r < R; ++r)
-#pragma unroll
-    for (int c = 0; c < C; ++c) acc[r][c] = 0.0f;
+  for (int j = 0; j < NV; ++j) acc[j] = 0.0f;
 
-  floatx4 hn[R], wn[WPT];
-  auto load_chunk = [&](int ch) {
-    const int g0 = ch * G, ng = min(G, K4 - g0);
+  for (int g0 = tid; g0 < K4; g0 += FWD_GPT * FWD_THREADS) {
+    floatx4 h[FWD_GPT][R], w[FWD_GPT][C];
 #pragma unroll
-    for (int r = 0; r < R; ++r)
-      hn[r] = (tid < ng && r < nrows)
-                  ? *reinterpret_cast<const floatx4*>(p.H + (int64_t)(r0 + r) * p.K + 4 * (g0 + tid))
-                  : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-    const floatx4* src = reinterpret_cast<const floatx4*>(p.W + (int64_t)g0 * 4 * C);
+    for (int s = 0; s < FWD_GPT; ++s) {
+      const int g = g0 + s * FWD_THREADS;
+      const bool in = g < K4;
 #pragma unroll
-    for (int j = 0; j < WPT; ++j) {
-      const int i = tid + HEAD_THREADS * j;
-      wn[j] = i < ng * C ? src[i] : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+      for (int r = 0; r < R; ++r)
+        h[s][r] = in && r < nrows ? *reinterpret_cast<const floatx4*>(p.H + (int64_t)(r0 + r) * p.K + 4 * g)
+                                  : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int j = 0; j < C; ++j) w[s][j] = in ? W4[(int64_t)g * C + j] : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
     }
-  };
-  // Blocks start at different chunks so they do not all read the same rows
-  // of W from L2 at the same moment.
-  const int rot = blockIdx.x % nchunks;
-  load_chunk(rot);
-  for (int i = 0; i < nchunks; ++i) {
-    const int ch = (i + rot) % nchunks;
-    const int ng = min(G, K4 - ch * G);
-    __syncthreads();  // the previous chunk's W slices have been read
 #pragma unroll
-    for (int j = 0; j < WPT; ++j) {
-      const int i = tid + HEAD_THREADS * j;
-      if (i < G * C) reinterpret_cast<floatx4*>(smem)[i] = wn[j];
-    }
-    floatx4 h[R];
-#pragma unroll
-    for (int r = 0; r < R; ++r) h[r] = hn[r];
-    __syncthreads();
-    if (i + 1 < nchunks) load_chunk((ch + 1) % nchunks);
-    if (tid < ng) {
-      const floatx4* ws = reinterpret_cast<const floatx4*>(smem + tid * 4 * C);
-      float w[4 * C];
+    for (int s = 0; s < FWD_GPT; ++s) {
+      float wf[4 * C];  // W rows 4g .. 4g+3, C values each
 #pragma unroll
       for (int j = 0; j < C; ++j) {
-        const floatx4 v = ws[j];
-        w[4 * j] = v.x;
-        w[4 * j + 1] = v.y;
-        w[4 * j + 2] = v.z;
-        w[4 * j + 3] = v.w;
+        wf[4 * j] = w[s][j].x;
+        wf[4 * j + 1] = w[s][j].y;
+        wf[4 * j + 2] = w[s][j].z;
+        wf[4 * j + 3] = w[s][j].w;
       }
 #pragma unroll
       for (int r = 0; r < R; ++r)
 #pragma unroll
         for (int c = 0; c < C; ++c) {
-          float a = acc[r][c];
-          a = fmaf(h[r].x, w[c], a);
-          a = fmaf(h[r].y, w[C + c], a);
-          a = fmaf(h[r].z, w[2 * C + c], a);
-          a = fmaf(h[r].w, w[3 * C + c], a);
-          acc[r][c] = a;
+          float a = acc[r * C + c];
+          a = fmaf(h[s][r].x, wf[c], a);
+          a = fmaf(h[s][r].y, wf[C + c], a);
+          a = fmaf(h[s][r].z, wf[2 * C + c], a);
+          a = fmaf(h[s][r].w, wf[3 * C + c], a);
+          acc[r * C + c] = a;
         }
     }
   }
 
-  // Reduce the 256 partial sums of each of the R x C logits.
+  fold_to_lds<NV, 32, 1>(acc, part, NV, wave);
   __syncthreads();
+  if (tid < NV) {
+    float z = part[tid];
 #pragma unroll
-  for (int r = 0; r < R; ++r)
-#pragma unroll
-    for (int c = 0; c < C; ++c) smem[(r * C + c) * HEAD_THREADS + tid] = acc[r][c];
-  __syncthreads();
-  const float z = sum_rows_256(smem, R * C);
-  if ((tid & 3) == 0 && tid < 4 * R * C) logit[tid >> 2] = z;
+    for (int w = 1; w < NW; ++w) z = z + part[w * NV + tid];
+    logit[tid] = z;
+  }
   __syncthreads();
 
   // Loss phase: wave w < rows owns row r0 + w; lane c < C holds logit c.
@@ -261,9 +274,9 @@ struct HeadFinish {
   float inv_b;
 };
 
-__global__ void __launch_bounds__(HEAD_THREADS) head_finish_kernel(HeadFinish f, int B) {
-  __shared__ float red_f[HEAD_THREADS / 64];
-  __shared__ int red_i[HEAD_THREADS / 64];
+__global__ void __launch_bounds__(FINISH_THREADS) head_finish_kernel(HeadFinish f, int B) {
+  __shared__ float red_f[FINISH_THREADS / 64];
+  __shared__ int red_i[FINISH_THREADS / 64];
   finish_rows(f.row_loss, f.row_correct, B, f.inv_b, f.loss, f.correct, red_f, red_i);
 }
 
@@ -277,49 +290,31 @@ struct HeadBwdParams {
   HeadFinish fin;   // block 0 also finishes the forward's loss when fin.loss or fin.correct is set
   int B, K;
   int mask;
+  int dl_vec;  // dl is 16-byte aligned: staged with float4 loads
 };
 
-// C floats of row `row` of dl, with the widest loads the row alignment allows.
-template <int C>
-__device__ __forceinline__ void load_dl_row(const float* __restrict__ dl, int row, float (&d)[C]) {
-  const float* r = dl + (int64_t)row * C;
-  if constexpr (C % 4 == 0) {
-#pragma unroll
-    for (int j = 0; j < C / 4; ++j) {
-      const floatx4 v = reinterpret_cast<const floatx4*>(r)[j];
-      d[4 * j] = v.x;
-      d[4 * j + 1] = v.y;
-      d[4 * j + 2] = v.z;
-      d[4 * j + 3] = v.w;
-    }
-  } else if constexpr (C % 2 == 0) {
-#pragma unroll
-    for (int j = 0; j < C / 2; ++j) {
-      const floatx2 v = reinterpret_cast<const floatx2*>(r)[j];
-      d[2 * j] = v.x;
-      d[2 * j + 1] = v.y;
-    }
-  } else {
-#pragma unroll
-    for (int c = 0; c < C; ++c) d[c] = r[c];
-  }
-}
-
 // Block = 16 columns of H (a panel) x all B rows, so no block depends on
-// another.  Thread t owns the float4 column group q = t % 4 of the panel and
-// rows t / 4, + 64, ...; it keeps W's 4 x C slice for its columns and
-// accumulates 4 x C products of dW, loading BWD_UNROLL rows at a time before
-// using any of them.  The 64 row-lane partials of each dW entry are added by
-// sum_rows_256 (fixed order).  Adjacent panels share 128-byte lines of H and
-// dH, so they run on one XCD.
+// another; 512 threads: column group q = t % 4 of the panel, row lane
+// t / 4.  Rows go in groups of 1024 (512 when C > 10): the group's rows of
+// dlogits are staged in LDS and each thread loads its 8 (4) rows of H, all
+// before the first use.
+// A thread keeps W's 4 x C slice for its columns, writes
+// dH = (dlogits W^T) * [H > 0] for its rows and accumulates its 4 x C
+// products of dW in row order; the row lanes are then added by a wave fold
+// and the 8 waves in wave order.  Adjacent panels share 128-byte lines of H
+// and dH, so they run on one XCD.
 template <int C>
-__global__ void __launch_bounds__(HEAD_THREADS) head_backward_kernel(HeadBwdParams p) {
-  constexpr int ROW_LANES = HEAD_THREADS / 4;
-  constexpr int PASS = C <= 10 ? 4 * C : 2 * C;  // dW values per thread reduced per LDS pass
-  __shared__ __attribute__((aligned(16))) float red[PASS * HEAD_THREADS];
-  __shared__ float red_f[HEAD_THREADS / 64];
-  __shared__ int red_i[HEAD_THREADS / 64];
-  const int tid = threadIdx.x;
+__global__ void __launch_bounds__(BWD_THREADS) head_backward_kernel(HeadBwdParams p) {
+  constexpr int NW = BWD_THREADS / 64;
+  constexpr int NV = 4 * C;
+  constexpr int BWD_ROWS = bwd_rows<C>();
+  constexpr int BWD_GROUP = BWD_ROW_LANES * BWD_ROWS;
+  constexpr int SPT = (BWD_GROUP * C / 4 + BWD_THREADS - 1) / BWD_THREADS;  // staged float4s per thread
+  __shared__ __attribute__((aligned(16))) float dls[BWD_GROUP * C];
+  __shared__ float part[NW * 4 * NV];
+  __shared__ float red_f[NW];
+  __shared__ int red_i[NW];
+  const int tid = threadIdx.x, wave = tid >> 6;
   const int q = tid & 3, rl = tid >> 2;
   const int panel = xcd_local_index(blockIdx.x, gridDim.x);
   const int k0 = panel * HEAD_PANEL;
@@ -327,61 +322,98 @@ __global__ void __launch_bounds__(HEAD_THREADS) head_backward_kernel(HeadBwdPara
   const bool kin = k < p.K;
   const bool do_db = p.db != nullptr && panel == 0;
 
-  float w[4 * C];
-  if (kin) {
+  float w[NV];
+  {
     const floatx4* wp = reinterpret_cast<const floatx4*>(p.W + (int64_t)k * C);
 #pragma unroll
     for (int j = 0; j < C; ++j) {
-      const floatx4 v = wp[j];
+      const floatx4 v = kin ? wp[j] : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
       w[4 * j] = v.x;
       w[4 * j + 1] = v.y;
       w[4 * j + 2] = v.z;
       w[4 * j + 3] = v.w;
     }
-  } else {
-#pragma unroll
-    for (int j = 0; j < 4 * C; ++j) w[j] = 0.0f;
   }
-  float acc[4 * C];
+  float acc[NV];
 #pragma unroll
-  for (int j = 0; j < 4 * C; ++j) acc[j] = 0.0f;
+  for (int j = 0; j < NV; ++j) acc[j] = 0.0f;
   float adb[C];
 #pragma unroll
   for (int c = 0; c < C; ++c) adb[c] = 0.0f;
 
-  // Blocks start at different row groups so they do not all read the same
-  // rows of dlogits at the same moment.
-  constexpr int GROUP = ROW_LANES * BWD_UNROLL;
-  const int ngroups = (p.B + GROUP - 1) / GROUP;
-  const int rot = blockIdx.x % ngroups;
+  const int ngroups = (p.B + BWD_GROUP - 1) / BWD_GROUP;
   for (int gi = 0; gi < ngroups; ++gi) {
-    const int base = ((gi + rot) % ngroups) * GROUP + rl;
-    float d[BWD_UNROLL][C];
-    floatx4 h[BWD_UNROLL];
+    const int g0 = gi * BWD_GROUP;
+    const int cnt = min(BWD_GROUP, p.B - g0) * C;  // floats of dlogits in this group
+    const float* src = p.dl + (int64_t)g0 * C;
+    floatx4 st[SPT];
+    floatx4 h[BWD_ROWS];
+    if (p.dl_vec) {
 #pragma unroll
-    for (int u = 0; u < BWD_UNROLL; ++u) {
-      const int row = base + u * ROW_LANES;
-      if (row < p.B) {
-        load_dl_row<C>(p.dl, row, d[u]);
-      } else {
+      for (int j = 0; j < SPT; ++j) {
+        const int e = 4 * (tid + BWD_THREADS * j);
+        if (e + 3 < cnt) {
+          st[j] = *reinterpret_cast<const floatx4*>(src + e);
+        } else {
+          float t[4];
 #pragma unroll
-        for (int c = 0; c < C; ++c) d[u][c] = 0.0f;
+          for (int i = 0; i < 4; ++i) t[i] = e + i < cnt ? src[e + i] : 0.0f;
+          st[j] = floatx4{t[0], t[1], t[2], t[3]};
+        }
       }
+    }
+#pragma unroll
+    for (int u = 0; u < BWD_ROWS; ++u) {
+      const int row = g0 + rl + BWD_ROW_LANES * u;
       h[u] = row < p.B && kin ? *reinterpret_cast<const floatx4*>(p.H + (int64_t)row * p.K + k)
                               : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
     }
+    __syncthreads();  // the previous group's rows of dls have been read
+    if (p.dl_vec) {
 #pragma unroll
-    for (int u = 0; u < BWD_UNROLL; ++u) {
-      const int row = base + u * ROW_LANES;
+      for (int j = 0; j < SPT; ++j) {
+        const int i4 = tid + BWD_THREADS * j;
+        if (4 * i4 < BWD_GROUP * C) reinterpret_cast<floatx4*>(dls)[i4] = st[j];
+      }
+    } else {
+      for (int e = tid; e < BWD_GROUP * C; e += BWD_THREADS) dls[e] = e < cnt ? src[e] : 0.0f;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < BWD_ROWS; ++u) {
+      const int lr = rl + BWD_ROW_LANES * u;
+      const int row = g0 + lr;
       if (row >= p.B) break;
+      float d[C];
+      const float* dr = dls + lr * C;
+      if constexpr (C % 4 == 0) {
+#pragma unroll
+        for (int j = 0; j < C / 4; ++j) {
+          const floatx4 v = reinterpret_cast<const floatx4*>(dr)[j];
+          d[4 * j] = v.x;
+          d[4 * j + 1] = v.y;
+          d[4 * j + 2] = v.z;
+          d[4 * j + 3] = v.w;
+        }
+      } else if constexpr (C % 2 == 0) {
+#pragma unroll
+        for (int j = 0; j < C / 2; ++j) {
+          const floatx2 v = reinterpret_cast<const floatx2*>(dr)[j];
+          d[2 * j] = v.x;
+          d[2 * j + 1] = v.y;
+        }
+      } else {
+#pragma unroll
+        for (int c = 0; c < C; ++c) d[c] = dr[c];
+      }
       const float hv[4] = {h[u].x, h[u].y, h[u].z, h[u].w};
       if (kin && p.dH) {
         float dz[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          float s = d[u][0] * w[e * C];
+          float s = d[0] * w[e * C];
 #pragma unroll
-          for (int c = 1; c < C; ++c) s = fmaf(d[u][c], w[e * C + c], s);
+          for (int c = 1; c < C; ++c) s = fmaf(d[c], w[e * C + c], s);
           dz[e] = (!p.mask || hv[e] > 0.0f) ? s : 0.0f;
         }
         *reinterpret_cast<floatx4*>(p.dH + (int64_t)row * p.K + k) = floatx4{dz[0], dz[1], dz[2], dz[3]};
@@ -389,51 +421,34 @@ __global__ void __launch_bounds__(HEAD_THREADS) head_backward_kernel(HeadBwdPara
 #pragma unroll
       for (int e = 0; e < 4; ++e)
 #pragma unroll
-        for (int c = 0; c < C; ++c) acc[e * C + c] = fmaf(hv[e], d[u][c], acc[e * C + c]);
+        for (int c = 0; c < C; ++c) acc[e * C + c] = fmaf(hv[e], d[c], acc[e * C + c]);
       if (do_db && q == 0) {
 #pragma unroll
-        for (int c = 0; c < C; ++c) adb[c] = adb[c] + d[u][c];
+        for (int c = 0; c < C; ++c) adb[c] = adb[c] + d[c];
       }
     }
   }
 
-  // dW entry (4 q + e, c) = sum over the 64 row lanes of acc[e * C + c] on
-  // the threads with that q.  LDS row (jj, q) holds those 64 partials for
-  // j = j0 + jj (j = e * C + c); thread t adds LDS row t in row-lane order.
+  // dW entry (4 q + e, c) = the sum over all row lanes of acc[e * C + c] on
+  // the threads with that q.  Lane bits 2..5 are the wave's 16 row lanes and
+  // bits 0..1 are q, so the fold runs over bits 32..4; part row (wave, q).
+  fold_to_lds<NV, 32, 4>(acc, part, NV, wave * 4 + q);
+  __syncthreads();
+  if (tid < 4 * NV) {  // tid = q * NV + j: dW[k0 + 4 q + j / C][j % C] = dW[k0 * C + tid]
+    const int qq = tid / NV, j = tid % NV;
+    float v = part[qq * NV + j];
 #pragma unroll
-  for (int j0 = 0; j0 < 4 * C; j0 += PASS) {
-    __syncthreads();
-#pragma unroll
-    for (int jj = 0; jj < PASS; ++jj) red[(jj * 4 + q) * 64 + rl] = acc[j0 + jj];
-    __syncthreads();
-    if (tid < PASS * 4) {
-      const floatx4* src = reinterpret_cast<const floatx4*>(red + tid * 64);
-      floatx4 a[16];
-#pragma unroll
-      for (int i = 0; i < 16; ++i) a[i] = src[i];
-      float v = 0.0f;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) v = (((v + a[i].x) + a[i].y) + a[i].z) + a[i].w;
-      const int j = j0 + (tid >> 2), qq = tid & 3;
-      const int kk = k0 + 4 * qq + j / C;
-      if (kk < p.K) p.dW[(int64_t)kk * C + j % C] = v;
-    }
+    for (int w2 = 1; w2 < NW; ++w2) v = v + part[(w2 * 4 + qq) * NV + j];
+    if (k0 + 4 * qq + j / C < p.K) p.dW[(int64_t)k0 * C + tid] = v;
   }
   if (do_db) {
     __syncthreads();
-    if (q == 0) {
-#pragma unroll
-      for (int c = 0; c < C; ++c) red[c * 64 + rl] = adb[c];
-    }
+    fold_to_lds<C, 32, 4>(adb, part, C, wave * 4 + q);
     __syncthreads();
-    if (tid < C) {
-      const floatx4* src = reinterpret_cast<const floatx4*>(red + tid * 64);
-      float v = 0.0f;
+    if (tid < C) {  // the q = 0 rows of part hold the partial sums
+      float v = part[tid];
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const floatx4 a = src[i];
-        v = (((v + a.x) + a.y) + a.z) + a.w;
-      }
+      for (int w2 = 1; w2 < NW; ++w2) v = v + part[w2 * 4 * C + tid];
       p.db[tid] = v;
     }
   }
@@ -480,7 +495,7 @@ void head_forward(orca_hip_ctx* ctx, const float* H, size_t B, size_t K, const f
   switch (C) {
 #define HEAD_FWD_CASE(N)                                                                        \
   case N:                                                                                       \
-    hipLaunchKernelGGL(head_forward_kernel<N>, grid, dim3(HEAD_THREADS), 0, ctx->stream, p);   \
+    hipLaunchKernelGGL(head_forward_kernel<N>, grid, dim3(FWD_THREADS), 0, ctx->stream, p);    \
     break;
     HEAD_FWD_CASE(1) HEAD_FWD_CASE(2) HEAD_FWD_CASE(3) HEAD_FWD_CASE(4) HEAD_FWD_CASE(5) HEAD_FWD_CASE(6)
     HEAD_FWD_CASE(7) HEAD_FWD_CASE(8) HEAD_FWD_CASE(9) HEAD_FWD_CASE(10) HEAD_FWD_CASE(11) HEAD_FWD_CASE(12)
@@ -495,7 +510,7 @@ void head_forward(orca_hip_ctx* ctx, const float* H, size_t B, size_t K, const f
 void head_finish(orca_hip_ctx* ctx, const HeadWorkspace& ws, size_t B, float* loss, int64_t* correct) {
   if (!loss && !correct) return;
   HeadFinish f{ws.row_loss, ws.row_correct, loss, correct, 1.0f / (float)B};
-  hipLaunchKernelGGL(head_finish_kernel, dim3(1), dim3(HEAD_THREADS), 0, ctx->stream, f, (int)B);
+  hipLaunchKernelGGL(head_finish_kernel, dim3(1), dim3(FINISH_THREADS), 0, ctx->stream, f, (int)B);
   ORCA_HIP_CHECK(hipGetLastError());
 }
 
@@ -505,8 +520,6 @@ void head_backward(orca_hip_ctx* ctx, const float* H, size_t B, size_t K, const 
   if (!head_supported(B, K, C)) fail(ORCA_HIP_ERR_SHAPE, "head_backward: unsupported shape");
   if (!aligned16(H) || !aligned16(W) || (dH && !aligned16(dH)))
     fail(ORCA_HIP_ERR_INTERNAL, "head_backward: H, W and dH must be 16-byte aligned");
-  if (C % 4 == 0 ? !aligned16(dlogits) : (C % 2 == 0 && (reinterpret_cast<uintptr_t>(dlogits) & 7) != 0))
-    fail(ORCA_HIP_ERR_INTERNAL, "head_backward: dlogits is not aligned for its row length");
   const size_t panels = (K + HEAD_PANEL - 1) / HEAD_PANEL;
   HeadBwdParams p{};
   p.H = H;
@@ -519,13 +532,14 @@ void head_backward(orca_hip_ctx* ctx, const float* H, size_t B, size_t K, const 
   p.B = (int)B;
   p.K = (int)K;
   p.mask = mask ? 1 : 0;
+  p.dl_vec = aligned16(dlogits) ? 1 : 0;
   const dim3 grid((unsigned)panels);
   ProfScope ps(ctx, "head_bwd", 4.0 * (double)B * K * C,
                4.0 * ((double)B * K * (dH ? 2 : 1) + (double)B * C + 2.0 * K * C + C));
   switch (C) {
 #define HEAD_BWD_CASE(N)                                                                        \
   case N:                                                                                       \
-    hipLaunchKernelGGL(head_backward_kernel<N>, grid, dim3(HEAD_THREADS), 0, ctx->stream, p);  \
+    hipLaunchKernelGGL(head_backward_kernel<N>, grid, dim3(BWD_THREADS), 0, ctx->stream, p);   \
     break;
     HEAD_BWD_CASE(1) HEAD_BWD_CASE(2) HEAD_BWD_CASE(3) HEAD_BWD_CASE(4) HEAD_BWD_CASE(5) HEAD_BWD_CASE(6)
     HEAD_BWD_CASE(7) HEAD_BWD_CASE(8) HEAD_BWD_CASE(9) HEAD_BWD_CASE(10) HEAD_BWD_CASE(11) HEAD_BWD_CASE(12)
