@@ -93,6 +93,34 @@ def test_head_exact_on_integers(ctx, B, K, C):
                                   O.relu_backward(O.matmul(dl, O.transpose(W, 0, 1)), H))
 
 
+@pytest.mark.parametrize("B,K,C", [(1024, 4096, 10), (1000, 36, 16), (37, 20, 3), (4096, 64, 7)])
+def test_head_backward_unaligned_dlogits(ctx, B, K, C):
+    """dlogits, dW and db one float past a 16-byte boundary: dlogits is then
+    staged element by element instead of as float4s; the results are the
+    same bits as with aligned buffers (integer data: exact against the oracle)."""
+    rng = np.random.default_rng(11 * B + C)
+    H = int_matrix(rng, (B, K), -3, 4)
+    W = int_matrix(rng, (K, C), -3, 4)
+    dl = int_matrix(rng, (B, C), -5, 6)
+    dHp, dWp = ctx.upload(H), ctx.upload(W)
+    outs = []
+    for off in (0, 1):
+        pad = np.zeros(off, np.float32)
+        dlp = ctx.upload(np.concatenate([pad, dl.ravel()]))
+        gW, gb = ctx.upload(np.zeros(off + K * C, np.float32)), ctx.upload(np.zeros(off + C, np.float32))
+        gH = ctx.alloc(4 * B * K)
+        _lib.call("orca_hip_head_backward", ctx.handle, dHp.ptr, B, K, dWp.ptr, C, dlp.ptr + 4 * off, 1, gH.ptr,
+                  gW.ptr + 4 * off, gb.ptr + 4 * off)
+        outs.append((gH.download(count=B * K).reshape(B, K), gW.download(count=off + K * C)[off:].reshape(K, C),
+                     gb.download(count=off + C)[off:]))
+    for a, b in zip(*outs):
+        np.testing.assert_array_equal(a, b)
+    gH, gW, gb = outs[1]
+    np.testing.assert_array_equal(gW, O.matmul(O.transpose(H, 0, 1), dl))
+    np.testing.assert_array_equal(gb, O.sum_to_shape(dl, (1, C)).reshape(C))
+    np.testing.assert_array_equal(gH, O.relu_backward(O.matmul(dl, O.transpose(W, 0, 1)), H))
+
+
 @pytest.mark.parametrize("B,K,C", HEAD_SHAPES)
 def test_head_matches_composed_reference(ctx, B, K, C):
     rng = np.random.default_rng(7 * B + K + C)
