@@ -264,6 +264,10 @@ int orca_hip_mlp_get_param(orca_hip_mlp* mlp, size_t index, float* host, size_t 
 int orca_hip_mlp_get_grad(orca_hip_mlp* mlp, size_t index, float* host, size_t n);
 /* which = 0: first moment m, 1: second moment v */
 int orca_hip_mlp_get_moment(orca_hip_mlp* mlp, int which, size_t index, float* host, size_t n);
+/* Checkpoint restore of the AdamW moments.  No reference counterpart: the
+ * reference optimizer keeps m and v in Python lists (python/orca/optim/adamw.py:30-31)
+ * and does not save them; here they can be saved and restored with the step count. */
+int orca_hip_mlp_set_moment(orca_hip_mlp* mlp, int which, size_t index, const float* host, size_t n);
 /* Uploads the batch: x [batch][dims[0]] and either one-hot targets
  * [batch][dims[L]] or class labels [batch] (one of the two non-NULL). */
 int orca_hip_mlp_set_batch(orca_hip_mlp* mlp, const float* x, const float* onehot, const int32_t* labels);
@@ -279,8 +283,9 @@ int orca_hip_mlp_get_preds(orca_hip_mlp* mlp, int32_t* host, size_t n);
 /* Forward activations of the last step: layer l < L-1 gives the ReLU output
  * [batch][dims[l+1]], layer L-1 the logits [batch][dims[L]] (synchronises). */
 int orca_hip_mlp_get_activation(orca_hip_mlp* mlp, size_t layer, float* host, size_t n);
-/* AdamW step counter t. */
+/* AdamW step counter t (python/orca/optim/adamw.py:33, 64); set restores it from a checkpoint. */
 int orca_hip_mlp_get_step_count(const orca_hip_mlp* mlp, int64_t* t);
+int orca_hip_mlp_set_step_count(orca_hip_mlp* mlp, int64_t t);
 
 /* ===================== kernel timing ===================== */
 /* When enabled, each GEMM / fused-kernel launch is bracketed by HIP events on

@@ -136,6 +136,7 @@ SIGNATURES = {
     "orca_hip_mlp_get_param": [_P, _SZ, _P, _SZ],
     "orca_hip_mlp_get_grad": [_P, _SZ, _P, _SZ],
     "orca_hip_mlp_get_moment": [_P, _I, _SZ, _P, _SZ],
+    "orca_hip_mlp_set_moment": [_P, _I, _SZ, _P, _SZ],
     "orca_hip_mlp_set_batch": [_P, _P, _P, _P],
     "orca_hip_mlp_batch_ptrs": [_P, _PP, _PP],
     "orca_hip_mlp_step": [_P],
@@ -144,6 +145,7 @@ SIGNATURES = {
     "orca_hip_mlp_get_preds": [_P, _P, _SZ],
     "orca_hip_mlp_get_activation": [_P, _SZ, _P, _SZ],
     "orca_hip_mlp_get_step_count": [_P, ctypes.POINTER(ctypes.c_int64)],
+    "orca_hip_mlp_set_step_count": [_P, ctypes.c_int64],
     "orca_hip_prof_enable": [_P, _I],
     "orca_hip_prof_reset": [_P],
     "orca_hip_prof_report": [_P, ctypes.c_char_p, _SZ],

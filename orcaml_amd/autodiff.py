@@ -98,6 +98,25 @@ class Autodiff:
             return AdStorage(primal, out_id)
         return AdStorage(primal)
 
+    # --- a node with its own backward.  The reference's tape knows a fixed set
+    # of BackwardOp types; a fused op (one kernel for what is several ops)
+    # needs one more kind of node, recorded the same way ---
+    def custom(self, primal, inputs, backward):
+        """Records `primal` as the output of one node over `inputs`;
+        backward(g, backend) returns one gradient storage (or None) per input,
+        accumulated like any other node's."""
+
+        def node(out_id, ids=tuple(s.node_id for s in inputs)):
+            def run(tape, be):
+                g = tape.grads.get(out_id)
+                if g is None:
+                    return
+                for i, gi in zip(ids, backward(g, be)):
+                    if i is not None and gi is not None:
+                        tape.accumulate(i, gi, be)
+            return run
+        return self._record(primal, inputs, node)
+
     def add(self, a, b, shape):
         primal = self.inner.add(a.primal, b.primal, shape)
 
@@ -529,6 +548,38 @@ class Module:
         for m in self._modules.values():
             yield from m.parameters()
 
+    def named_parameters(self, prefix: str = ""):
+        """(name, Parameter) with the names save_weights writes: own parameters,
+        then each submodule's under "<submodule>." (python/orca/nn/module.py:176-184)."""
+        for n, p in self._parameters.items():
+            yield prefix + n, p
+        for n, m in self._modules.items():
+            yield from m.named_parameters(prefix + n + ".")
+
+    def state_dict(self) -> dict:
+        return {n: p.tensor for n, p in self.named_parameters()}
+
+    def save_weights(self, filepath: str) -> None:
+        """python/orca/nn/module.py:169-187: the parameters as a safetensors file."""
+        from .serialize import save_tensors
+        save_tensors(filepath, self.state_dict())
+
+    def load_weights(self, filepath: str) -> None:
+        """python/orca/nn/module.py:189-218: every parameter named in the file
+        is replaced by the file's tensor (others are left alone), which
+        requires grad if the parameter did."""
+        from .serialize import load_tensors
+        params = list(self.named_parameters())
+        if not params:
+            return
+        state = load_tensors(filepath, params[0][1].tensor.ad)
+        for n, p in params:
+            if n in state:
+                t = state[n]
+                if p.tensor.requires_grad:
+                    t.require_grad()
+                p.tensor = t
+
     def __call__(self, *args):
         return self.forward(*args)
 
@@ -579,15 +630,26 @@ class Sequential(Module):
 
 
 class CrossEntropyLoss(Module):
-    """python/orca/nn/loss.py:42-100 (one-hot targets)."""
+    """python/orca/nn/loss.py:42-100 (one-hot targets).
 
-    def __init__(self, reduction: str = "mean"):
+    fused=True (opt-in): when the backend has a fused softmax cross-entropy
+    (HipBackend.softmax_ce), a 2-D prediction with reduction "mean" takes one
+    kernel for the loss and dL/dpred, recorded as one tape node whose backward
+    scales the saved gradient by the incoming one.  The gradient is the
+    composed tape's to rounding (the row sums run in a different order); with
+    the usual seed of 1 it is passed on unchanged."""
+
+    def __init__(self, reduction: str = "mean", fused: bool = False):
         super().__init__()
         if reduction not in ("mean", "sum", "none"):
             raise ValueError(f"Invalid reduction mode: {reduction}")
         self.reduction = reduction
+        self.fused = fused
 
     def forward(self, pred: Tensor, target: Tensor) -> Tensor:
+        if (self.fused and self.reduction == "mean" and len(pred.shape) == 2
+                and hasattr(pred.ad.inner, "softmax_ce")):
+            return _fused_cross_entropy(pred, target)
         batch = pred.shape[0]
         max_pred_base = pred.max_to_shape([batch, 1])
         max_pred = max_pred_base.expand(list(pred.shape))
@@ -604,6 +666,20 @@ class CrossEntropyLoss(Module):
         if self.reduction == "sum":
             return per_batch_loss.sum()
         return per_batch_loss
+
+
+def _fused_cross_entropy(pred: Tensor, target: Tensor) -> Tensor:
+    if pred.shape != target.shape:
+        raise OrcaError(f"Shape mismatch during cross_entropy: expected {list(pred.shape)}, got {list(target.shape)}")
+    if pred.ad is not target.ad:
+        raise OrcaError("Device mismatch: tensors must be on the same device")
+    ad, (B, C) = pred.ad, pred.shape
+    want_grad = ad.grad_enabled and pred.storage.node_id is not None
+    loss, dpred = ad.inner.softmax_ce(pred.storage.primal, target.storage.primal, B, C, want_grad)
+
+    def backward(g, be):  # g: the gradient of the loss, shape [1]
+        return be.mul(be.expand(g, (1,), (B, C)), dpred, (B, C)), None
+    return Tensor(ad, ad.custom(loss, (pred.storage, target.storage), backward), (1,))
 
 
 class MSELoss(Module):
@@ -640,15 +716,31 @@ class Optimizer:
 
 
 class SGD(Optimizer):
-    """python/orca/optim/sgd.py:10-79."""
+    """python/orca/optim/sgd.py:10-79.
 
-    def __init__(self, parameters, lr=0.01, momentum=0.0, weight_decay=0.0, dampening=0.0):
+    fused=True (opt-in): with momentum = weight_decay = 0 and a backend that
+    has sgd_step_, each parameter's update p - g * f32(lr) is one kernel on
+    a copy of p (the old tensor is left as it was, as the composed update
+    leaves it); the same f32 operations, so the same bits."""
+
+    def __init__(self, parameters, lr=0.01, momentum=0.0, weight_decay=0.0, dampening=0.0, fused: bool = False):
         super().__init__(parameters)
         self.lr, self.momentum, self.weight_decay, self.dampening = lr, momentum, weight_decay, dampening
+        self.fused = fused
         self._velocity = [None] * len(self.parameters)
 
     def step(self) -> None:
         ad = self.parameters[0].tensor.ad
+        if (self.fused and self.momentum == 0.0 and self.weight_decay == 0.0
+                and hasattr(ad.inner, "sgd_step_")):
+            for p in self.parameters:
+                grad = p.tensor.grad()
+                if grad is None:
+                    continue
+                new = ad.inner.clone(p.tensor.storage.primal)
+                ad.inner.sgd_step_(new, grad.storage.primal, _numel(p.tensor.shape), self.lr)
+                p.update(_new_leaf(ad, new, p.tensor.shape))
+            return
         with no_grad(ad):
             for i, p in enumerate(self.parameters):
                 grad = p.tensor.grad()
@@ -672,14 +764,42 @@ class SGD(Optimizer):
 
 
 class AdamW(Optimizer):
-    """python/orca/optim/adamw.py:12-99."""
+    """python/orca/optim/adamw.py:12-99.
 
-    def __init__(self, parameters, lr=0.001, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.01):
+    fused=True (opt-in): with a backend that has adamw_step_, each
+    parameter's update is one kernel (the same f32 operations in the same
+    order, so the same bits) on a copy of p, with m and v updated in place
+    (they belong to the optimizer alone).
+
+    state_dict / load_state_dict carry m, v and t, which the reference does
+    not save."""
+
+    def __init__(self, parameters, lr=0.001, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.01, fused: bool = False):
         super().__init__(parameters)
         self.lr, (self.beta1, self.beta2), self.eps, self.weight_decay = lr, betas, eps, weight_decay
+        self.fused = fused
         self.t = 0
         self.m = [Tensor.zeros(p.tensor.ad, p.tensor.shape) for p in self.parameters]
         self.v = [Tensor.zeros(p.tensor.ad, p.tensor.shape) for p in self.parameters]
+
+    def state_dict(self) -> dict:
+        """{"m.<i>": Tensor, "v.<i>": Tensor, "t": int} for parameter i in optimizer order."""
+        out = {"t": self.t}
+        for i in range(len(self.parameters)):
+            out[f"m.{i}"], out[f"v.{i}"] = self.m[i], self.v[i]
+        return out
+
+    def load_state_dict(self, state: dict) -> None:
+        n = len(self.parameters)
+        for i in range(n):
+            for key, slots in ((f"m.{i}", self.m), (f"v.{i}", self.v)):
+                t = state[key]
+                if tuple(t.shape) != tuple(self.parameters[i].tensor.shape):
+                    raise OrcaError(f"Shape mismatch during load_state_dict: {key} expected "
+                                    f"{list(self.parameters[i].tensor.shape)}, got {list(t.shape)}")
+                # a private copy: the fused step updates moments in place
+                slots[i] = Tensor(t.ad, AdStorage(t.ad.inner.clone(t.storage.primal)), t.shape)
+        self.t = int(state["t"])
 
     def step(self) -> None:
         grads = []
@@ -693,6 +813,14 @@ class AdamW(Optimizer):
             return
         self.t += 1
         ad = self.parameters[0].tensor.ad
+        if self.fused and hasattr(ad.inner, "adamw_step_"):
+            for i, p, grad in grads:
+                new = ad.inner.clone(p.tensor.storage.primal)
+                ad.inner.adamw_step_(new, grad.storage.primal, self.m[i].storage.primal, self.v[i].storage.primal,
+                                     _numel(p.tensor.shape), self.lr, self.beta1, self.beta2, self.eps,
+                                     self.weight_decay, self.t)
+                p.update(_new_leaf(ad, new, p.tensor.shape))
+            return
         with no_grad(ad):
             for i, p, grad in grads:
                 decayed = p.tensor * (1.0 - self.lr * self.weight_decay)
@@ -709,6 +837,17 @@ class AdamW(Optimizer):
                 new_leaf = new_tensor.detach()
                 new_leaf.require_grad()
                 p.update(new_leaf)
+
+
+def _numel(shape) -> int:
+    return int(np.prod(shape, dtype=np.int64))
+
+
+def _new_leaf(ad: Autodiff, storage, shape) -> Tensor:
+    """detach() + require_grad() of an updated parameter (sgd.py:76-79, adamw.py:95-99)."""
+    t = Tensor(ad, AdStorage(storage), shape)
+    t.require_grad()
+    return t
 
 
 def build_mlp(ad: Autodiff, params) -> Sequential:

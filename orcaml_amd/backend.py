@@ -254,3 +254,37 @@ class HipBackend:
         res = ctypes.c_int()
         _lib.call("orca_hip_has_nan_or_inf", self.ctx.handle, s.ptr, s.n, dtype, ctypes.byref(res))
         return bool(res.value)
+
+    # ---- fused paths: inherent methods beside the trait (the reference's
+    # trait has no loss or optimizer op; nn.CrossEntropyLoss(fused=True),
+    # optim.SGD / AdamW(fused=True) call these when the backend has them) ----
+    def clone(self, s: HipStorage) -> HipStorage:
+        """A new buffer holding the same values (device to device)."""
+        s = self._plain(s)
+        out = HipStorage(self.ctx.alloc(4 * max(s.n, 1)), s.n)
+        if s.n:
+            self.ctx.d2d(out.buf, s.buf, 4 * s.n)
+        return out
+
+    def softmax_ce(self, logits: HipStorage, onehot: HipStorage, B: int, C: int, want_grad: bool = True):
+        """Mean softmax cross-entropy of [B, C] logits against one-hot targets
+        and, if want_grad, dL/dlogits for a loss seed of 1, in one kernel
+        (orca_hip_softmax_ce).  Returns (loss [1], dlogits [B, C] or None)."""
+        logits, onehot = self._plain(logits), self._plain(onehot)
+        loss = HipStorage(self.ctx.alloc(4), 1)
+        dl = HipStorage(self.ctx.alloc(4 * max(B * C, 1)), B * C) if want_grad else None
+        _lib.call("orca_hip_softmax_ce", self.ctx.handle, logits.ptr, B, C, onehot.ptr, None, loss.ptr,
+                  dl.ptr if dl is not None else None, None, None)
+        return loss, dl
+
+    def adamw_step_(self, p: HipStorage, g: HipStorage, m: HipStorage, v: HipStorage, n: int, lr: float,
+                    beta1: float, beta2: float, eps: float, weight_decay: float, t: int) -> None:
+        """In place on p, m, v (orca_hip_adamw_step)."""
+        g = self._plain(g)
+        _lib.call("orca_hip_adamw_step", self.ctx.handle, p.ptr, g.ptr, m.ptr, v.ptr, n, lr, beta1, beta2, eps,
+                  weight_decay, t)
+
+    def sgd_step_(self, p: HipStorage, g: HipStorage, n: int, lr: float) -> None:
+        """In place on p (orca_hip_sgd_step)."""
+        g = self._plain(g)
+        _lib.call("orca_hip_sgd_step", self.ctx.handle, p.ptr, g.ptr, n, lr)

@@ -386,6 +386,21 @@ int orca_hip_mlp_get_moment(orca_hip_mlp* mlp, int which, size_t index, float* h
   return read_arena(mlp, mlp ? (which == 0 ? mlp->Mo : mlp->Vo) : nullptr, index, host, n);
 }
 
+// Restores optimizer state from a checkpoint (the reference keeps m and v in
+// Python lists, python/orca/optim/adamw.py:30-31, and never saves them).
+int orca_hip_mlp_set_moment(orca_hip_mlp* mlp, int which, size_t index, const float* host, size_t n) {
+  return guard([&] {
+    checked(mlp);
+    check_index(mlp, index, n);
+    if (which != 0 && which != 1) fail(ORCA_HIP_ERR_INTERNAL, "moment index must be 0 (m) or 1 (v)");
+    float* arena = which == 0 ? mlp->Mo : mlp->Vo;
+    if (!arena) fail(ORCA_HIP_ERR_INTERNAL, "state not present for this optimizer");
+    ORCA_HIP_CHECK(hipMemcpyAsync(arena + mlp->off[index], host, n * sizeof(float), hipMemcpyHostToDevice,
+                                  mlp->ctx->stream));
+    ORCA_HIP_CHECK(hipStreamSynchronize(mlp->ctx->stream));
+  });
+}
+
 int orca_hip_mlp_set_batch(orca_hip_mlp* mlp, const float* x, const float* onehot, const int32_t* labels) {
   return guard([&] {
     checked(mlp);
@@ -475,6 +490,15 @@ int orca_hip_mlp_get_step_count(const orca_hip_mlp* mlp, int64_t* t) {
   return guard([&] {
     if (!mlp || !t) fail(ORCA_HIP_ERR_INTERNAL, "null argument");
     *t = mlp->t;
+  });
+}
+
+// The next step runs as step t + 1 (adamw.py:64 increments before use).
+int orca_hip_mlp_set_step_count(orca_hip_mlp* mlp, int64_t t) {
+  return guard([&] {
+    checked(mlp);
+    if (t < 0) fail(ORCA_HIP_ERR_INTERNAL, "step count must be >= 0");
+    mlp->t = t;
   });
 }
 

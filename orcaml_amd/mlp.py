@@ -22,6 +22,7 @@ class MLPTrainer:
         if kind not in ("sgd", "adamw"):
             raise ValueError(f"unknown optimizer {kind!r}")
         self.ctx = ctx
+        self.kind = kind
         self.dims = tuple(int(d) for d in dims)
         self.batch = int(batch)
         self.n_layers = len(self.dims) - 1
@@ -112,3 +113,21 @@ class MLPTrainer:
         t = ctypes.c_int64()
         _lib.call("orca_hip_mlp_get_step_count", self.handle, ctypes.byref(t))
         return int(t.value)
+
+    def set_moments(self, which: int, arrays) -> None:
+        """Restores AdamW's m (which = 0) or v (which = 1) for every parameter."""
+        for i, a in enumerate(arrays):
+            a = np.ascontiguousarray(a, np.float32)
+            _lib.call("orca_hip_mlp_set_moment", self.handle, which, i, a.ctypes.data_as(ctypes.c_void_p), a.size)
+
+    def set_step_count(self, t: int) -> None:
+        _lib.call("orca_hip_mlp_set_step_count", self.handle, int(t))
+
+    def save(self, path: str) -> None:
+        """Parameters (named as the equivalent nn.Sequential's) and AdamW state, as safetensors."""
+        from .serialize import save_trainer
+        save_trainer(path, self)
+
+    def load(self, path: str) -> None:
+        from .serialize import load_trainer
+        load_trainer(path, self)

@@ -19,3 +19,11 @@ def ctx():
     c = Context(0)
     yield c
     c.close()
+
+
+@pytest.fixture(scope="session")
+def hb(ctx):
+    """HipBackend on the session's context."""
+    from orcaml_amd.backend import HipBackend
+
+    return HipBackend(ctx)

@@ -106,3 +106,26 @@ class OracleBackend:
 
     def has_nan_or_inf(self, s, dtype=0):
         return O.has_nan_or_inf(s)
+
+    def to_bytes(self, s):
+        return np.ascontiguousarray(s, "<f4").tobytes()
+
+    def from_bytes(self, shape, data, dtype=0):
+        a = np.frombuffer(data, "<f4").copy()
+        assert a.size == _n(shape)
+        return a
+
+    # ---- the fused paths' methods, on the oracle ----
+    def clone(self, s):
+        return np.array(s, np.float32, copy=True)
+
+    def softmax_ce(self, logits, onehot, B, C, want_grad=True):
+        loss, d = O.cross_entropy(logits.reshape(B, C), onehot.reshape(B, C))
+        return np.array([loss], np.float32), (d.reshape(-1) if want_grad else None)
+
+    def adamw_step_(self, p, g, m, v, n, lr, beta1, beta2, eps, weight_decay, t):
+        p2, m2, v2 = O.adamw_update(p, g, m, v, t, lr=lr, weight_decay=weight_decay, betas=(beta1, beta2), eps=eps)
+        p[:], m[:], v[:] = p2, m2, v2
+
+    def sgd_step_(self, p, g, n, lr):
+        p[:] = O.sgd_update(p, g, lr)

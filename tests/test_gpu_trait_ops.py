@@ -17,13 +17,6 @@ from tests.util import assert_close, assert_close_scaled
 pytestmark = pytest.mark.gpu
 
 
-@pytest.fixture(scope="module")
-def hb(request):
-    from orcaml_amd.backend import HipBackend
-
-    return HipBackend(request.getfixturevalue("ctx"))
-
-
 def up(hb, a):
     a = np.ascontiguousarray(a, np.float32)
     return hb.from_f32_slice(a.shape, a.reshape(-1))
