@@ -69,7 +69,7 @@ int orc_transpose(const float* in, float* out, const size_t* dims, size_t rank,
 int orc_matmul(const float* a, const float* b, float* out, const size_t* a_dims, size_t a_rank,
                const size_t* b_dims, size_t b_rank);                       /* 130-221 */
 
-/* ---- MLP training step (SURVEY Appendix A order) ---- */
+/* ---- MLP training step: the reference's op order (linear.py:77-86 forward, loss.py:59-100, tape.rs:107-118 reverse walk) ---- */
 typedef struct {
   int kind;            /* 0 = SGD, 1 = AdamW */
   double lr;

@@ -251,7 +251,7 @@ def test_mlp_step_config1_sgd(ctx, use_labels):
     ((33, 41, 5), 129, "adamw"),       # head input width 41 (not a multiple of 4: GEMM head path)
 ])
 def test_mlp_step_odd_shapes(ctx, dims, batch, kind):
-    """The trainer on shapes off the BASELINE grid, two steps against the oracle."""
+    """The trainer on shapes other than the three benchmark MLPs, two steps against the oracle."""
     params, x, labels, onehot = synth.mlp_problem(7, dims, batch)
     opt = dict(kind=kind, lr=0.05 if kind == "sgd" else 1e-3, weight_decay=0.0 if kind == "sgd" else 0.01)
     tr = MLPTrainer(ctx, dims, batch, kind=kind, lr=opt["lr"], weight_decay=opt["weight_decay"])
