@@ -120,10 +120,10 @@ def secondary(ctx) -> dict:
     from orcaml_amd.mlp import MLPTrainer
 
     out = {}
-    for cfg in (1, 2):
-        w = synth.WORKLOADS[cfg]
+    for name in (synth.MLP_SMALL, synth.MLP_MEDIUM):
+        w = synth.WORKLOADS[name]
         o = w["opt"]
-        params, x, labels, onehot = synth.mlp_problem(cfg, w["dims"], w["batch"])
+        params, x, labels, onehot = synth.mlp_problem(w["seed"], w["dims"], w["batch"])
         tr = MLPTrainer(ctx, w["dims"], w["batch"], kind=o["kind"], lr=o["lr"], weight_decay=o.get("weight_decay", 0.0),
                         betas=o.get("betas", (0.9, 0.999)), eps=o.get("eps", 1e-8))
         tr.set_params(params)

@@ -106,12 +106,16 @@ def mlp_problem(seed: int, dims, batch: int):
     return params, x, labels, one_hot(labels, dims[-1])
 
 
-# The five workloads of the MLP hot path: (name, dims, batch, optimizer, steps).
+# The MLP workloads of the hot path by name: generator seed, dims, batch,
+# optimizer, and the number of steps their parity tests run.
+MLP_SMALL = "mlp784-128-128-10_b64_sgd"
+MLP_MEDIUM = "mlp784-1024-1024-10_b256_adamw"
+MLP_LARGE = "mlp784-4096-4096-10_b1024_adamw"
 WORKLOADS = {
-    1: dict(name="mlp784-128-128-10_b64_sgd", dims=(784, 128, 128, 10), batch=64,
-            opt=dict(kind="sgd", lr=0.1), steps=1),
-    2: dict(name="mlp784-1024-1024-10_b256_adamw", dims=(784, 1024, 1024, 10), batch=256,
-            opt=dict(kind="adamw", lr=1e-3, weight_decay=0.01, betas=(0.9, 0.999), eps=1e-8), steps=100),
-    3: dict(name="mlp784-4096-4096-10_b1024_adamw", dims=(784, 4096, 4096, 10), batch=1024,
-            opt=dict(kind="adamw", lr=1e-3, weight_decay=0.01, betas=(0.9, 0.999), eps=1e-8), steps=1),
+    MLP_SMALL: dict(name=MLP_SMALL, seed=1, dims=(784, 128, 128, 10), batch=64,
+                    opt=dict(kind="sgd", lr=0.1), steps=1),
+    MLP_MEDIUM: dict(name=MLP_MEDIUM, seed=2, dims=(784, 1024, 1024, 10), batch=256,
+                     opt=dict(kind="adamw", lr=1e-3, weight_decay=0.01, betas=(0.9, 0.999), eps=1e-8), steps=100),
+    MLP_LARGE: dict(name=MLP_LARGE, seed=3, dims=(784, 4096, 4096, 10), batch=1024,
+                    opt=dict(kind="adamw", lr=1e-3, weight_decay=0.01, betas=(0.9, 0.999), eps=1e-8), steps=1),
 }

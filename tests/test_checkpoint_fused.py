@@ -13,11 +13,11 @@ from orcaml_amd import serialize, synth
 from tests.cpu_backend import OracleBackend
 from tests.util import assert_close
 
-W1 = synth.WORKLOADS[1]
+W1 = synth.WORKLOADS[synth.MLP_SMALL]
 
 
 def problem():
-    params, x, labels, onehot = synth.mlp_problem(1, W1["dims"], W1["batch"])
+    params, x, labels, onehot = synth.mlp_problem(W1["seed"], W1["dims"], W1["batch"])
     return params, x, onehot
 
 

@@ -18,11 +18,11 @@ from tests.util import assert_close, assert_close_scaled
 
 pytestmark = pytest.mark.gpu
 
-W1 = synth.WORKLOADS[1]
+W1 = synth.WORKLOADS[synth.MLP_SMALL]
 
 
 def problem():
-    params, x, labels, onehot = synth.mlp_problem(1, W1["dims"], W1["batch"])
+    params, x, labels, onehot = synth.mlp_problem(W1["seed"], W1["dims"], W1["batch"])
     return params, x, labels, onehot
 
 
@@ -110,12 +110,12 @@ def make_trainer(ctx, wl):
     return MLPTrainer(ctx, w["dims"], w["batch"], kind=o["kind"], lr=o["lr"], weight_decay=o.get("weight_decay", 0.0))
 
 
-@pytest.mark.parametrize("workload", [1, 2])
+@pytest.mark.parametrize("workload", [synth.MLP_SMALL, synth.MLP_MEDIUM])
 def test_trainer_checkpoint_resume_matches_uninterrupted(ctx, tmp_path, workload):
     """3 steps, save, load into a fresh trainer, 2 more steps: the same
     parameters, moments, step count and metrics as 5 uninterrupted steps."""
     w = synth.WORKLOADS[workload]
-    params, x, labels, onehot = synth.mlp_problem(workload, w["dims"], w["batch"])
+    params, x, labels, onehot = synth.mlp_problem(w["seed"], w["dims"], w["batch"])
     a = make_trainer(ctx, workload)
     a.set_params(params)
     a.set_batch(x, labels=labels)
@@ -150,9 +150,9 @@ def test_trainer_file_loads_into_the_composed_model(ctx, hb, tmp_path):
     """The trainer's checkpoint names its parameters as nn.Sequential does, so
     the composed model's load_weights reads it; a weights-only file resets
     the trainer's AdamW state."""
-    w = synth.WORKLOADS[2]
-    params, x, labels, onehot = synth.mlp_problem(2, w["dims"], w["batch"])
-    tr = make_trainer(ctx, 2)
+    w = synth.WORKLOADS[synth.MLP_MEDIUM]
+    params, x, labels, onehot = synth.mlp_problem(w["seed"], w["dims"], w["batch"])
+    tr = make_trainer(ctx, synth.MLP_MEDIUM)
     tr.set_params(params)
     tr.set_batch(x, labels=labels)
     tr.step()
@@ -164,7 +164,7 @@ def test_trainer_file_loads_into_the_composed_model(ctx, hb, tmp_path):
         np.testing.assert_array_equal(q.tensor.numpy(), p)
     fw = str(tmp_path / "weights.safetensors")
     model.save_weights(fw)
-    fresh = make_trainer(ctx, 2)
+    fresh = make_trainer(ctx, synth.MLP_MEDIUM)
     fresh.load(fw)
     assert fresh.step_count() == 0
     for p, q in zip(fresh.params(), tr.params()):
@@ -176,10 +176,10 @@ def test_trainer_file_loads_into_the_composed_model(ctx, hb, tmp_path):
 
 
 def test_trainer_load_rejects_other_dims(ctx, tmp_path):
-    tr = make_trainer(ctx, 1)
+    tr = make_trainer(ctx, synth.MLP_SMALL)
     f = str(tmp_path / "t.safetensors")
     tr.save(f)
-    other = make_trainer(ctx, 2)
+    other = make_trainer(ctx, synth.MLP_MEDIUM)
     with pytest.raises(A.OrcaError):
         other.load(f)
     tr.close()

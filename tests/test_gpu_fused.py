@@ -211,7 +211,7 @@ def test_adamw_and_sgd_bit_exact(ctx):
 
 
 def _trainer_run(ctx, w, steps, use_labels=False):
-    params, x, labels, onehot = synth.mlp_problem(1, w["dims"], w["batch"])
+    params, x, labels, onehot = synth.mlp_problem(w["seed"], w["dims"], w["batch"])
     o = w["opt"]
     tr = MLPTrainer(ctx, w["dims"], w["batch"], kind=o["kind"], lr=o["lr"], weight_decay=o.get("weight_decay", 0.0),
                     betas=o.get("betas", (0.9, 0.999)), eps=o.get("eps", 1e-8))
@@ -231,8 +231,8 @@ def _trainer_run(ctx, w, steps, use_labels=False):
 
 
 @pytest.mark.parametrize("use_labels", [False, True])
-def test_mlp_step_config1_sgd(ctx, use_labels):
-    tr, ref, losses = _trainer_run(ctx, synth.WORKLOADS[1], 1, use_labels)
+def test_mlp_step_784_128_128_10_sgd(ctx, use_labels):
+    tr, ref, losses = _trainer_run(ctx, synth.WORKLOADS[synth.MLP_SMALL], 1, use_labels)
     assert_close(losses, ref["losses"], what="loss")
     for i, (g, gr) in enumerate(zip(tr.grads(), ref["grads"])):
         assert_close(g, gr, what=f"grad {i}")

@@ -33,12 +33,12 @@ def assert_same(a, b, what):
             np.testing.assert_array_equal(x, y, err_msg=f"{what}: {key} {i}")
 
 
-@pytest.mark.parametrize("workload,steps", [(1, 6), (2, 6), (3, 3)])
+@pytest.mark.parametrize("workload,steps", [(synth.MLP_SMALL, 6), (synth.MLP_MEDIUM, 6), (synth.MLP_LARGE, 3)])
 def test_graph_replays_match_eager_steps(ctx, monkeypatch, workload, steps):
     w = dict(synth.WORKLOADS[workload])
-    if workload == 1:  # SGD in the workload; also run AdamW so both update paths replay
+    if workload == synth.MLP_SMALL:  # SGD in the workload; also run AdamW so both update paths replay
         w["opt"] = dict(kind="adamw", lr=1e-3, weight_decay=0.01)
-    params, x, labels, onehot = synth.mlp_problem(workload, w["dims"], w["batch"])
+    params, x, labels, onehot = synth.mlp_problem(w["seed"], w["dims"], w["batch"])
     trs = [make(ctx, monkeypatch, w, graph) for graph in (True, False)]
     for tr in trs:
         tr.set_params(params)
@@ -60,8 +60,8 @@ def test_graph_replays_match_eager_steps(ctx, monkeypatch, workload, steps):
 
 def test_graph_replays_back_to_back_sgd(ctx, monkeypatch):
     """Several replays enqueued without a host read in between, then compared."""
-    w = synth.WORKLOADS[1]
-    params, x, labels, onehot = synth.mlp_problem(1, w["dims"], w["batch"])
+    w = synth.WORKLOADS[synth.MLP_SMALL]
+    params, x, labels, onehot = synth.mlp_problem(w["seed"], w["dims"], w["batch"])
     trs = [make(ctx, monkeypatch, w, graph) for graph in (True, False)]
     for tr in trs:
         tr.set_params(params)

@@ -13,7 +13,7 @@ from tests.util import assert_close, assert_close_scaled, int_matrix
 
 pytestmark = pytest.mark.gpu
 
-# (B, K, C): the config-1/2/3 output layers, ragged rows (B not a multiple of
+# (B, K, C): the output layers of the three benchmark MLPs, ragged rows (B not a multiple of
 # the 4-row forward block), one float4 of K, K not a multiple of the 32-column
 # backward panel, the 1- and 16-class extremes, and row-split backward grids.
 HEAD_SHAPES = [(1024, 4096, 10), (64, 128, 10), (256, 1024, 10), (37, 20, 3), (5, 4, 1), (1000, 36, 16),
@@ -182,12 +182,12 @@ def test_head_rejects_unsupported_shapes(ctx):
         assert e.value.code == _lib.ERR_SHAPE
 
 
-@pytest.mark.parametrize("workload", [1, 3])
+@pytest.mark.parametrize("workload", [synth.MLP_SMALL, synth.MLP_LARGE])
 def test_trainer_fused_head_equals_gemm_head(ctx, monkeypatch, workload):
     """The trainer's fused head and its GEMM + softmax-CE path agree on one
     step (both are checked against the oracle elsewhere)."""
     w = synth.WORKLOADS[workload]
-    params, x, labels, onehot = synth.mlp_problem(workload, w["dims"], w["batch"])
+    params, x, labels, onehot = synth.mlp_problem(w["seed"], w["dims"], w["batch"])
     out = {}
     for fused in ("1", "0"):
         monkeypatch.setenv("ORCA_HIP_FUSED_HEAD", fused)

@@ -187,10 +187,10 @@ def composed(ad, dims, params, x, onehot, kind, steps, **opt):
 
 
 @pytest.mark.parametrize("kind,steps", [("sgd", 1), ("adamw", 3)])
-def test_composed_step_config1_on_hip(hb, kind, steps):
+def test_composed_step_mlp784_128_on_hip(hb, kind, steps):
     """The reference's unchanged frontend + tape driving HipBackend's trait ops."""
-    w = synth.WORKLOADS[1]
-    params, x, labels, onehot = synth.mlp_problem(1, w["dims"], w["batch"])
+    w = synth.WORKLOADS[synth.MLP_SMALL]
+    params, x, labels, onehot = synth.mlp_problem(w["seed"], w["dims"], w["batch"])
     opt = dict(lr=0.1) if kind == "sgd" else dict(lr=1e-3, weight_decay=0.01)
     ad = A.Autodiff(hb)
     losses, grads, logits, new_params = composed(ad, w["dims"], params, x, onehot, kind, steps, **opt)
@@ -207,8 +207,8 @@ def test_composed_step_config1_on_hip(hb, kind, steps):
 
 def test_composed_step_allocates_nothing_in_steady_state(hb, ctx):
     """After warm-up the caching allocator serves every buffer of a step."""
-    w = synth.WORKLOADS[1]
-    params, x, labels, onehot = synth.mlp_problem(1, w["dims"], w["batch"])
+    w = synth.WORKLOADS[synth.MLP_SMALL]
+    params, x, labels, onehot = synth.mlp_problem(w["seed"], w["dims"], w["batch"])
     ad = A.Autodiff(hb)
     composed(ad, w["dims"], params, x, onehot, "sgd", 2, lr=0.1)
     composed(ad, w["dims"], params, x, onehot, "sgd", 2, lr=0.1)

@@ -61,7 +61,7 @@ def allowed_outliers(i, size, flips, dims):
     return int(np.ceil(1e-5 * size)) + flips[l] * (dims[l] if i % 2 == 0 else 1)
 
 
-def test_config2_hundred_adamw_steps_teacher_forced(ctx):
+def test_mlp784_1024_b256_hundred_adamw_steps_teacher_forced(ctx):
     """784-1024-1024-10, batch 256, 100 AdamW(1e-3, wd 0.01) steps on one fixed
     batch.  At every step the oracle takes one step from the GPU's own state
     (parameters, moments, t):
@@ -73,10 +73,10 @@ def test_config2_hundred_adamw_steps_teacher_forced(ctx):
         normalises gradients, so near-cancelling moments would turn rounding-
         level gradient differences into parameter differences of order lr;
         the update itself has no rounding freedom)."""
-    w = synth.WORKLOADS[2]
+    w = synth.WORKLOADS[synth.MLP_MEDIUM]
     dims = w["dims"]
     o = w["opt"]
-    params, x, labels, onehot = synth.mlp_problem(2, dims, w["batch"])
+    params, x, labels, onehot = synth.mlp_problem(w["seed"], dims, w["batch"])
     tr = make_trainer(ctx, w, params)
     tr.set_batch(x, onehot=onehot)
     zeros = [np.zeros_like(p) for p in params]
@@ -104,11 +104,11 @@ def test_config2_hundred_adamw_steps_teacher_forced(ctx):
             np.testing.assert_array_equal(got_m[i], m1, err_msg=f"step {step} m {i}")
             np.testing.assert_array_equal(got_v[i], v1, err_msg=f"step {step} v {i}")
         state = dict(params=got_p, m=got_m, v=got_v, t=t)
-    print(f"config2 teacher-forced: {total_flips} ReLU mask flips over {w['steps']} steps")
+    print(f"784-1024-1024-10 teacher-forced: {total_flips} ReLU mask flips over {w['steps']} steps")
     assert tr.step_count() == state["t"] == 100
 
 
-def test_config2_free_running_within_natural_spread(ctx):
+def test_mlp784_1024_b256_free_running_within_natural_spread(ctx):
     """Free-running, 100 AdamW steps amplify rounding (near-zero gradients get
     +-lr updates while t is small), so trajectories from different valid
     summation orders drift apart; per-step parity is the teacher-forced test
@@ -117,8 +117,8 @@ def test_config2_free_running_within_natural_spread(ctx):
     Measured: two CPU GEMM orders (blocked f32, f64-accumulated) differ by up
     to 0.16% of L0 (2.6% of the step's own loss late in training, where it is
     ~1e-3); the GPU differs from the oracle by up to 0.55% of L0."""
-    w = synth.WORKLOADS[2]
-    params, x, labels, onehot = synth.mlp_problem(2, w["dims"], w["batch"])
+    w = synth.WORKLOADS[synth.MLP_MEDIUM]
+    params, x, labels, onehot = synth.mlp_problem(w["seed"], w["dims"], w["batch"])
     tr = make_trainer(ctx, w, params)
     tr.set_batch(x, onehot=onehot)
     losses = []
@@ -136,7 +136,7 @@ def test_config2_free_running_within_natural_spread(ctx):
     l0 = ref[0]
     spread = np.abs(ref - b["losses"]) / l0
     dev = np.abs(gpu - ref) / l0
-    print(f"config2 free-running: max |dL|/L0 GPU {dev.max():.2e}, oracle orders {spread.max():.2e}; "
+    print(f"784-1024-1024-10 free-running: max |dL|/L0 GPU {dev.max():.2e}, oracle orders {spread.max():.2e}; "
           f"final loss gpu {gpu[-1]:.6f} oracle {ref[-1]:.6f}")
     assert np.isfinite(gpu).all()
     assert (np.abs(gpu[:5] - ref[:5]) <= 1e-4 * ref[:5]).all()  # identical until rounding differences can act
@@ -144,7 +144,7 @@ def test_config2_free_running_within_natural_spread(ctx):
     assert gpu[-1] < 0.05 * gpu[0]  # the fixed batch is memorised
 
 
-def test_config3_one_adamw_step(ctx):
+def test_mlp784_4096_b1024_one_adamw_step(ctx):
     """784-4096-4096-10, batch 1024, one AdamW step against the oracle, end to end:
     loss and logits to the path's tolerance (1e-5 abs + 1e-4 rel); gradients and
     updated parameters to that tolerance except for a reported fraction <= 1e-5
@@ -154,9 +154,9 @@ def test_config3_one_adamw_step(ctx):
     printed, and the shared-input layer-wise test below shows the kernels agree
     when the masks are the same.  Argmax / accuracy are exact outside rows whose
     top-2 margin is within rounding."""
-    w = synth.WORKLOADS[3]
+    w = synth.WORKLOADS[synth.MLP_LARGE]
     dims = w["dims"]
-    params, x, labels, onehot = synth.mlp_problem(3, dims, w["batch"])
+    params, x, labels, onehot = synth.mlp_problem(w["seed"], dims, w["batch"])
     tr = make_trainer(ctx, w, params)
     tr.set_batch(x, onehot=onehot)
     tr.step()
@@ -197,7 +197,7 @@ def test_config3_one_adamw_step(ctx):
             report.append(f"{kind}{i}:{n_out}/{allowed}")
             if n_out > allowed:
                 over.append(f"{kind} {i}: {n_out} of {g.size} outside tolerance (allowed {allowed})")
-    print(f"config3 end-to-end: ReLU mask flips layer1 {flips[0]}, layer2 {flips[1]}; "
+    print(f"784-4096-4096-10 end-to-end: ReLU mask flips layer1 {flips[0]}, layer2 {flips[1]}; "
           f"elements outside 1e-5+1e-4|x| / allowed: {' '.join(report)}")
     assert not over, over
     for i, (gg, gr) in enumerate(zip(grads, ref["grads"])):  # sign noise itself is rare
@@ -208,15 +208,15 @@ def test_config3_one_adamw_step(ctx):
     assert abs(correct - ref["correct"]) <= int(ties.sum())
 
 
-def test_config3_layerwise_on_shared_inputs(ctx):
+def test_mlp784_4096_b1024_layerwise_on_shared_inputs(ctx):
     """Each layer of the fused step against the oracle's ops fed the GPU's own
     inputs to that layer (so ReLU masks are identical): forward activations,
     the CE gradient, every dZ-driven gradient -- tight, scale-relative
     tolerance.  End-to-end ReLU mask flips (pre-activations within rounding of
     zero) are counted and must be rare."""
-    w = synth.WORKLOADS[3]
+    w = synth.WORKLOADS[synth.MLP_LARGE]
     dims = w["dims"]
-    params, x, labels, onehot = synth.mlp_problem(3, dims, w["batch"])
+    params, x, labels, onehot = synth.mlp_problem(w["seed"], dims, w["batch"])
     tr = make_trainer(ctx, w, params)
     tr.set_batch(x, onehot=onehot)
     tr.step()
@@ -234,7 +234,7 @@ def test_config3_layerwise_on_shared_inputs(ctx):
                             ("logits", logits, lin(H2, 2))):
         assert_close_scaled(got, want, rtol=1e-5, what=name)
     flips = [int(((O.relu(lin(x, 0)) > 0) != (H1 > 0)).sum()), int(((O.relu(lin(H1, 1)) > 0) != (H2 > 0)).sum())]
-    print(f"config3 ReLU mask flips vs the oracle's own pre-activations: layer1 {flips[0]}, layer2 {flips[1]} "
+    print(f"784-4096-4096-10 ReLU mask flips vs the oracle's own pre-activations: layer1 {flips[0]}, layer2 {flips[1]} "
           f"of {H1.size} each")
     assert max(flips) <= 1e-5 * H1.size
     # backward from the GPU's logits and activations
@@ -248,7 +248,7 @@ def test_config3_layerwise_on_shared_inputs(ctx):
         assert_close_scaled(g, r, rtol=1e-4, what=f"grad {i}")
 
 
-def test_config4_fused_backward_epilogue(ctx):
+def test_ce_and_relu_backward_8192x4096(ctx):
     """Logits [8192, 4096] ~ N(0, 2^2) with int targets -> softmax-CE gradient;
     then ReLU-mask backward on a N(0,1) pre-activation and the bias column sum."""
     B, C = 8192, 4096
@@ -279,7 +279,7 @@ def test_config4_fused_backward_epilogue(ctx):
 
 
 @pytest.mark.timeout(600)
-def test_config5_adamw_2pow28(ctx):
+def test_adamw_2pow28(ctx):
     """AdamW over one flat buffer of 2^28 f32 params, 10 steps from zero moments:
     bit-exact against the oracle on a sample of 2^20 positions (the update is
     elementwise), and finite everywhere."""

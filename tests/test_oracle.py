@@ -164,13 +164,13 @@ def test_bias_gradient_is_column_sum_and_mask_from_preactivation():
     np.testing.assert_allclose(r["grads"][0], x.T @ dz1, rtol=1e-4, atol=1e-8)
 
 
-def test_golden_config1():
+def test_golden_mlp784_128_128_10_b64_sgd():
     """The committed fixture of the 784-128-128-10 / batch 64 / SGD(0.1) step
     (tests/golden/make_golden.py) reproduces bit for bit."""
-    path = os.path.join(GOLDEN, "config1_sgd.npz")
+    path = os.path.join(GOLDEN, "mlp784-128-128-10_b64_sgd.npz")
     gold = np.load(path, allow_pickle=False)
-    w = synth.WORKLOADS[1]
-    params, x, labels, onehot = synth.mlp_problem(1, w["dims"], w["batch"])
+    w = synth.WORKLOADS[synth.MLP_SMALL]
+    params, x, labels, onehot = synth.mlp_problem(w["seed"], w["dims"], w["batch"])
     np.testing.assert_array_equal(labels, gold["labels"])
     assert float(x.astype(np.float64).sum()) == float(gold["x_sum"])
     r = O.mlp_train(w["dims"], params, x, onehot, O.make_opt("sgd", 0.1), steps=1)
