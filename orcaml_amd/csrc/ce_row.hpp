@@ -83,14 +83,68 @@ __device__ __forceinline__ void wave_argmax(float& v, int& idx) {
   idx = __builtin_amdgcn_readlane(idx, 63);
 }
 
+// Row-wide reductions for the per-row functions below.  WaveRed: the row is
+// held by one wave64.  BlockRed: the row is held by a whole block of NW waves;
+// each reduction runs on the DPP network within a wave and then over the
+// waves in wave order through LDS (every thread forms the same total), with
+// barriers, so every thread of the block must take part in each call.
+struct WaveRed {
+  __device__ float sum(float v) const { return wave_sum(v); }
+  __device__ float max(float v) const { return wave_max(v); }
+  __device__ void argmax(float& v, int& idx) const { wave_argmax(v, idx); }
+  __device__ bool any(bool b) const { return __any(b); }
+  // The value `v` of the row's first thread (lane 0).
+  __device__ float first(float v) const { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0)); }
+};
+
+template <int NW>
+struct BlockRed {
+  float* f;  // NW floats of LDS
+  int* n;    // NW ints of LDS
+
+  __device__ float combine(float v, bool is_max) const {
+    const int w = threadIdx.x >> 6;
+    __syncthreads();  // the previous reduction's values have been read
+    if ((threadIdx.x & 63) == 0) f[w] = v;
+    __syncthreads();
+    float t = f[0];
+#pragma unroll
+    for (int k = 1; k < NW; ++k) t = is_max ? (f[k] > t ? f[k] : t) : t + f[k];
+    return t;
+  }
+  __device__ float sum(float v) const { return combine(wave_sum(v), false); }
+  __device__ float max(float v) const { return combine(wave_max(v), true); }
+  __device__ void argmax(float& v, int& idx) const {
+    wave_argmax(v, idx);
+    const int w = threadIdx.x >> 6;
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) {
+      f[w] = v;
+      n[w] = idx;
+    }
+    __syncthreads();
+    v = f[0];
+    idx = n[0];
+#pragma unroll
+    for (int k = 1; k < NW; ++k) argmax_combine(v, idx, f[k], n[k]);
+  }
+  __device__ bool any(bool b) const { return __syncthreads_or(b ? 1 : 0) != 0; }
+  __device__ float first(float v) const {
+    __syncthreads();
+    if (threadIdx.x == 0) f[0] = v;
+    __syncthreads();
+    return f[0];
+  }
+};
+
 // Row argmax with the reference's sequential rule (python/orca/nn/model.py:65-75):
 // best starts at r[0]; a later value replaces it only if strictly greater.
 // Lanes propose their first strict maximum over c >= 1 (NaN never proposes);
 // the winner beats r[0] only if strictly greater, and a NaN r[0] is never beaten.
-// col(j) is the column of the lane's j-th value, increasing in j; column 0 is
-// lane 0's value 0.
-template <int VPL, class Get, class Col, class Valid>
-__device__ __forceinline__ int row_argmax(Get get, Col col, Valid valid) {
+// col(j) is the column of the thread's j-th value, increasing in j; column 0 is
+// value 0 of the row's first thread.
+template <int VPL, class Get, class Col, class Valid, class R = WaveRed>
+__device__ __forceinline__ int row_argmax(Get get, Col col, Valid valid, const R& red = R()) {
   float bv = -INFINITY;
   int bi = INT_MAX;
 #pragma unroll
@@ -104,8 +158,8 @@ __device__ __forceinline__ int row_argmax(Get get, Col col, Valid valid) {
       }
     }
   }
-  wave_argmax(bv, bi);
-  const float first = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(get(0)), 0));
+  red.argmax(bv, bi);
+  const float first = red.first(get(0));
   if (bi == INT_MAX) return 0;
   return (bv > first) ? bi : 0;
 }
@@ -128,16 +182,17 @@ struct CeRowOut {
 // (sum_c (0 + g_lse_c)) / se when se is finite and positive: for one-hot
 // targets only the target's term is nonzero, so the two are the same f32
 // value; other rows keep one division per element.
-template <int VPL, class TVal, class Col, class Valid, class Store>
+template <int VPL, class TVal, class Col, class Valid, class Store, class R = WaveRed>
 __device__ __forceinline__ CeRowOut ce_row(const float (&x)[VPL], Valid valid, TVal tval, Col col, bool labels,
-                                           int label, float inv_b, bool grad, Store store, bool want_argmax) {
+                                           int label, float inv_b, bool grad, Store store, bool want_argmax,
+                                           const R& red = R()) {
   float e[VPL];
   // max_to_shape (init -FLT_MAX, strict >)
   float mx = -FLT_MAX;
 #pragma unroll
   for (int j = 0; j < VPL; ++j)
     if (valid(j) && x[j] > mx) mx = x[j];
-  mx = wave_max(mx);
+  mx = red.max(mx);
   // exp(p - max) and its row sum
   float se = 0.0f;
 #pragma unroll
@@ -145,7 +200,7 @@ __device__ __forceinline__ CeRowOut ce_row(const float (&x)[VPL], Valid valid, T
     e[j] = valid(j) ? expf(x[j] - mx) : 0.0f;
     se = se + e[j];
   }
-  se = wave_sum(se);
+  se = red.sum(se);
   const float lg = logf(fmaxf(se, 1e-7f));
   const float lse = mx + lg;
   // per-row loss: sum_c -(t * (p - lse))
@@ -153,7 +208,7 @@ __device__ __forceinline__ CeRowOut ce_row(const float (&x)[VPL], Valid valid, T
 #pragma unroll
   for (int j = 0; j < VPL; ++j)
     if (valid(j)) pb = pb + (tval(j) * (x[j] - lse)) * -1.0f;
-  pb = wave_sum(pb);
+  pb = red.sum(pb);
 
   if (grad) {
     const float g_tm = inv_b * -1.0f;
@@ -162,7 +217,7 @@ __device__ __forceinline__ CeRowOut ce_row(const float (&x)[VPL], Valid valid, T
 #pragma unroll
       for (int j = 0; j < VPL; ++j)
         if (valid(j)) gse = gse + (0.0f + (0.0f + ((g_tm * tval(j)) * -1.0f)));
-      gse = wave_sum(gse) / se;
+      gse = red.sum(gse) / se;
     } else {
 #pragma unroll
       for (int j = 0; j < VPL; ++j)
@@ -170,7 +225,7 @@ __device__ __forceinline__ CeRowOut ce_row(const float (&x)[VPL], Valid valid, T
           float g_lse = 0.0f + ((g_tm * tval(j)) * -1.0f);
           gse = gse + (0.0f + g_lse) / se;
         }
-      gse = wave_sum(gse);
+      gse = red.sum(gse);
     }
     float gmx = 0.0f;
 #pragma unroll
@@ -180,7 +235,7 @@ __device__ __forceinline__ CeRowOut ce_row(const float (&x)[VPL], Valid valid, T
         float g_sh = gse * e[j];
         gmx = gmx + ((0.0f + g_lse) + (0.0f + (g_sh * -1.0f)));
       }
-    gmx = wave_sum(gmx);
+    gmx = red.sum(gmx);
 #pragma unroll
     for (int j = 0; j < VPL; ++j) {
       if (valid(j)) {
@@ -196,9 +251,106 @@ __device__ __forceinline__ CeRowOut ce_row(const float (&x)[VPL], Valid valid, T
 
   CeRowOut out{pb, 0, 0};
   if (want_argmax) {
-    out.pred = row_argmax<VPL>([&](int j) { return x[j]; }, col, valid);
-    out.target = labels ? label : row_argmax<VPL>(tval, col, valid);
+    out.pred = row_argmax<VPL>([&](int j) { return x[j]; }, col, valid, red);
+    out.target = labels ? label : row_argmax<VPL>(tval, col, valid, red);
   }
+  return out;
+}
+
+// ce_row for class-index targets, t_c = [c == label]: the same f32 operations
+// element by element, without materialising t.  Every term a zero target
+// contributes to the row sums (the loss term and LogBackward's sum) is +0,
+// which leaves a sum unchanged, so those sums are formed from the label's term
+// alone (on its lane; +0 elsewhere) with the same bits as the full sums.  A
+// label outside [0, C) leaves every target zero, as its one-hot row would.
+template <int VPL, class Col, class Valid, class Store, class R = WaveRed>
+__device__ __forceinline__ CeRowOut ce_row_label(const float (&x)[VPL], Valid valid, Col col, int label, float inv_b,
+                                                 bool grad, Store store, bool want_argmax, const R& red = R()) {
+  int jl = -1;  // this lane's slot holding the label column
+#pragma unroll
+  for (int j = 0; j < VPL; ++j)
+    if (valid(j) && col(j) == label) jl = j;
+  float e[VPL];
+  float mx = -FLT_MAX;
+#pragma unroll
+  for (int j = 0; j < VPL; ++j)
+    if (valid(j) && x[j] > mx) mx = x[j];
+  mx = red.max(mx);
+  float se = 0.0f;
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    e[j] = valid(j) ? expf(x[j] - mx) : 0.0f;
+    se = se + e[j];
+  }
+  se = red.sum(se);
+  const float lg = logf(fmaxf(se, 1e-7f));
+  const float lse = mx + lg;
+  // A zero target's loss term (0 * (x - lse)) * -1 is +-0 only while x - lse
+  // is finite; with an infinite or NaN difference it is NaN, and the full sum
+  // is formed as the reference forms it.
+  float pl = 0.0f;
+  bool irregular = false;
+#pragma unroll
+  for (int j = 0; j < VPL; ++j)
+    if (valid(j)) {
+      const float dj = x[j] - lse;
+      if (j == jl) pl = (1.0f * dj) * -1.0f;
+      irregular = irregular || !(fabsf(dj) <= FLT_MAX);
+    }
+  float pb;
+  if (red.any(irregular)) {
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < VPL; ++j)
+      if (valid(j)) s = s + ((j == jl ? 1.0f : 0.0f) * (x[j] - lse)) * -1.0f;
+    pb = red.sum(s);
+  } else {
+    pb = red.sum(pl);
+  }
+
+  if (grad) {
+    const float g_tm = inv_b * -1.0f;
+    const float g_lse_t = 0.0f + ((g_tm * 1.0f) * -1.0f);  // the label's 0 + ((g_tm * t) * -1)
+    const float g_lse_0 = 0.0f + ((g_tm * 0.0f) * -1.0f);  // any other column's (+0)
+    float gse;
+    if (se > 0.0f && se <= FLT_MAX) {
+      gse = red.sum(jl >= 0 ? 0.0f + g_lse_t : 0.0f) / se;
+    } else {
+      gse = 0.0f;
+#pragma unroll
+      for (int j = 0; j < VPL; ++j)
+        if (valid(j)) gse = gse + (0.0f + (j == jl ? g_lse_t : g_lse_0)) / se;
+      gse = red.sum(gse);
+    }
+    // gse is +0, positive, +inf or NaN and e[j] is in [0, 1] or NaN, so
+    // g_sh = gse * e[j] is never negative and never -0.  Then, exactly:
+    //   (0 + g_lse) + (0 + (g_sh * -1)) = 0 - g_sh          (zero target: g_lse = +0)
+    //   (0 + g_ls) + (0 + g_sh)         = g_sh              (zero target: g_ls = -0)
+    //   d + g3 = d where x != max (g3 = +0 and d is never -0),
+    // and the target column keeps the full expressions.
+    const float g_lse_c = 0.0f + g_lse_t;
+    float gmx = 0.0f;
+#pragma unroll
+    for (int j = 0; j < VPL; ++j)
+      if (valid(j)) {
+        const float t = 0.0f - gse * e[j];
+        gmx = gmx + (j == jl ? g_lse_c + t : t);
+      }
+    gmx = red.sum(gmx);
+    const float g3 = 0.0f + gmx;
+    const float g_ls_c = 0.0f + g_tm * 1.0f;
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+      if (valid(j)) {
+        const float g_sh = gse * e[j];
+        const float d = j == jl ? g_ls_c + g_sh : g_sh;
+        store(j, x[j] == mx ? d + g3 : d);
+      }
+    }
+  }
+
+  CeRowOut out{pb, 0, label};
+  if (want_argmax) out.pred = row_argmax<VPL>([&](int j) { return x[j]; }, col, valid, red);
   return out;
 }
 

@@ -69,9 +69,79 @@ __global__ void __launch_bounds__(256) softmax_ce_kernel(const float* __restrict
       dr[col(j)] = v;
     }
   };
-  const CeRowOut r = ce_row<VPL>(x, valid, tval, col, LABELS, label, inv_b, dr != nullptr, store,
-                                 preds || row_correct);
+  CeRowOut r;
+  if constexpr (LABELS)
+    r = ce_row_label<VPL>(x, valid, col, label, inv_b, dr != nullptr, store, preds || row_correct);
+  else
+    r = ce_row<VPL>(x, valid, tval, col, false, label, inv_b, dr != nullptr, store, preds || row_correct);
   if (lane == 0) {
+    row_loss[row] = r.loss;
+    if (preds) preds[row] = r.pred;
+    if (row_correct) row_correct[row] = (r.pred == r.target) ? 1 : 0;
+  }
+}
+
+// Rows of 1025..4096 logits: one 256-thread block per row, 16 values per
+// thread (VEC: float4 column groups tid + 256 q, so every load and store is a
+// coalesced float4; otherwise columns tid + 256 j).  The row reductions run
+// across the block's 4 waves (BlockRed); with 16 values a thread holds few
+// registers, so many rows are in flight.
+template <bool VEC, bool FULL, bool LABELS>
+__global__ void __launch_bounds__(256) softmax_ce_block_kernel(const float* __restrict__ logits, int B, int C,
+                                                               const float* __restrict__ onehot,
+                                                               const int32_t* __restrict__ labels, float inv_b,
+                                                               float* __restrict__ row_loss,
+                                                               float* __restrict__ dlogits,
+                                                               int32_t* __restrict__ preds,
+                                                               int* __restrict__ row_correct) {
+  constexpr int VPT = 16;
+  __shared__ float red_f[4];
+  __shared__ int red_i[4];
+  const BlockRed<4> red{red_f, red_i};
+  const int tid = threadIdx.x;
+  const int row = blockIdx.x;
+  const float* xr = logits + (int64_t)row * C;
+  const float* tr = LABELS ? nullptr : onehot + (int64_t)row * C;
+  float* dr = dlogits ? dlogits + (int64_t)row * C : nullptr;
+  const int label = LABELS ? labels[row] : -1;
+  auto col = [&](int j) -> int { return VEC ? (j >> 2) * 1024 + tid * 4 + (j & 3) : tid + 256 * j; };
+  auto valid = [&](int j) -> bool { return FULL || col(j) < C; };
+  float x[VPT];
+  if (VEC) {
+#pragma unroll
+    for (int q = 0; q < VPT / 4; ++q) {
+      const int c0 = q * 1024 + tid * 4;
+      floatx4 v = {0.0f, 0.0f, 0.0f, 0.0f};
+      if (FULL || c0 < C) v = __builtin_nontemporal_load(reinterpret_cast<const floatx4*>(xr + c0));
+      x[4 * q] = v.x;
+      x[4 * q + 1] = v.y;
+      x[4 * q + 2] = v.z;
+      x[4 * q + 3] = v.w;
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) x[j] = valid(j) ? xr[col(j)] : 0.0f;
+  }
+  float buf[4];
+  auto store = [&](int j, float v) {
+    if (VEC) {
+      buf[j & 3] = v;
+      if ((j & 3) == 3)
+        __builtin_nontemporal_store(floatx4{buf[0], buf[1], buf[2], buf[3]},
+                                    reinterpret_cast<floatx4*>(dr + col(j) - 3));
+    } else {
+      dr[col(j)] = v;
+    }
+  };
+  const bool want_argmax = preds || row_correct;
+  CeRowOut r;
+  if constexpr (LABELS) {
+    r = ce_row_label<VPT>(x, valid, col, label, inv_b, dr != nullptr, store, want_argmax, red);
+  } else {
+    auto tval = [&](int j) -> float { return valid(j) ? tr[col(j)] : 0.0f; };
+    r = ce_row<VPT>(x, valid, tval, col, false, label, inv_b, dr != nullptr, store, want_argmax, red);
+  }
+  if (tid == 0) {
     row_loss[row] = r.loss;
     if (preds) preds[row] = r.pred;
     if (row_correct) row_correct[row] = (r.pred == r.target) ? 1 : 0;
@@ -302,9 +372,19 @@ void softmax_ce(orca_hip_ctx* ctx, const float* logits, size_t B, size_t C, cons
       if (vec) CE_LAUNCH(16, true, false);
       else CE_LAUNCH(16, false, false);
     } else {
-      if (vec && C == 4096) CE_LAUNCH(64, true, true);
-      else if (vec) CE_LAUNCH(64, true, false);
-      else CE_LAUNCH(64, false, false);
+#define CE_BLOCK_LAUNCH(VEC, FULL)                                                                            \
+  do {                                                                                                        \
+    if (labels)                                                                                               \
+      hipLaunchKernelGGL((softmax_ce_block_kernel<VEC, FULL, true>), dim3((unsigned)B), dim3(256), 0,         \
+                         ctx->stream, logits, (int)B, (int)C, onehot, labels, inv_b, row_loss, dlogits, preds, rc); \
+    else                                                                                                      \
+      hipLaunchKernelGGL((softmax_ce_block_kernel<VEC, FULL, false>), dim3((unsigned)B), dim3(256), 0,        \
+                         ctx->stream, logits, (int)B, (int)C, onehot, labels, inv_b, row_loss, dlogits, preds, rc); \
+  } while (0)
+      if (vec && C == 4096) CE_BLOCK_LAUNCH(true, true);
+      else if (vec) CE_BLOCK_LAUNCH(true, false);
+      else CE_BLOCK_LAUNCH(false, false);
+#undef CE_BLOCK_LAUNCH
     }
 #undef CE_LAUNCH
     ORCA_HIP_CHECK(hipGetLastError());

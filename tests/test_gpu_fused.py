@@ -171,6 +171,39 @@ def test_softmax_ce_matches_composed_reference(ctx, B, C):
         assert correct == int((O.argmax_rows(logits) == labels).sum())
 
 
+@pytest.mark.parametrize("B,C", [(5, 2000), (7, 1027), (300, 4096), (4, 1025)])
+def test_softmax_ce_wide_rows_match_composed_reference(ctx, B, C):
+    """Rows of 1025..4096 logits (a block per row): float4 and element-wise
+    column layouts, full and partial rows."""
+    test_softmax_ce_matches_composed_reference(ctx, B, C)
+
+
+@pytest.mark.parametrize("C", [1, 10, 64, 300, 1025, 2048, 4096])
+def test_softmax_ce_labels_equal_onehot_bit_exact(ctx, C):
+    """Class-index targets and their one-hot rows give the same bits (loss,
+    gradient, argmax, count), also for rows with infinite or NaN logits,
+    whose loss term the class-index path forms in full as the reference does."""
+    B = 12
+    rng = np.random.default_rng(C + 5)
+    logits = (3.0 * rng.standard_normal((B, C))).astype(np.float32)
+    logits[1, C // 2] = np.inf
+    logits[2, 0] = np.nan
+    logits[3, :] = -np.inf
+    logits[3, C - 1] = 2.0
+    logits[4, :] = 7.0                      # equal logits
+    logits[5, C // 3] = 300.0               # every other exp underflows: se == 1
+    labels = rng.integers(0, C, B)
+    labels[5] = C // 3                      # the label is the only non-underflowing column
+    labels[6] = C // 3 if C > 1 else 0
+    onehot = synth.one_hot(labels, C)
+    a = run_ce(ctx, logits, labels=labels)
+    b = run_ce(ctx, logits, onehot=onehot)
+    np.testing.assert_array_equal(np.float32(a[0]), np.float32(b[0]))
+    np.testing.assert_array_equal(a[1], b[1])
+    np.testing.assert_array_equal(a[2], b[2])
+    assert a[3] == b[3]
+
+
 def test_softmax_ce_ties_nan_and_equal_logits(ctx):
     B, C = 6, 10
     logits = np.zeros((B, C), np.float32)  # equal logits: loss = ln C, ties everywhere
