@@ -19,6 +19,7 @@ namespace {
 
 constexpr int kMaxRank = 8;
 constexpr unsigned kBlock = 256;
+constexpr int RED_UNROLL = 128;  // loads in flight per thread of a single-axis reduction
 
 // ---------------------------------------------------------------- functors
 struct OpAdd { __device__ float operator()(float a, float b) const { return a + b; } };
@@ -174,17 +175,28 @@ __global__ void reduce_kernel(const float* __restrict__ in, float* __restrict__ 
     base += c * (size_t)a.kept_strides[d];
   }
   float acc = IS_MAX ? -FLT_MAX : 0.0f;
-  if (a.n_red == 1) {
-    const float* p = in + base;
-    size_t st = (size_t)a.red_strides[0];
-    for (int64_t j = 0; j < a.red_count; ++j) {
-      float v = p[(size_t)j * st];
-      if (IS_MAX) {
-        if (v > acc) acc = v;
-      } else {
-        acc = acc + v;
-      }
+  auto step = [&](float v) {
+    if (IS_MAX) {
+      if (v > acc) acc = v;
+    } else {
+      acc = acc + v;
     }
+  };
+  if (a.n_red == 1) {
+    // RED_UNROLL loads in flight, then combined in index order: the same
+    // sequence of operations as one load at a time.
+    const float* p = in + base;
+    const size_t st = (size_t)a.red_strides[0];
+    const int64_t n = a.red_count;
+    int64_t j = 0;
+    for (; j + RED_UNROLL <= n; j += RED_UNROLL) {
+      float v[RED_UNROLL];
+#pragma unroll
+      for (int u = 0; u < RED_UNROLL; ++u) v[u] = p[(size_t)(j + u) * st];
+#pragma unroll
+      for (int u = 0; u < RED_UNROLL; ++u) step(v[u]);
+    }
+    for (; j < n; ++j) step(p[(size_t)j * st]);
   } else {
     int64_t c[kMaxRank] = {0};
     size_t off = base;
