@@ -149,6 +149,48 @@ __global__ void expand_kernel(const float* __restrict__ in, float* __restrict__ 
   }
 }
 
+// The broadcasts the Linear layer, the loss and the optimizer make on every
+// step, as copies without index arithmetic: rows (out[r][c] = in[c], a bias
+// [1, N] expanded to [B, N]), columns (out[r][c] = in[r], [B, 1] to [B, C])
+// and a single value.
+__global__ void expand_rows_kernel(const float* __restrict__ in, float* __restrict__ out, size_t rows, size_t cols,
+                                   bool vec) {
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  const size_t t0 = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  for (size_t r = blockIdx.y; r < rows; r += gridDim.y) {
+    if (vec) {
+      const float4* i4 = reinterpret_cast<const float4*>(in);
+      float4* o4 = reinterpret_cast<float4*>(out + r * cols);
+      for (size_t c = t0; c < cols / 4; c += stride) o4[c] = i4[c];
+    } else {
+      for (size_t c = t0; c < cols; c += stride) out[r * cols + c] = in[c];
+    }
+  }
+}
+
+// A one-element input everywhere (e.g. eps expanded to a parameter's shape).
+__global__ void expand_scalar_kernel(const float* __restrict__ in, float* __restrict__ out, size_t n, bool vec) {
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  const size_t t0 = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const float v = in[0];
+  if (vec) {
+    float4* o4 = reinterpret_cast<float4*>(out);
+    for (size_t i = t0; i < n / 4; i += stride) o4[i] = make_float4(v, v, v, v);
+    for (size_t i = 4 * (n / 4) + t0; i < n; i += stride) out[i] = v;
+  } else {
+    for (size_t i = t0; i < n; i += stride) out[i] = v;
+  }
+}
+
+__global__ void expand_cols_kernel(const float* __restrict__ in, float* __restrict__ out, size_t rows, size_t cols) {
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  const size_t t0 = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  for (size_t r = blockIdx.y; r < rows; r += gridDim.y) {
+    const float v = in[r];
+    for (size_t c = t0; c < cols; c += stride) out[r * cols + c] = v;
+  }
+}
+
 // One thread per output element; the reduced coordinates are walked as an
 // odometer in row-major order, i.e. ascending input index (backend.rs:519-527,
 // 1355-1372).
@@ -532,8 +574,32 @@ int orca_hip_expand(orca_hip_ctx* ctx, const void* s, const size_t* in_shape, si
     float* o = new_output(ctx, n);
     if (n) {
       ProfScope ps(ctx, "expand", 0.0, 8.0 * n);
-      unsigned g = grid_for(n, kBlock, ctx->num_cus * 16);
-      hipLaunchKernelGGL(expand_kernel, dim3(g), dim3(kBlock), 0, ctx->stream, as_f(s), o, n, a);
+      // The output as [rows, cols] with cols its last dim: a row broadcast
+      // takes the input only along the last dim, a column broadcast only
+      // along the others (the input's last dim is 1).
+      const size_t cols = out_rank ? out_shape[out_rank - 1] : 1, rows = cols ? n / cols : 0;
+      bool row_bc = out_rank >= 1 && pin[out_rank - 1] == (int64_t)cols, col_bc = out_rank >= 2 && pin[out_rank - 1] == 1;
+      for (size_t d = 0; d + 1 < out_rank; ++d) {
+        if (pin[d] != 1) row_bc = false;
+        if (pin[d] != (int64_t)out_shape[d]) col_bc = false;
+      }
+      const unsigned gy = (unsigned)std::min<size_t>(rows, 65535);
+      if (numel(in_shape, in_rank) == 1 && n > 1) {
+        const bool vec = aligned16(o);
+        unsigned g = grid_for(vec ? (n + 3) / 4 : n, kBlock, ctx->num_cus * 16);
+        hipLaunchKernelGGL(expand_scalar_kernel, dim3(g), dim3(kBlock), 0, ctx->stream, as_f(s), o, n, vec);
+      } else if (row_bc && rows > 1) {
+        const bool vec = cols % 4 == 0 && aligned16(s) && aligned16(o);
+        const size_t per_row = vec ? cols / 4 : cols;
+        const unsigned gx = (unsigned)std::min<size_t>((per_row + kBlock - 1) / kBlock, 64);
+        hipLaunchKernelGGL(expand_rows_kernel, dim3(gx, gy), dim3(kBlock), 0, ctx->stream, as_f(s), o, rows, cols, vec);
+      } else if (col_bc && cols > 1) {
+        const unsigned gx = (unsigned)std::min<size_t>((cols + kBlock - 1) / kBlock, 64);
+        hipLaunchKernelGGL(expand_cols_kernel, dim3(gx, gy), dim3(kBlock), 0, ctx->stream, as_f(s), o, rows, cols);
+      } else {
+        unsigned g = grid_for(n, kBlock, ctx->num_cus * 16);
+        hipLaunchKernelGGL(expand_kernel, dim3(g), dim3(kBlock), 0, ctx->stream, as_f(s), o, n, a);
+      }
       ORCA_HIP_CHECK(hipGetLastError());
     }
     *out = o;

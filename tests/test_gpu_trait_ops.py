@@ -80,7 +80,9 @@ def test_unary_and_scalar_ops(hb, shape):
 
 
 @pytest.mark.parametrize("in_shape,out_shape", [((1, 7), (5, 7)), ((5, 1), (5, 9)), ((1,), (3, 4)),
-                                                ((2, 1, 3), (4, 2, 5, 3)), ((1, 4096), (1024, 4096))])
+                                                ((2, 1, 3), (4, 2, 5, 3)), ((1, 4096), (1024, 4096)),
+                                                ((2, 3, 1), (2, 3, 5)), ((1, 1, 8), (3, 2, 8)), ((7,), (7,)),
+                                                ((1024, 1), (1024, 10)), ((1,), (33, 65)), ((1, 1), (4096, 16))])
 def test_expand_and_sum_to_shape_bit_exact(hb, in_shape, out_shape):
     rng = np.random.default_rng(sum(out_shape))
     a = rng.standard_normal(in_shape).astype(np.float32)
