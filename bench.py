@@ -110,10 +110,11 @@ def _kernel_times(ctx, fn, reps: int) -> dict:
 def secondary(ctx) -> dict:
     """The other workloads of the path, on the same GPU: step time of the two
     small MLP configurations (784-128-128-10 B=64 SGD; 784-1024-1024-10 B=256
-    AdamW), the fused backward epilogue on [8192, 4096] (softmax-CE gradient
-    with int targets; ReLU-mask backward + bias column sum), and AdamW over one
-    flat buffer of 2^28 parameters.  Bandwidths are algorithmic bytes / mean
-    kernel time."""
+    AdamW), the 784-4096-4096-10 step through the drop-in path (reference
+    frontend and tape over the trait ops), the fused backward epilogue on
+    [8192, 4096] (softmax-CE gradient with int targets; ReLU-mask backward +
+    bias column sum), and AdamW over one flat buffer of 2^28 parameters.
+    Bandwidths are algorithmic bytes / mean kernel time."""
     import ctypes
 
     from orcaml_amd import _lib, synth
@@ -139,6 +140,38 @@ def secondary(ctx) -> dict:
         dt = (time.perf_counter() - t0) / n
         out[w["name"]] = {"ms_per_step": dt * 1e3, "steps_per_s": 1.0 / dt, "samples_per_s": w["batch"] / dt}
         tr.close()
+
+    # The drop-in path: the reference frontend (nn.Sequential of Linear/ReLU,
+    # CrossEntropyLoss, AdamW) and the autodiff tape running on the backend's
+    # trait ops, unchanged and with the opt-in fused loss and optimizer.
+    from orcaml_amd import autodiff as A
+    from orcaml_amd.backend import HipBackend
+
+    w = synth.WORKLOADS[synth.MLP_LARGE]
+    params, x, labels, onehot = synth.mlp_problem(w["seed"], w["dims"], w["batch"])
+    composed = {}
+    for tag, fused in (("unchanged", False), ("fused_loss_and_adamw", True)):
+        ad = A.Autodiff(HipBackend(ctx))
+        model = A.build_mlp(ad, params)
+        opt = A.AdamW(model.parameters(), lr=OPT["lr"], weight_decay=OPT["weight_decay"], fused=fused)
+        xt, tt = A.Tensor.from_numpy(ad, x), A.Tensor.from_numpy(ad, onehot)
+
+        def step():
+            opt.zero_grad()
+            A.CrossEntropyLoss(fused=fused)(model(xt), tt).backward()
+            opt.step()
+
+        for _ in range(3):
+            step()
+        ctx.sync()
+        n = 10
+        t0 = time.perf_counter()
+        for _ in range(n):
+            step()
+        ctx.sync()
+        dt = (time.perf_counter() - t0) / n
+        composed[tag] = {"ms_per_step": dt * 1e3, "steps_per_s": 1.0 / dt}
+    out["composed_" + w["name"]] = composed
 
     # Fused backward epilogue, [8192, 4096].
     B, C = 8192, 4096
