@@ -7,7 +7,8 @@
 // value replaces the running max, max_to_shape_backward hands the full
 // gradient to every element equal to the max, and sum_to_shape / max_to_shape
 // visit inputs in ascending row-major order -- here one thread owns one output
-// element, so those reductions are bit-identical to the reference's loops.
+// element (for column reductions, one lane combining LDS-staged rows), so those
+// reductions are bit-identical to the reference's loops.
 // Built with -ffp-contract=off: no multiply-add is fused.
 #include <cfloat>
 #include <cmath>
@@ -40,6 +41,10 @@ struct OpScale {
   float s;
   __device__ float operator()(float x) const { return x * s; }
 };
+// One visit per output of sum_to_shape / max_to_shape (nothing reduced): the first step of
+// the reduction from its start value, so -0 becomes +0 and NaN / -inf become -FLT_MAX.
+struct OpSumVisit { __device__ float operator()(float x) const { return 0.0f + x; } };
+struct OpMaxVisit { __device__ float operator()(float x) const { return x > -FLT_MAX ? x : -FLT_MAX; } };
 struct OpDivBwRhs {  // g * (-l / (r * r))
   __device__ float operator()(float g, float l, float r) const { return g * (-l / (r * r)); }
 };
@@ -260,6 +265,94 @@ __global__ void reduce_kernel(const float* __restrict__ in, float* __restrict__ 
   out[o] = acc;
 }
 
+// Column reduction of a row-strided matrix (contiguous kept axis, one reduced axis of stride
+// `st`), e.g. a bias gradient [rows, cols] -> [1, cols]. One thread per column leaves a
+// 4096-column matrix with 64 waves; here every thread of a 256-thread block stages a
+// CR_COLS-column slab through LDS (one 128-byte line per row, transposed so that each column's
+// rows are contiguous, double-buffered, two slabs' loads in flight), and lane c of wave 0
+// combines column c's values in row order: the same sequence of operations as reduce_kernel,
+// so the result is bit-identical.
+constexpr int CR_THREADS = 256;
+constexpr int CR_COLS = 32;
+constexpr int CR_ROWS = 128;
+constexpr int CR_LD = CR_ROWS + 4;  // LDS floats per staged column (16-byte aligned, offset banks)
+
+template <bool IS_MAX>
+__global__ void __launch_bounds__(CR_THREADS)
+    colreduce_kernel(const float* __restrict__ in, float* __restrict__ out, size_t cols, int64_t rows, size_t st) {
+  constexpr int GROUPS = CR_THREADS / CR_COLS;     // row quads loaded side by side
+  constexpr int QUADS = CR_ROWS / (4 * GROUPS);    // row quads per thread per slab
+  __shared__ __align__(16) float buf[2][CR_COLS * CR_LD];
+  const int t = threadIdx.x;
+  const int lc = t % CR_COLS, rg = t / CR_COLS;
+  const size_t c = (size_t)blockIdx.x * CR_COLS + lc;
+  const bool col_ok = c < cols;
+  const int64_t n_slabs = (rows + CR_ROWS - 1) / CR_ROWS;
+  // Rows past the end and columns past the edge load a clamped (in-bounds) element instead
+  // of branching around the load: their values are never combined or stored.
+  const float* src = in + (col_ok ? c : cols - 1);
+  auto load = [&](int64_t k, float4 (&v)[QUADS]) {
+#pragma unroll
+    for (int q = 0; q < QUADS; ++q) {
+      const int64_t r = k * CR_ROWS + 4 * (rg + GROUPS * q);
+      v[q].x = src[(size_t)min(r, rows - 1) * st];
+      v[q].y = src[(size_t)min(r + 1, rows - 1) * st];
+      v[q].z = src[(size_t)min(r + 2, rows - 1) * st];
+      v[q].w = src[(size_t)min(r + 3, rows - 1) * st];
+    }
+  };
+  auto stash = [&](int b, const float4 (&v)[QUADS]) {
+    float4* dst = reinterpret_cast<float4*>(buf[b] + lc * CR_LD);
+#pragma unroll
+    for (int q = 0; q < QUADS; ++q) dst[rg + GROUPS * q] = v[q];
+  };
+  float acc = IS_MAX ? -FLT_MAX : 0.0f;
+  auto step = [&](float x) {
+    if (IS_MAX) {
+      if (x > acc) acc = x;
+    } else {
+      acc = acc + x;
+    }
+  };
+  auto combine = [&](int64_t k) {
+    const int n = (int)min((int64_t)CR_ROWS, rows - k * CR_ROWS);
+    const float* col = buf[k & 1] + t * CR_LD;
+    const float4* col4 = reinterpret_cast<const float4*>(col);
+    int q = 0;
+    for (; q + 8 <= n / 4; q += 8) {
+      float4 x[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) x[u] = col4[q + u];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        step(x[u].x);
+        step(x[u].y);
+        step(x[u].z);
+        step(x[u].w);
+      }
+    }
+    for (int r = 4 * q; r < n; ++r) step(col[r]);
+  };
+  // Slab k sits in LDS buffer k & 1; `cur` held slab k (already staged) and receives slab
+  // k + 2, `nxt` holds slab k + 1 (in flight), staged after slab k is combined.
+  auto iter = [&](int64_t k, float4 (&cur)[QUADS], const float4 (&nxt)[QUADS]) {
+    if (k + 2 < n_slabs) load(k + 2, cur);
+    if (t < CR_COLS) combine(k);
+    if (k + 1 < n_slabs) stash((int)((k + 1) & 1), nxt);
+    __syncthreads();
+  };
+  float4 va[QUADS], vb[QUADS];
+  load(0, va);
+  if (n_slabs > 1) load(1, vb);
+  stash(0, va);
+  __syncthreads();
+  for (int64_t k = 0; k < n_slabs; k += 2) {
+    iter(k, va, vb);
+    if (k + 1 < n_slabs) iter(k + 1, vb, va);
+  }
+  if (t < CR_COLS && col_ok) out[c] = acc;
+}
+
 // max_to_shape_backward: thread per input element (backend.rs:1407-1424).
 __global__ void max_bw_kernel(const float* __restrict__ g, const float* __restrict__ x, const float* __restrict__ y,
                               float* __restrict__ out, size_t n, Dims in_dims, ExpandArgs map) {
@@ -380,6 +473,25 @@ ReduceArgs make_reduce(const size_t* in_shape, size_t in_rank, const size_t* out
     a.red_dims[0] = 1;
     a.red_strides[0] = 0;
   }
+  // Adjacent dims that tile memory contiguously become one dim: the odometer then visits the
+  // same elements in the same order, with fewer index steps (and [B, S, N] -> [N] reaches the
+  // one-axis paths).
+  auto merge = [](int& n, int64_t* dims, int64_t* strides) {
+    int m = 0;
+    for (int d = 1; d < n; ++d) {
+      if (strides[m] == strides[d] * dims[d]) {
+        dims[m] *= dims[d];
+        strides[m] = strides[d];
+      } else {
+        ++m;
+        dims[m] = dims[d];
+        strides[m] = strides[d];
+      }
+    }
+    if (n > 0) n = m + 1;
+  };
+  merge(a.n_kept, a.kept_dims, a.kept_strides);
+  merge(a.n_red, a.red_dims, a.red_strides);
   return a;
 }
 
@@ -625,10 +737,27 @@ static int reduce_entry(orca_hip_ctx* ctx, bool is_max, const void* s, const siz
       } else {
         // Out-of-range output slots (rank padding quirk) stay zero like the reference.
         if ((size_t)a.red_count * n_out != n_in) launch_fill(ctx, o, 0.0f, n_out);
+        if (a.red_count == 1 && n_out == n_in && a.n_kept == 1 && a.kept_strides[0] == 1) {
+          if (is_max)
+            run_ew1(ctx, op, as_f(s), o, n_in, OpMaxVisit{});
+          else
+            run_ew1(ctx, op, as_f(s), o, n_in, OpSumVisit{});
+          *out = o;
+          return;
+        }
         size_t n_threads = n_in / (size_t)a.red_count;
         ProfScope ps(ctx, op, 0.0, 4.0 * (n_in + n_out));
         unsigned g = (unsigned)((n_threads + 63) / 64);
-        if (is_max)
+        if (a.n_red == 1 && a.n_kept == 1 && a.kept_strides[0] == 1 && a.red_count >= CR_ROWS) {
+          const unsigned gc = (unsigned)((n_threads + CR_COLS - 1) / CR_COLS);
+          const size_t st = (size_t)a.red_strides[0];
+          if (is_max)
+            hipLaunchKernelGGL(colreduce_kernel<true>, dim3(gc), dim3(CR_THREADS), 0, ctx->stream, as_f(s), o,
+                               n_threads, a.red_count, st);
+          else
+            hipLaunchKernelGGL(colreduce_kernel<false>, dim3(gc), dim3(CR_THREADS), 0, ctx->stream, as_f(s), o,
+                               n_threads, a.red_count, st);
+        } else if (is_max)
           hipLaunchKernelGGL(reduce_kernel<true>, dim3(g), dim3(64), 0, ctx->stream, as_f(s), o, n_threads, a);
         else
           hipLaunchKernelGGL(reduce_kernel<false>, dim3(g), dim3(64), 0, ctx->stream, as_f(s), o, n_threads, a);

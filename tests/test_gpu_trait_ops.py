@@ -82,7 +82,10 @@ def test_unary_and_scalar_ops(hb, shape):
 @pytest.mark.parametrize("in_shape,out_shape", [((1, 7), (5, 7)), ((5, 1), (5, 9)), ((1,), (3, 4)),
                                                 ((2, 1, 3), (4, 2, 5, 3)), ((1, 4096), (1024, 4096)),
                                                 ((2, 3, 1), (2, 3, 5)), ((1, 1, 8), (3, 2, 8)), ((7,), (7,)),
-                                                ((1024, 1), (1024, 10)), ((1,), (33, 65)), ((1, 1), (4096, 16))])
+                                                ((1024, 1), (1024, 10)), ((1,), (33, 65)), ((1, 1), (4096, 16)),
+                                                ((1, 100), (1000, 100)), ((70,), (3, 300, 70)),
+                                                ((1, 1, 33), (2, 129, 33)), ((1, 10), (1024, 10)),
+                                                ((1, 4100), (300, 4100)), ((1, 64), (127, 64)), ((1, 5), (128, 5))])
 def test_expand_and_sum_to_shape_bit_exact(hb, in_shape, out_shape):
     rng = np.random.default_rng(sum(out_shape))
     a = rng.standard_normal(in_shape).astype(np.float32)
@@ -114,6 +117,16 @@ def test_max_to_shape_and_backward_bit_exact(hb, shape):
     np.testing.assert_array_equal(
         down(hb, hb.max_to_shape_backward(up(hb, g), up(hb, x), up(hb, y), shape, out_shape), shape),
         O.max_to_shape_backward(g, x, y))
+
+
+@pytest.mark.parametrize("shape,out_shape", [((1000, 70), (1, 70)), ((3, 300, 33), (33,)), ((129, 4096), (1, 4096))])
+def test_column_max_to_shape_bit_exact(hb, shape, out_shape):
+    rng = np.random.default_rng(shape[-1])
+    x = rng.integers(-3, 3, shape).astype(np.float32)  # many ties
+    x.reshape(-1)[::13] = np.nan
+    x.reshape(-1)[5::17] = -np.inf
+    np.testing.assert_array_equal(down(hb, hb.max_to_shape(up(hb, x), shape, out_shape), out_shape),
+                                  O.max_to_shape(x, out_shape))
 
 
 @pytest.mark.parametrize("shape,d0,d1", [((5, 7), 0, 1), ((3, 130, 70), 1, 2), ((2, 3, 4, 5), 0, 2),
