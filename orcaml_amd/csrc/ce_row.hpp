@@ -13,6 +13,16 @@
 
 namespace orca_hip {
 
+// exp(d) of the softmax terms as 2^(d * log2 e) on the hardware exp2
+// (v_exp_f32, 1 ulp): three instructions instead of libm expf's range
+// reduction in extended precision, which dominated the instruction count of
+// the wide-row kernels.  The rounded product shifts the exponent by at most
+// |d * log2 e| * 2^-24, so the relative error is below 1.2e-6 for d > -20
+// (every term above 2e-9 of the row's largest) and below 6e-6 down to the
+// underflow of the result; exp(0) = 1 and exp(-inf) = 0 exactly, NaN stays
+// NaN.
+__device__ __forceinline__ float ce_exp(float d) { return __builtin_amdgcn_exp2f(d * 1.44269504088896341f); }
+
 // ---- wave64 reductions on the DPP network (no LDS round trips) ----
 // Steps: quad_perm [1,0,3,2] and [2,3,0,1], row_half_mirror and row_mirror
 // leave every lane of a 16-lane row holding the row's result; row_bcast:15
@@ -197,7 +207,7 @@ __device__ __forceinline__ CeRowOut ce_row(const float (&x)[VPL], Valid valid, T
   float se = 0.0f;
 #pragma unroll
   for (int j = 0; j < VPL; ++j) {
-    e[j] = valid(j) ? expf(x[j] - mx) : 0.0f;
+    e[j] = valid(j) ? ce_exp(x[j] - mx) : 0.0f;
     se = se + e[j];
   }
   se = red.sum(se);
@@ -263,50 +273,63 @@ __device__ __forceinline__ CeRowOut ce_row(const float (&x)[VPL], Valid valid, T
 // which leaves a sum unchanged, so those sums are formed from the label's term
 // alone (on its lane; +0 elsewhere) with the same bits as the full sums.  A
 // label outside [0, C) leaves every target zero, as its one-hot row would.
-template <int VPL, class Col, class Valid, class Store, class R = WaveRed>
-__device__ __forceinline__ CeRowOut ce_row_label(const float (&x)[VPL], Valid valid, Col col, int label, float inv_b,
-                                                 bool grad, Store store, bool want_argmax, const R& red = R()) {
-  int jl = -1;  // this lane's slot holding the label column
+//
+// x is overwritten with exp(x - max): a thread holds one array of row values
+// instead of two, so more rows are resident per CU (more loads in flight).
+// What later steps need of x is kept on the side: the label's logit, a bit
+// mask of the columns equal to the max, and for the check below the lane's
+// smallest value and whether it holds a non-finite one.  reload(j) reads
+// x[j] again from memory for rows whose loss terms are irregular.  jl is this
+// lane's slot of the label column (col(jl) == label, valid), or -1.
+template <int VPL, class Col, class Valid, class Store, class Reload, class R = WaveRed>
+__device__ __forceinline__ CeRowOut ce_row_label(float (&x)[VPL], Valid valid, Col col, Reload reload, int label,
+                                                 int jl, float inv_b, bool grad, Store store, bool want_argmax,
+                                                 const R& red = R()) {
+  static_assert(VPL <= 32, "the max mask holds one bit per value");
+  float mx = -FLT_MAX, xmin = FLT_MAX, xl = 0.0f;
+  bool nonfinite = false;
 #pragma unroll
   for (int j = 0; j < VPL; ++j)
-    if (valid(j) && col(j) == label) jl = j;
-  float e[VPL];
-  float mx = -FLT_MAX;
-#pragma unroll
-  for (int j = 0; j < VPL; ++j)
-    if (valid(j) && x[j] > mx) mx = x[j];
+    if (valid(j)) {
+      if (x[j] > mx) mx = x[j];
+      xmin = fminf(xmin, x[j]);
+      nonfinite = nonfinite || !(fabsf(x[j]) <= FLT_MAX);
+      if (j == jl) xl = x[j];
+    }
+  CeRowOut out{0.0f, 0, label};
+  if (want_argmax) out.pred = row_argmax<VPL>([&](int j) { return x[j]; }, col, valid, red);
   mx = red.max(mx);
   float se = 0.0f;
+  unsigned at_max = 0;
 #pragma unroll
   for (int j = 0; j < VPL; ++j) {
-    e[j] = valid(j) ? expf(x[j] - mx) : 0.0f;
-    se = se + e[j];
+    const float e = valid(j) ? ce_exp(x[j] - mx) : 0.0f;
+    if (valid(j) && x[j] == mx) at_max |= 1u << j;
+    x[j] = e;
+    se = se + e;
   }
   se = red.sum(se);
   const float lg = logf(fmaxf(se, 1e-7f));
   const float lse = mx + lg;
   // A zero target's loss term (0 * (x - lse)) * -1 is +-0 only while x - lse
   // is finite; with an infinite or NaN difference it is NaN, and the full sum
-  // is formed as the reference forms it.
-  float pl = 0.0f;
-  bool irregular = false;
-#pragma unroll
-  for (int j = 0; j < VPL; ++j)
-    if (valid(j)) {
-      const float dj = x[j] - lse;
-      if (j == jl) pl = (1.0f * dj) * -1.0f;
-      irregular = irregular || !(fabsf(dj) <= FLT_MAX);
-    }
+  // is formed as the reference forms it.  The max element's term exp(0) = 1
+  // makes se >= 1, so lse >= max >= x and x - lse <= 0 for every finite x:
+  // all differences are finite exactly when the lane's values are finite and
+  // the smallest difference is (x - lse is monotone in x).
+  const float pl = jl >= 0 ? (1.0f * (xl - lse)) * -1.0f : 0.0f;
+  const bool irregular = valid(0) && (nonfinite || !(fabsf(xmin - lse) <= FLT_MAX));
   float pb;
   if (red.any(irregular)) {
     float s = 0.0f;
-#pragma unroll
-    for (int j = 0; j < VPL; ++j)
-      if (valid(j)) s = s + ((j == jl ? 1.0f : 0.0f) * (x[j] - lse)) * -1.0f;
+#pragma unroll 1
+    for (int j = 0; j < VPL; ++j)  // one reload at a time: the rare path adds no register pressure
+      if (valid(j)) s = s + ((j == jl ? 1.0f : 0.0f) * (reload(j) - lse)) * -1.0f;
     pb = red.sum(s);
   } else {
     pb = red.sum(pl);
   }
+  out.loss = pb;
 
   if (grad) {
     const float g_tm = inv_b * -1.0f;
@@ -333,7 +356,7 @@ __device__ __forceinline__ CeRowOut ce_row_label(const float (&x)[VPL], Valid va
 #pragma unroll
     for (int j = 0; j < VPL; ++j)
       if (valid(j)) {
-        const float t = 0.0f - gse * e[j];
+        const float t = 0.0f - gse * x[j];
         gmx = gmx + (j == jl ? g_lse_c + t : t);
       }
     gmx = red.sum(gmx);
@@ -342,15 +365,12 @@ __device__ __forceinline__ CeRowOut ce_row_label(const float (&x)[VPL], Valid va
 #pragma unroll
     for (int j = 0; j < VPL; ++j) {
       if (valid(j)) {
-        const float g_sh = gse * e[j];
+        const float g_sh = gse * x[j];
         const float d = j == jl ? g_ls_c + g_sh : g_sh;
-        store(j, x[j] == mx ? d + g3 : d);
+        store(j, (at_max >> j) & 1u ? d + g3 : d);
       }
     }
   }
-
-  CeRowOut out{pb, 0, label};
-  if (want_argmax) out.pred = row_argmax<VPL>([&](int j) { return x[j]; }, col, valid, red);
   return out;
 }
 

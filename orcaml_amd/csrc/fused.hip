@@ -70,10 +70,18 @@ __global__ void __launch_bounds__(256) softmax_ce_kernel(const float* __restrict
     }
   };
   CeRowOut r;
-  if constexpr (LABELS)
-    r = ce_row_label<VPL>(x, valid, col, label, inv_b, dr != nullptr, store, preds || row_correct);
-  else
+  if constexpr (LABELS) {
+    // The label's slot: col(j) = label for j = jl on one lane.
+    int jl = -1;
+    if (label >= 0 && label < C) {
+      if (VEC && (((label & 255) >> 2) == lane)) jl = 4 * (label >> 8) + (label & 3);
+      if (!VEC && (label & 63) == lane) jl = label >> 6;
+    }
+    r = ce_row_label<VPL>(x, valid, col, [&](int j) { return xr[col(j)]; }, label, jl, inv_b, dr != nullptr, store,
+                          preds || row_correct);
+  } else {
     r = ce_row<VPL>(x, valid, tval, col, false, label, inv_b, dr != nullptr, store, preds || row_correct);
+  }
   if (lane == 0) {
     row_loss[row] = r.loss;
     if (preds) preds[row] = r.pred;
@@ -136,7 +144,14 @@ __global__ void __launch_bounds__(256) softmax_ce_block_kernel(const float* __re
   const bool want_argmax = preds || row_correct;
   CeRowOut r;
   if constexpr (LABELS) {
-    r = ce_row_label<VPT>(x, valid, col, label, inv_b, dr != nullptr, store, want_argmax, red);
+    // The label's slot: col(j) = label for j = jl on one thread.
+    int jl = -1;
+    if (label >= 0 && label < C) {
+      if (VEC && (((label & 1023) >> 2) == tid)) jl = 4 * (label >> 10) + (label & 3);
+      if (!VEC && (label & 255) == tid) jl = label >> 8;
+    }
+    r = ce_row_label<VPT>(x, valid, col, [&](int j) { return xr[col(j)]; }, label, jl, inv_b, dr != nullptr, store,
+                          want_argmax, red);
   } else {
     auto tval = [&](int j) -> float { return valid(j) ? tr[col(j)] : 0.0f; };
     r = ce_row<VPT>(x, valid, tval, col, false, label, inv_b, dr != nullptr, store, want_argmax, red);
@@ -375,11 +390,11 @@ void softmax_ce(orca_hip_ctx* ctx, const float* logits, size_t B, size_t C, cons
 #define CE_BLOCK_LAUNCH(VEC, FULL)                                                                            \
   do {                                                                                                        \
     if (labels)                                                                                               \
-      hipLaunchKernelGGL((softmax_ce_block_kernel<VEC, FULL, true>), dim3((unsigned)B), dim3(256), 0,         \
-                         ctx->stream, logits, (int)B, (int)C, onehot, labels, inv_b, row_loss, dlogits, preds, rc); \
+      hipLaunchKernelGGL((softmax_ce_block_kernel<VEC, FULL, true>), dim3((unsigned)B), dim3(256), 0, ctx->stream, \
+                         logits, (int)B, (int)C, onehot, labels, inv_b, row_loss, dlogits, preds, rc);           \
     else                                                                                                      \
-      hipLaunchKernelGGL((softmax_ce_block_kernel<VEC, FULL, false>), dim3((unsigned)B), dim3(256), 0,        \
-                         ctx->stream, logits, (int)B, (int)C, onehot, labels, inv_b, row_loss, dlogits, preds, rc); \
+      hipLaunchKernelGGL((softmax_ce_block_kernel<VEC, FULL, false>), dim3((unsigned)B), dim3(256), 0, ctx->stream, \
+                         logits, (int)B, (int)C, onehot, labels, inv_b, row_loss, dlogits, preds, rc);           \
   } while (0)
       if (vec && C == 4096) CE_BLOCK_LAUNCH(true, true);
       else if (vec) CE_BLOCK_LAUNCH(true, false);
