@@ -256,21 +256,39 @@ __global__ void __launch_bounds__(256) relu_bw_colsum_scalar_kernel(const float*
   if (partial) partial[(size_t)blockIdx.y * cols + c] = s;
 }
 
-// colsum[c] = sum over chunks (in chunk order) of partial[chunk][c]; the
-// loads of RB_UNROLL chunks are issued before their adds.
-__global__ void chunk_reduce_kernel(const float* __restrict__ partial, int chunks, size_t cols, float* __restrict__ out) {
-  size_t c = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (c >= cols) return;
+// colsum[c] from the per-chunk partials: a 256-thread block takes
+// CR_PARTS_COLS columns, and the CR_PARTS threads of a column each add one
+// contiguous quarter of the chunks in chunk order (RB_UNROLL loads issued
+// before their adds); the quarters are then added in order,
+// ((q0 + q1) + q2) + q3 -- a fixed order, so the result is deterministic.
+constexpr int CR_PARTS = 4;
+constexpr int CR_PARTS_COLS = 256 / CR_PARTS;
+__global__ void __launch_bounds__(256) chunk_reduce_kernel(const float* __restrict__ partial, int chunks, size_t cols,
+                                                           float* __restrict__ out) {
+  __shared__ float q[CR_PARTS][CR_PARTS_COLS];
+  const int lc = threadIdx.x % CR_PARTS_COLS, part = threadIdx.x / CR_PARTS_COLS;
+  const size_t c = (size_t)blockIdx.x * CR_PARTS_COLS + lc;
+  const int per = (chunks + CR_PARTS - 1) / CR_PARTS;
+  const int k_begin = part * per, k_end = min(chunks, k_begin + per);
   float s = 0.0f;
-  for (int k0 = 0; k0 < chunks; k0 += RB_UNROLL) {
-    float v[RB_UNROLL];
+  if (c < cols) {
+    for (int k0 = k_begin; k0 < k_end; k0 += RB_UNROLL) {
+      float v[RB_UNROLL];
 #pragma unroll
-    for (int u = 0; u < RB_UNROLL; ++u) v[u] = k0 + u < chunks ? partial[(size_t)(k0 + u) * cols + c] : 0.0f;
+      for (int u = 0; u < RB_UNROLL; ++u) v[u] = k0 + u < k_end ? partial[(size_t)(k0 + u) * cols + c] : 0.0f;
 #pragma unroll
-    for (int u = 0; u < RB_UNROLL; ++u)
-      if (k0 + u < chunks) s = s + v[u];
+      for (int u = 0; u < RB_UNROLL; ++u)
+        if (k0 + u < k_end) s = s + v[u];
+    }
   }
-  out[c] = s;
+  q[part][lc] = s;
+  __syncthreads();
+  if (part == 0 && c < cols) {
+    float t = q[0][lc];
+#pragma unroll
+    for (int p = 1; p < CR_PARTS; ++p) t = t + q[p][lc];
+    out[c] = t;
+  }
 }
 
 __device__ __forceinline__ void adamw_elem(float& p, float g, float& m, float& v, const AdamWScalars& k) {
@@ -547,8 +565,8 @@ int orca_hip_relu_bw_colsum(orca_hip_ctx* ctx, const float* grad, const float* p
     }
     if (colsum) {
       ProfScope ps(ctx, "colsum_chunks", 0.0, 4.0 * (double)chunks * cols + 4.0 * cols);
-      hipLaunchKernelGGL(chunk_reduce_kernel, dim3((unsigned)((cols + 255) / 256)), dim3(256), 0, ctx->stream, part,
-                         (int)chunks, cols, colsum);
+      hipLaunchKernelGGL(chunk_reduce_kernel, dim3((unsigned)((cols + CR_PARTS_COLS - 1) / CR_PARTS_COLS)), dim3(256),
+                         0, ctx->stream, part, (int)chunks, cols, colsum);
       ORCA_HIP_CHECK(hipGetLastError());
     }
   });
