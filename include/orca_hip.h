@@ -111,6 +111,15 @@ int orca_hip_to_bytes(orca_hip_ctx* ctx, const void* storage, size_t n_bytes, ui
 int orca_hip_matmul(orca_hip_ctx* ctx, const void* lhs, const void* rhs, const size_t* lhs_shape,
                     size_t lhs_rank, const size_t* rhs_shape, size_t rhs_rank, int dtype, int lhs_view,
                     int rhs_view, void** out);
+/* Backend::matmul of rank-2 operands (backend.rs:38-45) together with
+ * Backend::sum_to_shape(rhs, [K, N] -> [1, N]) (backend.rs:499-530): C = op(lhs) x rhs
+ * ([M, K] x [K, N]; lhs_view as above, rhs contiguous) and colsum[n] = sum_k rhs[k][n] in
+ * ascending k, the bits sum_to_shape produces.  One call serves MatMulBackward's
+ * grad_W = X^T x G and ExpandBackward's bias gradient of the same G
+ * (orca-autograd/src/backend.rs:1467-1495, 1684-1697): the column sum rides on
+ * the product's loads of G. */
+int orca_hip_matmul_colsum(orca_hip_ctx* ctx, const void* lhs, const void* rhs, size_t M, size_t K, size_t N,
+                           int lhs_view, int dtype, void* colsum, void** out);
 /* Backend::transpose (backend.rs:48-55), materialised */
 int orca_hip_transpose(orca_hip_ctx* ctx, const void* s, const size_t* shape, size_t rank, size_t dim0,
                        size_t dim1, int dtype, void** out);

@@ -11,10 +11,24 @@ consumes with the transpose folded into its loads (the MatMulBackward
 pattern, orca-autograd/src/backend.rs:1467-1495).  Any other consumer of a
 view materialises it first.  Errors surface as `_lib.OrcaHipError`
 (a ValueError, as orca-python maps OrcaError).
+
+Two more internal shortcuts, invisible to the tape, serve Linear's backward
+(ExpandBackward then MatMulBackward on the same upstream gradient G,
+orca-autograd/src/backend.rs:1684-1697, 1448-1499):
+
+* an identity `sum_to_shape` ([B, N] -> [B, N], one `0 + g` pass) computed
+  once per source storage: the expand-both broadcast of `x @ W + b` asks for
+  it twice on the same G, and storages are immutable, so the second call
+  returns the first result;
+* a column sum `sum_to_shape(G, [B, N] -> [1, N])` is returned pending; the
+  next `matmul(X^T, G)` on that storage computes it inside the product
+  (orca_hip_matmul_colsum, the same bits as the sum_to_shape kernel), and any
+  other use computes it with the sum_to_shape kernel first.
 """
 from __future__ import annotations
 
 import ctypes
+import weakref
 
 import numpy as np
 
@@ -23,17 +37,34 @@ from .device import Buffer, Context
 
 
 class HipStorage:
-    __slots__ = ("buf", "n", "transposed_shape")
+    __slots__ = ("_buf", "n", "transposed_shape", "_fill", "colsum_waiters", "ident", "__weakref__")
 
-    def __init__(self, buf: Buffer, n: int, transposed_shape=None):
-        self.buf = buf
+    def __init__(self, buf: Buffer | None, n: int, transposed_shape=None):
+        self._buf = buf
         self.n = n
         # Logical shape of a lazy last-two-dims transpose (buffer holds the
         # untransposed data), or None for contiguous storage.
         self.transposed_shape = transposed_shape
+        # Pending values: fill(self) sets _buf; run at the first use.
+        self._fill = None
+        # Weak references to pending column sums of this storage.
+        self.colsum_waiters = None
+        # This storage's identity sum_to_shape result, once computed.
+        self.ident = None
 
     def __len__(self) -> int:
         return self.n
+
+    @property
+    def pending(self) -> bool:
+        return self._fill is not None
+
+    @property
+    def buf(self) -> Buffer:
+        if self._fill is not None:
+            fill, self._fill = self._fill, None
+            fill(self)
+        return self._buf
 
     @property
     def ptr(self) -> int:
@@ -47,8 +78,11 @@ def _dims(shape):
 class HipBackend:
     """Drop-in for `GpuBackend` (orca-backend-gpu/src/backend.rs:45-50)."""
 
-    def __init__(self, ctx: Context | None = None):
+    def __init__(self, ctx: Context | None = None, deferred: bool = True):
         self.ctx = ctx if ctx is not None else Context(0)
+        # The identity-reduction memo and the deferred column sum (module
+        # docstring); off, every sum_to_shape runs its kernel at once.
+        self.deferred = deferred
 
     def __repr__(self) -> str:
         return f"HipBackend(device=gpu:{self.ctx.device})"
@@ -129,6 +163,18 @@ class HipBackend:
         return out.tobytes()
 
     def matmul(self, lhs: HipStorage, rhs: HipStorage, lhs_shape, rhs_shape, dtype=_lib.F32):
+        if (rhs.colsum_waiters and dtype == _lib.F32 and len(lhs_shape) == 2 and len(rhs_shape) == 2
+                and rhs.transposed_shape is None and lhs_shape[1] == rhs_shape[0]):
+            target = self._take_colsum_waiter(rhs, int(rhs_shape[1]))
+            if target is not None:
+                M, K, N = int(lhs_shape[0]), int(lhs_shape[1]), int(rhs_shape[1])
+                lv = _lib.VIEW_TRANSPOSED if lhs.transposed_shape is not None else _lib.VIEW_CONTIGUOUS
+                cs = self.ctx.alloc(4 * max(N, 1))
+                out = ctypes.c_void_p()
+                _lib.call("orca_hip_matmul_colsum", self.ctx.handle, lhs.ptr, rhs.ptr, M, K, N, lv, dtype, cs.ptr,
+                          ctypes.byref(out))
+                target._buf, target._fill = cs, None
+                return self._wrap(out, M * N)
         out = ctypes.c_void_p()
         dl, rl = _dims(lhs_shape)
         dr, rr = _dims(rhs_shape)
@@ -227,7 +273,58 @@ class HipBackend:
         return self._reshape_like("expand", s, in_shape, out_shape, dtype)
 
     def sum_to_shape(self, s, in_shape, out_shape, dtype=_lib.F32):
+        in_shape, out_shape = tuple(int(d) for d in in_shape), tuple(int(d) for d in out_shape)
+        if self.deferred and dtype == _lib.F32 and s.transposed_shape is None and not s.pending:
+            if in_shape == out_shape:
+                if s.ident is None:
+                    s.ident = self._reshape_like("sum_to_shape", s, in_shape, out_shape, dtype)
+                return s.ident
+            if len(in_shape) == 2 and out_shape in ((1, in_shape[1]), (in_shape[1],)):
+                return self._deferred_colsum(s, in_shape)
         return self._reshape_like("sum_to_shape", s, in_shape, out_shape, dtype)
+
+    def _deferred_colsum(self, s: HipStorage, in_shape) -> HipStorage:
+        """sum_to_shape(s, [R, N] -> [1, N]) left pending on s (see the module docstring)."""
+        cols = in_shape[1]
+        out = HipStorage(None, cols)
+
+        def fill(st, src=s, shape=in_shape):
+            st._buf = self._reshape_like("sum_to_shape", src, shape, (1, shape[1]), _lib.F32)._buf
+
+        out._fill = fill
+        if s.colsum_waiters is None:
+            s.colsum_waiters = []
+        s.colsum_waiters.append(weakref.ref(out))
+        return out
+
+    @staticmethod
+    def _take_colsum_waiter(s: HipStorage, cols: int):
+        """Removes and returns a still-pending column sum of s with `cols` columns, or None."""
+        found = None
+        live = []
+        for ref in s.colsum_waiters:
+            t = ref()
+            if t is None or not t.pending:
+                continue
+            if found is None and t.n == cols:
+                found = t
+            else:
+                live.append(ref)
+        s.colsum_waiters = live or None
+        return found
+
+    @staticmethod
+    def _mutating(*storages) -> None:
+        """Before an in-place update: values derived lazily from these storages are computed
+        from their current contents, and their memoised identity reductions are dropped."""
+        for s in storages:
+            if s.colsum_waiters:
+                for ref in s.colsum_waiters:
+                    t = ref()
+                    if t is not None:
+                        t.buf  # runs a pending fill
+            s.colsum_waiters = None
+            s.ident = None
 
     def reshape(self, s, in_shape, out_shape, dtype=_lib.F32):
         n_in = int(np.prod(in_shape, dtype=np.int64))
@@ -281,10 +378,12 @@ class HipBackend:
                     beta1: float, beta2: float, eps: float, weight_decay: float, t: int) -> None:
         """In place on p, m, v (orca_hip_adamw_step)."""
         g = self._plain(g)
+        self._mutating(p, m, v)
         _lib.call("orca_hip_adamw_step", self.ctx.handle, p.ptr, g.ptr, m.ptr, v.ptr, n, lr, beta1, beta2, eps,
                   weight_decay, t)
 
     def sgd_step_(self, p: HipStorage, g: HipStorage, n: int, lr: float) -> None:
         """In place on p (orca_hip_sgd_step)."""
         g = self._plain(g)
+        self._mutating(p)
         _lib.call("orca_hip_sgd_step", self.ctx.handle, p.ptr, g.ptr, n, lr)

@@ -693,7 +693,7 @@ void gemm(orca_hip_ctx* ctx, bool trans_a, bool trans_b, size_t M, size_t N, siz
   p.bias = epi.bias;
   p.mask = epi.mask;
   p.ldmask = (int64_t)epi.ldmask;
-  const bool fold_colsum = epi.colsum != nullptr && batch == 1 && !trans_b;
+  const bool fold_colsum = epi.colsum != nullptr && batch == 1 && !trans_b && (splits == 1 || !epi.exact_colsum);
   // Split-K partials (and per-split column sums) go to the caller's workspace
   // when it provides one, else to blocks from the context cache.
   const size_t ws_need = plan_workspace_floats(plan, M, N, batch, fold_colsum);
@@ -822,6 +822,34 @@ int orca_hip_gemm(orca_hip_ctx* ctx, int trans_a, int trans_b, size_t M, size_t 
 }
 
 // orca-backend-cpu/src/backend.rs:130-221 (contract), with lazy-transpose views.
+// Backend::matmul of [M, K] x [K, N] plus sum_to_shape(rhs, [K, N] -> [1, N])
+// (backend.rs:499-530) in one product: the column sum is folded into the
+// GEMM's loads of rhs when K is not split, else taken in a separate pass.
+int orca_hip_matmul_colsum(orca_hip_ctx* ctx, const void* lhs, const void* rhs, size_t M, size_t K, size_t N,
+                           int lhs_view, int dtype, void* colsum, void** out) {
+  return guard([&] {
+    bind(ctx);
+    check_f32(dtype, "matmul");
+    if (!colsum) fail(ORCA_HIP_ERR_INTERNAL, "matmul_colsum: null column-sum output");
+    const bool ta = lhs_view == ORCA_HIP_VIEW_TRANSPOSED;
+    check_extent(ctx, lhs, M * K * sizeof(float), "matmul (lhs)");
+    check_extent(ctx, rhs, K * N * sizeof(float), "matmul (rhs)");
+    check_extent(ctx, colsum, N * sizeof(float), "matmul_colsum (colsum)");
+    float* o = new_output(ctx, M * N);
+    if (M == 0) {  // no product, but the column sum still covers rhs
+      launch_colsum(ctx, static_cast<const float*>(rhs), K, N, N, static_cast<float*>(colsum));
+      *out = o;
+      return;
+    }
+    GemmEpi e;
+    e.colsum = static_cast<float*>(colsum);
+    e.exact_colsum = true;
+    gemm(ctx, ta, false, M, N, K, static_cast<const float*>(lhs), ta ? M : K, 0, static_cast<const float*>(rhs), N,
+         0, o, N, 0, 1, e);
+    *out = o;
+  });
+}
+
 int orca_hip_matmul(orca_hip_ctx* ctx, const void* lhs, const void* rhs, const size_t* lhs_shape, size_t lhs_rank,
                     const size_t* rhs_shape, size_t rhs_rank, int dtype, int lhs_view, int rhs_view, void** out) {
   return guard([&] {

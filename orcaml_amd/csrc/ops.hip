@@ -498,6 +498,22 @@ ReduceArgs make_reduce(const size_t* in_shape, size_t in_rank, const size_t* out
 const float* as_f(const void* p) { return static_cast<const float*>(p); }
 
 }  // namespace
+
+// colsum[c] = sum_r src[r * ld + c] in ascending r, through colreduce_kernel:
+// the same sequence of f32 additions as sum_to_shape's loop.
+void launch_colsum(orca_hip_ctx* ctx, const float* src, size_t rows, size_t cols, size_t ld, float* colsum) {
+  if (cols == 0) return;
+  if (rows == 0) {
+    launch_fill(ctx, colsum, 0.0f, cols);
+    return;
+  }
+  ProfScope ps(ctx, "colsum_rows", 0.0, 4.0 * (double)rows * cols + 4.0 * cols);
+  const unsigned g = (unsigned)((cols + CR_COLS - 1) / CR_COLS);
+  hipLaunchKernelGGL(colreduce_kernel<false>, dim3(g), dim3(CR_THREADS), 0, ctx->stream, src, colsum, cols,
+                     (int64_t)rows, ld);
+  ORCA_HIP_CHECK(hipGetLastError());
+}
+
 }  // namespace orca_hip
 
 using namespace orca_hip;

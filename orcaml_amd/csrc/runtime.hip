@@ -1,4 +1,4 @@
-// Context, caching allocator, host I/O, timing and the small copy/fill/colsum
+// Context, caching allocator, host I/O, timing and the small copy/fill
 // kernels of liborca_hip.so.
 #include <algorithm>
 #include <cstdio>
@@ -197,15 +197,6 @@ __global__ void copy_kernel(float* __restrict__ dst, const float* __restrict__ s
 
 // One thread per column, rows in ascending order: the accumulation order of
 // orca-backend-cpu's sum_to_shape (backend.rs:519-527) for [R,C] -> [1,C].
-__global__ void colsum_kernel(const float* __restrict__ src, size_t rows, size_t cols, size_t ld,
-                              float* __restrict__ out) {
-  size_t c = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (c >= cols) return;
-  float s = 0.0f;
-  const float* p = src + c;
-  for (size_t r = 0; r < rows; ++r) s = s + p[r * ld];
-  out[c] = s;
-}
 
 void launch_fill(orca_hip_ctx* ctx, float* dst, float v, size_t n) {
   if (n == 0) return;
@@ -221,13 +212,6 @@ void launch_copy(orca_hip_ctx* ctx, float* dst, const float* src, size_t n) {
   ORCA_HIP_CHECK(hipGetLastError());
 }
 
-void launch_colsum(orca_hip_ctx* ctx, const float* src, size_t rows, size_t cols, size_t ld, float* colsum) {
-  if (cols == 0) return;
-  ProfScope ps(ctx, "colsum_seq", 0.0, 4.0 * (double)rows * cols + 4.0 * cols);
-  unsigned g = (unsigned)((cols + 63) / 64);
-  hipLaunchKernelGGL(colsum_kernel, dim3(g), dim3(64), 0, ctx->stream, src, rows, cols, ld, colsum);
-  ORCA_HIP_CHECK(hipGetLastError());
-}
 
 float* new_output(orca_hip_ctx* ctx, size_t n) {
   return static_cast<float*>(ctx->alloc.allocate(n * sizeof(float), ctx->stream));

@@ -195,6 +195,9 @@ struct GemmEpi {
   const float* mask = nullptr;
   size_t ldmask = 0;
   float* colsum = nullptr;
+  // Column sums in ascending row order (bit-identical to sum_to_shape) even
+  // when K is split: the split product then takes them in a separate pass.
+  bool exact_colsum = false;
   // Optional caller-owned workspace for split-K partials (see
   // gemm_workspace_floats); without it they come from the context cache.
   float* ws = nullptr;

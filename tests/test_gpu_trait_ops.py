@@ -220,6 +220,78 @@ def test_composed_step_mlp784_128_on_hip(hb, kind, steps):
     np.testing.assert_array_equal(A.argmax_rows(logits), ref["preds"])
 
 
+@pytest.mark.parametrize("M,K,N,view", [(784, 1024, 4096, True), (128, 64, 128, True), (64, 2048, 64, True),
+                                        (33, 300, 70, True), (1000, 100, 1030, True), (96, 256, 160, False),
+                                        (0, 16, 8, True), (8, 0, 12, True)])
+def test_matmul_colsum_equals_matmul_and_sum_to_shape(hb, M, K, N, view):
+    """orca_hip_matmul_colsum (via a pending sum_to_shape consumed by matmul): the product bit
+    for bit as matmul, the column sum bit for bit as the oracle's sum_to_shape loop -- folded
+    into the product (pipelined or generic kernel) or, when K is split, in its own pass."""
+    from orcaml_amd.backend import HipBackend
+
+    rng = np.random.default_rng(M + 7 * K + N)
+    g = rng.standard_normal((K, N)).astype(np.float32)
+    if view:
+        lhs = hb.transpose(up(hb, rng.standard_normal((K, M)).astype(np.float32)), (K, M), 0, 1)
+    else:
+        lhs = up(hb, rng.standard_normal((M, K)).astype(np.float32))
+    plain = HipBackend(hb.ctx, deferred=False)
+    want = down(hb, plain.matmul(lhs, up(hb, g), (M, K), (K, N)), (M, N))
+    G = up(hb, g)
+    pend = hb.sum_to_shape(G, (K, N), (1, N))
+    assert pend.pending
+    got = hb.matmul(lhs, G, (M, K), (K, N))
+    assert not pend.pending
+    np.testing.assert_array_equal(down(hb, got, (M, N)), want)
+    np.testing.assert_array_equal(down(hb, pend, (1, N)), O.sum_to_shape(g, (1, N)))
+
+
+def test_pending_column_sum_used_first_and_identity_memo(hb):
+    """A pending column sum read before any matmul is computed by the sum_to_shape kernel, and
+    the matmul that follows leaves it alone; an identity sum_to_shape of one storage is one
+    storage; an in-place update drops what was derived from the old values."""
+    rng = np.random.default_rng(5)
+    g = rng.standard_normal((300, 70)).astype(np.float32)
+    G = up(hb, g)
+    pend = hb.sum_to_shape(G, (300, 70), (70,))
+    first = down(hb, pend, (70,))
+    np.testing.assert_array_equal(first, O.sum_to_shape(g, (70,)))
+    x = up(hb, rng.standard_normal((300, 40)).astype(np.float32))
+    hb.matmul(hb.transpose(x, (300, 40), 0, 1), G, (40, 300), (300, 70))
+    np.testing.assert_array_equal(down(hb, pend, (70,)), first)
+    a = hb.sum_to_shape(G, (300, 70), (300, 70))
+    assert hb.sum_to_shape(G, (300, 70), (300, 70)) is a
+    np.testing.assert_array_equal(down(hb, a, (300, 70)), O.sum_to_shape(g, (300, 70)))
+    p = up(hb, rng.standard_normal((300, 70)).astype(np.float32))
+    m, v = (up(hb, np.zeros((300, 70), np.float32)) for _ in range(2))
+    before = hb.sum_to_shape(p, (300, 70), (1, 70))
+    ident = hb.sum_to_shape(p, (300, 70), (300, 70))
+    p_old = down(hb, p, (300, 70))
+    hb.adamw_step_(p, G, m, v, 300 * 70, 1e-3, 0.9, 0.999, 1e-8, 0.01, 1)
+    np.testing.assert_array_equal(down(hb, before, (1, 70)), O.sum_to_shape(p_old, (1, 70)))
+    assert hb.sum_to_shape(p, (300, 70), (300, 70)) is not ident
+
+
+@pytest.mark.parametrize("name,kind", [(synth.MLP_SMALL, "sgd"), (synth.MLP_SMALL, "adamw"),
+                                       (synth.MLP_MEDIUM, "adamw")])
+def test_composed_step_deferred_reductions_change_no_bit(hb, name, kind):
+    """The composed step with the identity memo and the deferred bias column sums equals the
+    same step with every sum_to_shape run at once, bit for bit (the 784-1024-1024-10 case
+    splits dW1's K, so its column sum takes the separate pass)."""
+    from orcaml_amd.backend import HipBackend
+
+    w = synth.WORKLOADS[name]
+    params, x, labels, onehot = synth.mlp_problem(w["seed"], w["dims"], w["batch"])
+    opt = dict(lr=0.1) if kind == "sgd" else dict(lr=1e-3, weight_decay=0.01)
+    runs = [composed(A.Autodiff(HipBackend(hb.ctx, deferred=d)), w["dims"], params, x, onehot, kind, 2, **opt)
+            for d in (True, False)]
+    (l1, g1, o1, p1), (l2, g2, o2, p2) = runs
+    np.testing.assert_array_equal(l1, l2)
+    np.testing.assert_array_equal(o1, o2)
+    for a, b in zip(g1 + p1, g2 + p2):
+        np.testing.assert_array_equal(a, b)
+
+
 def test_composed_step_allocates_nothing_in_steady_state(hb, ctx):
     """After warm-up the caching allocator serves every buffer of a step."""
     w = synth.WORKLOADS[synth.MLP_SMALL]
