@@ -182,11 +182,31 @@ def check(rc: int) -> None:
         raise OrcaHipError(rc, msg.decode() if msg else "")
 
 
+_FNS: dict = {}
+
+
 def call(name: str, *args) -> None:
-    check(getattr(load(), name)(*args))
+    fn = _FNS.get(name)
+    if fn is None:
+        fn = _FNS[name] = getattr(load(), name)
+    rc = fn(*args)
+    if rc != OK:
+        check(rc)
+
+
+_DIMS: dict = {}
 
 
 def dims(shape) -> tuple:
-    shape = tuple(int(s) for s in shape)
-    arr = (ctypes.c_size_t * max(1, len(shape)))(*shape)
-    return arr, len(shape)
+    """(size_t array, rank) of a shape.  The C side only reads the array, so one
+    array per distinct shape is built and reused (ops see few distinct shapes)."""
+    key = shape if type(shape) is tuple else tuple(shape)
+    hit = _DIMS.get(key)
+    if hit is not None:
+        return hit
+    dims_ = tuple(int(s) for s in key)
+    hit = ((ctypes.c_size_t * max(1, len(dims_)))(*dims_), len(dims_))
+    if len(_DIMS) >= 4096:
+        _DIMS.clear()
+    _DIMS[key] = hit
+    return hit

@@ -28,6 +28,7 @@ orca-autograd/src/backend.rs:1684-1697, 1448-1499):
 from __future__ import annotations
 
 import ctypes
+import math
 import weakref
 
 import numpy as np
@@ -75,6 +76,10 @@ def _dims(shape):
     return _lib.dims(shape)
 
 
+def _numel(shape) -> int:
+    return math.prod(int(d) for d in shape)
+
+
 class HipBackend:
     """Drop-in for `GpuBackend` (orca-backend-gpu/src/backend.rs:45-50)."""
 
@@ -107,14 +112,14 @@ class HipBackend:
         out = ctypes.c_void_p()
         d, r = _dims(shape)
         _lib.call("orca_hip_" + name, self.ctx.handle, s.ptr, d, r, dtype, ctypes.byref(out))
-        return self._wrap(out, int(np.prod(shape, dtype=np.int64)))
+        return self._wrap(out, _numel(shape))
 
     def _op2(self, name, a, b, shape, dtype):
         a, b = self._plain(a), self._plain(b)
         out = ctypes.c_void_p()
         d, r = _dims(shape)
         _lib.call("orca_hip_" + name, self.ctx.handle, a.ptr, b.ptr, d, r, dtype, ctypes.byref(out))
-        return self._wrap(out, int(np.prod(shape, dtype=np.int64)))
+        return self._wrap(out, _numel(shape))
 
     def _reshape_like(self, name, s, in_shape, out_shape, dtype):
         s = self._plain(s)
@@ -122,7 +127,7 @@ class HipBackend:
         di, ri = _dims(in_shape)
         do, ro = _dims(out_shape)
         _lib.call("orca_hip_" + name, self.ctx.handle, s.ptr, di, ri, do, ro, dtype, ctypes.byref(out))
-        return self._wrap(out, int(np.prod(out_shape, dtype=np.int64)))
+        return self._wrap(out, _numel(out_shape))
 
     # ---- trait methods (orca-tensor/src/backend.rs) ----
     def device(self) -> str:
@@ -132,7 +137,7 @@ class HipBackend:
         out = ctypes.c_void_p()
         d, r = _dims(shape)
         _lib.call("orca_hip_zeros", self.ctx.handle, d, r, dtype, ctypes.byref(out))
-        return self._wrap(out, int(np.prod(shape, dtype=np.int64)))
+        return self._wrap(out, _numel(shape))
 
     def from_f32_slice(self, shape, data):
         data = np.ascontiguousarray(data, np.float32).reshape(-1)
@@ -154,7 +159,7 @@ class HipBackend:
         d, r = _dims(shape)
         _lib.call("orca_hip_from_bytes", self.ctx.handle, d, r, arr.ctypes.data_as(ctypes.c_void_p), arr.size, dtype,
                   ctypes.byref(out))
-        return self._wrap(out, int(np.prod(shape, dtype=np.int64)))
+        return self._wrap(out, _numel(shape))
 
     def to_bytes(self, s: HipStorage) -> bytes:
         s = self._plain(s)
@@ -182,7 +187,7 @@ class HipBackend:
         rv = _lib.VIEW_TRANSPOSED if rhs.transposed_shape is not None else _lib.VIEW_CONTIGUOUS
         _lib.call("orca_hip_matmul", self.ctx.handle, lhs.ptr, rhs.ptr, dl, rl, dr, rr, dtype, lv, rv,
                   ctypes.byref(out))
-        n = int(np.prod(lhs_shape[:-1], dtype=np.int64)) * int(rhs_shape[-1])
+        n = _numel(lhs_shape[:-1]) * int(rhs_shape[-1])
         return self._wrap(out, n)
 
     def transpose(self, s: HipStorage, shape, dim0: int, dim1: int, dtype=_lib.F32):
@@ -219,7 +224,7 @@ class HipBackend:
         d, r = _dims(shape)
         _lib.call("orca_hip_mul_scalar", self.ctx.handle, s.ptr, ctypes.c_float(scalar), d, r, dtype,
                   ctypes.byref(out))
-        return self._wrap(out, int(np.prod(shape, dtype=np.int64)))
+        return self._wrap(out, _numel(shape))
 
     def relu(self, s, shape, dtype=_lib.F32):
         return self._op1("relu", s, shape, dtype)
@@ -259,7 +264,7 @@ class HipBackend:
         out = ctypes.c_void_p()
         d, rk = _dims(shape)
         _lib.call("orca_hip_div_backward_rhs", self.ctx.handle, g.ptr, l.ptr, r.ptr, d, rk, dtype, ctypes.byref(out))
-        return self._wrap(out, int(np.prod(shape, dtype=np.int64)))
+        return self._wrap(out, _numel(shape))
 
     def accumulate_grad(self, a, b):
         a, b = self._plain(a), self._plain(b)
@@ -327,8 +332,8 @@ class HipBackend:
             s.ident = None
 
     def reshape(self, s, in_shape, out_shape, dtype=_lib.F32):
-        n_in = int(np.prod(in_shape, dtype=np.int64))
-        n_out = int(np.prod(out_shape, dtype=np.int64))
+        n_in = _numel(in_shape)
+        n_out = _numel(out_shape)
         if n_in != n_out:
             raise _lib.OrcaHipError(_lib.ERR_SHAPE, f"Shape mismatch during reshape: expected {n_in} elements, "
                                                     f"got {n_out} elements")
@@ -344,7 +349,7 @@ class HipBackend:
         do, ro = _dims(out_shape)
         _lib.call("orca_hip_max_to_shape_backward", self.ctx.handle, g.ptr, x.ptr, y.ptr, di, ri, do, ro, dtype,
                   ctypes.byref(out))
-        return self._wrap(out, int(np.prod(in_shape, dtype=np.int64)))
+        return self._wrap(out, _numel(in_shape))
 
     def has_nan_or_inf(self, s, dtype=_lib.F32) -> bool:
         s = self._plain(s)
