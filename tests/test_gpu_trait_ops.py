@@ -119,6 +119,23 @@ def test_max_to_shape_and_backward_bit_exact(hb, shape):
         O.max_to_shape_backward(g, x, y))
 
 
+@pytest.mark.parametrize("shape", [(1024, 4096), (7, 33), (3, 5, 8)])
+def test_reductions_that_reduce_nothing_bit_exact(hb, shape):
+    """sum_to_shape / max_to_shape onto the input's own shape still take the reduction's first
+    step (0 + x; max(-FLT_MAX, x) with a strict >): -0 becomes +0, NaN and -inf become -FLT_MAX
+    for max, as the reference's loops give."""
+    from orcaml_amd.backend import HipBackend
+
+    plain = HipBackend(hb.ctx, deferred=False)  # no memo: the kernel runs on every call
+    x = special_values(np.random.default_rng(shape[-1]), shape)
+    got = down(plain, plain.sum_to_shape(up(plain, x), shape, shape), shape)
+    want = O.sum_to_shape(x, shape)
+    np.testing.assert_array_equal(got, want)
+    assert not np.signbit(got[x == 0]).any()
+    np.testing.assert_array_equal(down(plain, plain.max_to_shape(up(plain, x), shape, shape), shape),
+                                  O.max_to_shape(x, shape))
+
+
 @pytest.mark.parametrize("shape,out_shape", [((1000, 70), (1, 70)), ((3, 300, 33), (33,)), ((129, 4096), (1, 4096))])
 def test_column_max_to_shape_bit_exact(hb, shape, out_shape):
     rng = np.random.default_rng(shape[-1])
