@@ -178,6 +178,9 @@ struct CeRowOut {
   float loss;  // -sum_c t_c (p_c - lse): the row's term of the loss before the 1/B mean
   int pred;    // argmax of the logits
   int target;  // target class (label, or argmax of the one-hot row)
+  // ce_row_label only: whether this thread holds `loss` (one thread of the row does);
+  // pred and target are held by every thread.
+  bool has_loss = true;
 };
 
 // One row held by one wave64: x[j] is the logit of column col(j), used where
@@ -280,11 +283,16 @@ __device__ __forceinline__ CeRowOut ce_row(const float (&x)[VPL], Valid valid, T
 // mask of the columns equal to the max, and for the check below the lane's
 // smallest value and whether it holds a non-finite one.  reload(j) reads
 // x[j] again from memory for rows whose loss terms are irregular.  jl is this
-// lane's slot of the label column (col(jl) == label, valid), or -1.
+// lane's slot of the label column (col(jl) == label, valid), or -1;
+// label_valid says whether some thread of the row has jl >= 0 (0 <= label < C).
+// Two of the row sums have one nonzero term, the label's, so they need no
+// reduction: the loss term is 0 + pl, held by the label's thread (a row
+// without a label column has +0, held by the first thread), and LogBackward's
+// sum is 0 + g_lse_t or +0, known to every thread.
 template <int VPL, class Col, class Valid, class Store, class Reload, class R = WaveRed>
 __device__ __forceinline__ CeRowOut ce_row_label(float (&x)[VPL], Valid valid, Col col, Reload reload, int label,
-                                                 int jl, float inv_b, bool grad, Store store, bool want_argmax,
-                                                 const R& red = R()) {
+                                                 int jl, bool label_valid, bool first, float inv_b, bool grad,
+                                                 Store store, bool want_argmax, const R& red = R()) {
   static_assert(VPL <= 32, "the max mask holds one bit per value");
   float mx = -FLT_MAX, xmin = FLT_MAX, xl = 0.0f;
   bool nonfinite = false;
@@ -319,17 +327,17 @@ __device__ __forceinline__ CeRowOut ce_row_label(float (&x)[VPL], Valid valid, C
   // the smallest difference is (x - lse is monotone in x).
   const float pl = jl >= 0 ? (1.0f * (xl - lse)) * -1.0f : 0.0f;
   const bool irregular = valid(0) && (nonfinite || !(fabsf(xmin - lse) <= FLT_MAX));
-  float pb;
   if (red.any(irregular)) {
     float s = 0.0f;
 #pragma unroll 1
     for (int j = 0; j < VPL; ++j)  // one reload at a time: the rare path adds no register pressure
       if (valid(j)) s = s + ((j == jl ? 1.0f : 0.0f) * (reload(j) - lse)) * -1.0f;
-    pb = red.sum(s);
+    out.loss = red.sum(s);
+    out.has_loss = first;
   } else {
-    pb = red.sum(pl);
+    out.loss = 0.0f + pl;
+    out.has_loss = jl >= 0 || (!label_valid && first);
   }
-  out.loss = pb;
 
   if (grad) {
     const float g_tm = inv_b * -1.0f;
@@ -337,7 +345,7 @@ __device__ __forceinline__ CeRowOut ce_row_label(float (&x)[VPL], Valid valid, C
     const float g_lse_0 = 0.0f + ((g_tm * 0.0f) * -1.0f);  // any other column's (+0)
     float gse;
     if (se > 0.0f && se <= FLT_MAX) {
-      gse = red.sum(jl >= 0 ? 0.0f + g_lse_t : 0.0f) / se;
+      gse = (label_valid ? 0.0f + g_lse_t : 0.0f) / se;
     } else {
       gse = 0.0f;
 #pragma unroll

@@ -77,13 +77,14 @@ __global__ void __launch_bounds__(256) softmax_ce_kernel(const float* __restrict
       if (VEC && (((label & 255) >> 2) == lane)) jl = 4 * (label >> 8) + (label & 3);
       if (!VEC && (label & 63) == lane) jl = label >> 6;
     }
-    r = ce_row_label<VPL>(x, valid, col, [&](int j) { return xr[col(j)]; }, label, jl, inv_b, dr != nullptr, store,
-                          preds || row_correct);
+    r = ce_row_label<VPL>(x, valid, col, [&](int j) { return xr[col(j)]; }, label, jl, label >= 0 && label < C,
+                          lane == 0, inv_b, dr != nullptr, store, preds || row_correct);
   } else {
     r = ce_row<VPL>(x, valid, tval, col, false, label, inv_b, dr != nullptr, store, preds || row_correct);
+    r.has_loss = lane == 0;
   }
+  if (r.has_loss) row_loss[row] = r.loss;
   if (lane == 0) {
-    row_loss[row] = r.loss;
     if (preds) preds[row] = r.pred;
     if (row_correct) row_correct[row] = (r.pred == r.target) ? 1 : 0;
   }
@@ -150,14 +151,15 @@ __global__ void __launch_bounds__(256) softmax_ce_block_kernel(const float* __re
       if (VEC && (((label & 1023) >> 2) == tid)) jl = 4 * (label >> 10) + (label & 3);
       if (!VEC && (label & 255) == tid) jl = label >> 8;
     }
-    r = ce_row_label<VPT>(x, valid, col, [&](int j) { return xr[col(j)]; }, label, jl, inv_b, dr != nullptr, store,
-                          want_argmax, red);
+    r = ce_row_label<VPT>(x, valid, col, [&](int j) { return xr[col(j)]; }, label, jl, label >= 0 && label < C,
+                          tid == 0, inv_b, dr != nullptr, store, want_argmax, red);
   } else {
     auto tval = [&](int j) -> float { return valid(j) ? tr[col(j)] : 0.0f; };
     r = ce_row<VPT>(x, valid, tval, col, false, label, inv_b, dr != nullptr, store, want_argmax, red);
+    r.has_loss = tid == 0;
   }
+  if (r.has_loss) row_loss[row] = r.loss;
   if (tid == 0) {
-    row_loss[row] = r.loss;
     if (preds) preds[row] = r.pred;
     if (row_correct) row_correct[row] = (r.pred == r.target) ? 1 : 0;
   }
