@@ -312,14 +312,17 @@ __device__ __forceinline__ void adamw_elem(float& p, float g, float& m, float& v
 // and stores: the arrays are streamed once per step, so they bypass cache
 // allocation.  (Measured on 2^28 parameters: 6.2 TB/s, against 5.2 TB/s for
 // a grid-stride loop with ordinary accesses.)
+// p_src holds the parameters read, p receives the updated ones (the same
+// buffer for an update in place; each element is read before it is written
+// by the same thread).
 template <bool DEV>
-__global__ void __launch_bounds__(256) adamw_vec_kernel(float4* __restrict__ p, const float4* __restrict__ g,
+__global__ void __launch_bounds__(256) adamw_vec_kernel(float4* p, const float4* p_src, const float4* __restrict__ g,
                                                         float4* __restrict__ m, float4* __restrict__ v, size_t n4,
                                                         AdamWScalars ka, const AdamWScalars* __restrict__ kd) {
   const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n4) return;
   const AdamWScalars k = DEV ? *kd : ka;
-  floatx4 pp = __builtin_nontemporal_load(reinterpret_cast<const floatx4*>(p) + i);
+  floatx4 pp = __builtin_nontemporal_load(reinterpret_cast<const floatx4*>(p_src) + i);
   const floatx4 gg = __builtin_nontemporal_load(reinterpret_cast<const floatx4*>(g) + i);
   floatx4 mm = __builtin_nontemporal_load(reinterpret_cast<const floatx4*>(m) + i);
   floatx4 vv = __builtin_nontemporal_load(reinterpret_cast<const floatx4*>(v) + i);
@@ -332,14 +335,54 @@ __global__ void __launch_bounds__(256) adamw_vec_kernel(float4* __restrict__ p, 
   __builtin_nontemporal_store(floatx4{va[0], va[1], va[2], va[3]}, reinterpret_cast<floatx4*>(v) + i);
 }
 
+// Bounded-grid variant for an update that runs beside a GEMM on another
+// stream: a few 256-thread blocks per CU, each thread streaming ADAMW_RES_U
+// float4 of every array per iteration (all loads issued before the
+// arithmetic).  The launch holds few registers per SIMD, so a GEMM launched
+// while it runs can still place its blocks; a flat grid of one float4 per
+// thread fills every SIMD's register file and delays such a GEMM.
+constexpr int ADAMW_RES_U = 4;
 template <bool DEV>
-__global__ void adamw_scalar_kernel(float* __restrict__ p, const float* __restrict__ g, float* __restrict__ m,
+__global__ void __launch_bounds__(256) adamw_res_kernel(float4* p, const float4* p_src, const float4* __restrict__ g,
+                                                        float4* __restrict__ m, float4* __restrict__ v, size_t n4,
+                                                        AdamWScalars ka, const AdamWScalars* __restrict__ kd) {
+  const AdamWScalars k = DEV ? *kd : ka;
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  auto update4 = [&](floatx4 pp, floatx4 gg, floatx4 mm, floatx4 vv, size_t j) {
+    float pa[4] = {pp.x, pp.y, pp.z, pp.w}, ma[4] = {mm.x, mm.y, mm.z, mm.w}, va[4] = {vv.x, vv.y, vv.z, vv.w};
+    const float ga[4] = {gg.x, gg.y, gg.z, gg.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) adamw_elem(pa[e], ga[e], ma[e], va[e], k);
+    __builtin_nontemporal_store(floatx4{pa[0], pa[1], pa[2], pa[3]}, reinterpret_cast<floatx4*>(p) + j);
+    __builtin_nontemporal_store(floatx4{ma[0], ma[1], ma[2], ma[3]}, reinterpret_cast<floatx4*>(m) + j);
+    __builtin_nontemporal_store(floatx4{va[0], va[1], va[2], va[3]}, reinterpret_cast<floatx4*>(v) + j);
+  };
+  auto ld = [](const float4* a, size_t j) { return __builtin_nontemporal_load(reinterpret_cast<const floatx4*>(a) + j); };
+  for (; i + (ADAMW_RES_U - 1) * stride < n4; i += ADAMW_RES_U * stride) {
+    floatx4 pp[ADAMW_RES_U], gg[ADAMW_RES_U], mm[ADAMW_RES_U], vv[ADAMW_RES_U];
+#pragma unroll
+    for (int u = 0; u < ADAMW_RES_U; ++u) {
+      const size_t j = i + u * stride;
+      pp[u] = ld(p_src, j);
+      gg[u] = ld(g, j);
+      mm[u] = ld(m, j);
+      vv[u] = ld(v, j);
+    }
+#pragma unroll
+    for (int u = 0; u < ADAMW_RES_U; ++u) update4(pp[u], gg[u], mm[u], vv[u], i + u * stride);
+  }
+  for (; i < n4; i += stride) update4(ld(p_src, i), ld(g, i), ld(m, i), ld(v, i), i);
+}
+
+template <bool DEV>
+__global__ void adamw_scalar_kernel(float* p, const float* p_src, const float* __restrict__ g, float* __restrict__ m,
                                     float* __restrict__ v, size_t begin, size_t n, AdamWScalars ka,
                                     const AdamWScalars* __restrict__ kd) {
   const AdamWScalars k = DEV ? *kd : ka;
   size_t stride = (size_t)gridDim.x * blockDim.x;
   for (size_t i = begin + (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
-    float pp = p[i], mm = m[i], vv = v[i];
+    float pp = p_src[i], mm = m[i], vv = v[i];
     adamw_elem(pp, g[i], mm, vv, k);
     p[i] = pp;
     m[i] = mm;
@@ -454,13 +497,15 @@ void adamw_store_scalars(orca_hip_ctx* ctx, AdamWScalars* dst, const AdamWScalar
 }
 
 void adamw(orca_hip_ctx* ctx, float* p, const float* g, float* m, float* v, size_t n, double lr, double b1, double b2,
-           double eps, double wd, int64_t t, hipStream_t stream, const AdamWScalars* dev_scalars) {
+           double eps, double wd, int64_t t, hipStream_t stream, const AdamWScalars* dev_scalars, const float* p_src,
+           int blocks_per_cu) {
   if (!stream) stream = ctx->stream;
   if (n == 0) return;
+  if (!p_src) p_src = p;
   const AdamWScalars k = dev_scalars ? AdamWScalars{} : adamw_scalars(lr, b1, b2, eps, wd, t);
   ProfScope ps(ctx, "adamw", 0.0, 28.0 * (double)n, stream);
   size_t done = 0;
-  if (aligned16(p) && aligned16(g) && aligned16(m) && aligned16(v)) {
+  if (aligned16(p) && aligned16(p_src) && aligned16(g) && aligned16(m) && aligned16(v)) {
     size_t n4 = n / 4;
     if (n4) {
       const size_t gsz = (n4 + 255) / 256;
@@ -469,22 +514,31 @@ void adamw(orca_hip_ctx* ctx, float* p, const float* g, float* m, float* v, size
       auto* g4 = reinterpret_cast<const float4*>(g);
       auto* m4 = reinterpret_cast<float4*>(m);
       auto* v4 = reinterpret_cast<float4*>(v);
-      if (dev_scalars)
-        hipLaunchKernelGGL(adamw_vec_kernel<true>, dim3((unsigned)gsz), dim3(256), 0, stream, p4, g4, m4, v4, n4, k,
-                           dev_scalars);
-      else
-        hipLaunchKernelGGL(adamw_vec_kernel<false>, dim3((unsigned)gsz), dim3(256), 0, stream, p4, g4, m4, v4, n4,
+      auto* s4 = reinterpret_cast<const float4*>(p_src);
+      if (blocks_per_cu > 0) {
+        const size_t rg = std::min(gsz, (size_t)ctx->num_cus * (size_t)blocks_per_cu);
+        if (dev_scalars)
+          hipLaunchKernelGGL(adamw_res_kernel<true>, dim3((unsigned)rg), dim3(256), 0, stream, p4, s4, g4, m4, v4, n4,
+                             k, dev_scalars);
+        else
+          hipLaunchKernelGGL(adamw_res_kernel<false>, dim3((unsigned)rg), dim3(256), 0, stream, p4, s4, g4, m4, v4,
+                             n4, k, dev_scalars);
+      } else if (dev_scalars)
+        hipLaunchKernelGGL(adamw_vec_kernel<true>, dim3((unsigned)gsz), dim3(256), 0, stream, p4, s4, g4, m4, v4, n4,
                            k, dev_scalars);
+      else
+        hipLaunchKernelGGL(adamw_vec_kernel<false>, dim3((unsigned)gsz), dim3(256), 0, stream, p4, s4, g4, m4, v4,
+                           n4, k, dev_scalars);
     }
     done = 4 * n4;
   }
   if (done < n) {
     unsigned gsz = grid_for(n - done, 256, ctx->num_cus * 8);
     if (dev_scalars)
-      hipLaunchKernelGGL(adamw_scalar_kernel<true>, dim3(gsz), dim3(256), 0, stream, p, g, m, v, done, n, k,
+      hipLaunchKernelGGL(adamw_scalar_kernel<true>, dim3(gsz), dim3(256), 0, stream, p, p_src, g, m, v, done, n, k,
                          dev_scalars);
     else
-      hipLaunchKernelGGL(adamw_scalar_kernel<false>, dim3(gsz), dim3(256), 0, stream, p, g, m, v, done, n, k,
+      hipLaunchKernelGGL(adamw_scalar_kernel<false>, dim3(gsz), dim3(256), 0, stream, p, p_src, g, m, v, done, n, k,
                          dev_scalars);
   }
   ORCA_HIP_CHECK(hipGetLastError());

@@ -19,6 +19,13 @@
 // streaming the layer's input once.  ORCA_HIP_FUSED_HEAD=0 at creation keeps
 // the GEMM + softmax-CE path, ORCA_HIP_OVERLAP_UPDATE=0 runs the whole update
 // on the context stream after the backward (A/B comparisons).
+// With AdamW and a side stream the parameters have two arenas, P and P_next:
+// the update reads P and writes P_next, and they swap after each step.  The
+// update of layers >= 1 then starts right after dW of layer 1, beside layer
+// 1's dZ product (which reads P): 70 % of it on a grid of two blocks per CU
+// (room for the GEMM's blocks), the rest on the flat grid once that product
+// is done, beside layer 0's dW.  ORCA_HIP_DOUBLE_ARENA=0 keeps one arena;
+// ORCA_HIP_SIDE_FRAC (percent) and ORCA_HIP_SIDE_BPC tune the split.
 // Every buffer, split-K workspaces included, is allocated at creation: a step
 // allocates nothing and never synchronises.  With ORCA_HIP_GRAPH=1 the step is
 // captured into a HIP graph at its first call (forward, loss, backward and the
@@ -58,7 +65,17 @@ struct orca_hip_mlp {
   // Second stream (default priority) for the update of layers >= 1, which
   // overlaps the first layer's weight-gradient GEMM; fork / join events.
   hipStream_t side = nullptr;
-  hipEvent_t fork = nullptr, join = nullptr;
+  hipEvent_t fork = nullptr, join = nullptr, mid = nullptr;
+  // Second parameter arena: with it, AdamW reads P and writes P_next, so the
+  // update of layers >= 1 can start as soon as their gradients exist (dW of
+  // layer 1) and run beside layer 1's dZ product, which still reads P; the
+  // two arenas swap roles after every step.
+  float* P_next = nullptr;
+  // The side-stream update in two parts: [split, split + side_a) with a grid of
+  // side_bpc blocks per CU beside layer 1's dZ product, the rest with the flat
+  // grid once that product is done (beside layer 0's dW, which leaves CUs idle).
+  int side_bpc = 2;
+  size_t side_a = 0;
   // Persistent workspaces: a step makes no allocator call, so it can be
   // captured once into a HIP graph and replayed.
   orca_hip::AdamWScalars* kdev = nullptr;  // this step's AdamW scalars (device)
@@ -77,6 +94,7 @@ struct orca_hip_mlp {
     for (void* p : owned) ctx->alloc.release(p);
     if (fork) (void)hipEventDestroy(fork);
     if (join) (void)hipEventDestroy(join);
+    if (mid) (void)hipEventDestroy(mid);
     if (side) (void)hipStreamDestroy(side);
   }
 };
@@ -137,29 +155,41 @@ void step_body(orca_hip_mlp* m, const AdamWScalars* kdev) {
   // when both streams have finished.
   const size_t split = L > 1 ? m->off[2] : 0;  // arena offset of W_1
   bool forked = false;
-  auto update = [&](size_t begin, size_t end, hipStream_t stream) {
+  // With a second arena the update writes P_next and reads P.
+  float* P_out = m->P_next ? m->P_next : m->P;
+  auto update = [&](size_t begin, size_t end, hipStream_t stream, int bpc = 0) {
     if (end <= begin) return;
     if (m->opt.kind == 1)
-      adamw(ctx, m->P + begin, m->G + begin, m->Mo + begin, m->Vo + begin, end - begin, m->opt.lr, m->opt.beta1,
-            m->opt.beta2, m->opt.eps, m->opt.weight_decay, m->t, stream, kdev);
+      adamw(ctx, P_out + begin, m->G + begin, m->Mo + begin, m->Vo + begin, end - begin, m->opt.lr, m->opt.beta1,
+            m->opt.beta2, m->opt.eps, m->opt.weight_decay, m->t, stream, kdev, m->P + begin, bpc);
     else
       sgd(ctx, m->P + begin, m->G + begin, end - begin, m->opt.lr, stream);
+  };
+  auto fork_update = [&]() {
+    ORCA_HIP_CHECK(hipEventRecord(m->fork, ctx->stream));
+    ORCA_HIP_CHECK(hipStreamWaitEvent(m->side, m->fork, 0));
+    update(split, m->arena, m->side);
+    ORCA_HIP_CHECK(hipEventRecord(m->join, m->side));
+    forked = true;
   };
   for (size_t l = n_gemm; l-- > 0;) {
     const size_t K = m->dims[l], N = m->dims[l + 1];
     const float* a = l == 0 ? m->x : m->H[l - 1];
-    if (l == 0 && m->side && split > 0) {
-      ORCA_HIP_CHECK(hipEventRecord(m->fork, ctx->stream));
-      ORCA_HIP_CHECK(hipStreamWaitEvent(m->side, m->fork, 0));
-      update(split, m->arena, m->side);
-      ORCA_HIP_CHECK(hipEventRecord(m->join, m->side));
-      forked = true;
-    }
+    if (l == 0 && m->side && split > 0 && !forked) fork_update();
     GemmEpi ew;
     ew.ws = m->gemm_ws;
     ew.ws_floats = m->gemm_ws_floats;
     ew.colsum = m->G + m->off[2 * l + 1];  // bias gradient
     gemm(ctx, true, false, K, N, B, a, K, 0, g, N, 0, m->G + m->off[2 * l], N, 0, 1, ew);
+    // Layers >= 1 have all their gradients after dW of layer 1; with a second
+    // arena nothing of this step writes the P that layer 1's dZ reads.
+    const bool early = l == 1 && m->P_next && m->side && split > 0;
+    if (early) {
+      ORCA_HIP_CHECK(hipEventRecord(m->fork, ctx->stream));
+      ORCA_HIP_CHECK(hipStreamWaitEvent(m->side, m->fork, 0));
+      update(split, split + m->side_a, m->side, m->side_bpc);
+      forked = true;
+    }
     if (l > 0) {
       GemmEpi ex;
       ex.ws = m->gemm_ws;
@@ -171,6 +201,12 @@ void step_body(orca_hip_mlp* m, const AdamWScalars* kdev) {
       gemm(ctx, false, true, B, K, N, g, N, 0, m->P + m->off[2 * l], N, 0, dz, K, 0, 1, ex);
       g = dz;
       ping ^= 1;
+    }
+    if (early) {
+      ORCA_HIP_CHECK(hipEventRecord(m->mid, ctx->stream));
+      ORCA_HIP_CHECK(hipStreamWaitEvent(m->side, m->mid, 0));
+      update(split + m->side_a, m->arena, m->side);
+      ORCA_HIP_CHECK(hipEventRecord(m->join, m->side));
     }
   }
   // ---- update (parameter order W_0, b_0, W_1, ...; flat passes over the arena) ----
@@ -213,6 +249,7 @@ void step(orca_hip_mlp* m) {
   // Per-kernel timing needs events around each launch: run eagerly then.
   if (!m->use_graph || ctx->prof.enabled) {
     step_body(m, nullptr);
+    if (m->P_next) std::swap(m->P, m->P_next);
     return;
   }
   if (m->opt.kind == 1)
@@ -331,6 +368,20 @@ int orca_hip_mlp_create(orca_hip_ctx* ctx, const size_t* dims, size_t n_layers, 
     // it is opt-in.
     const char* eg = std::getenv("ORCA_HIP_GRAPH");
     m->use_graph = eg && eg[0] == '1';
+    // A captured step holds fixed arena pointers, so the second arena is for
+    // eager steps with AdamW and a side stream only.
+    const char* da = std::getenv("ORCA_HIP_DOUBLE_ARENA");
+    const char* sb = std::getenv("ORCA_HIP_SIDE_BPC");
+    if (sb) m->side_bpc = std::atoi(sb);
+    if (m->side && opt->kind == 1 && !m->use_graph && !(da && da[0] == '0')) {
+      m->P_next = m->dev(o);
+      launch_fill(ctx, m->P_next, 0.0f, o);
+      ORCA_HIP_CHECK(hipEventCreateWithFlags(&m->mid, hipEventDisableTiming));
+      const char* sf = std::getenv("ORCA_HIP_SIDE_FRAC");
+      const double frac = sf ? std::atof(sf) / 100.0 : 0.7;
+      const size_t span = o - m->off[2];
+      m->side_a = std::min(span, (size_t)(frac * (double)span) / 64 * 64);
+    }
     ORCA_HIP_CHECK(hipStreamSynchronize(ctx->stream));
     *out = m.release();
   });

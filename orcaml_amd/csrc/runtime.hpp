@@ -247,10 +247,12 @@ AdamWScalars adamw_scalars(double lr, double b1, double b2, double eps, double w
 void adamw_store_scalars(orca_hip_ctx* ctx, AdamWScalars* dst, const AdamWScalars& s, hipStream_t stream);
 
 // Optimizer passes over flat buffers, on `stream` (the context stream when null).
-// adamw: the scalars come from (lr, ..., t), or from device memory when dev_scalars is set.
+// adamw: the scalars come from (lr, ..., t), or from device memory when dev_scalars is set;
+// the parameters are read from p_src when it is set (and written to p), else updated in place;
+// blocks_per_cu > 0 bounds the grid to that many blocks per CU (an update beside a GEMM).
 void adamw(orca_hip_ctx* ctx, float* p, const float* g, float* m, float* v, size_t n, double lr, double b1,
            double b2, double eps, double wd, int64_t t, hipStream_t stream = nullptr,
-           const AdamWScalars* dev_scalars = nullptr);
+           const AdamWScalars* dev_scalars = nullptr, const float* p_src = nullptr, int blocks_per_cu = 0);
 void sgd(orca_hip_ctx* ctx, float* p, const float* g, size_t n, double lr, hipStream_t stream = nullptr);
 
 }  // namespace orca_hip

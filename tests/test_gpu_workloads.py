@@ -208,6 +208,29 @@ def test_mlp784_4096_b1024_one_adamw_step(ctx):
     assert abs(correct - ref["correct"]) <= int(ties.sum())
 
 
+def test_mlp784_4096_b1024_second_arena_changes_no_bit(ctx, monkeypatch):
+    """784-4096-4096-10, batch 1024, three AdamW steps: with the second parameter arena (the
+    update of layers >= 1 beside layer 1's dZ product, P and P_next swapping every step) every
+    parameter, moment-driven update and gradient equals the single-arena schedule bit for bit."""
+    w = synth.WORKLOADS[synth.MLP_LARGE]
+    params, x, labels, onehot = synth.mlp_problem(w["seed"], w["dims"], w["batch"])
+    out = []
+    for double in ("1", "0"):
+        monkeypatch.setenv("ORCA_HIP_DOUBLE_ARENA", double)
+        tr = make_trainer(ctx, w, params)
+        tr.set_batch(x, onehot=onehot)
+        losses = []
+        for _ in range(3):
+            tr.step()
+            losses.append(tr.metrics()[0])
+        out.append((losses, tr.params(), tr.grads()))
+        tr.close()
+    (l1, p1, g1), (l2, p2, g2) = out
+    assert l1 == l2
+    for a, b in zip(p1 + g1, p2 + g2):
+        np.testing.assert_array_equal(a, b)
+
+
 def test_mlp784_4096_b1024_layerwise_on_shared_inputs(ctx):
     """Each layer of the fused step against the oracle's ops fed the GPU's own
     inputs to that layer (so ReLU masks are identical): forward activations,
