@@ -503,7 +503,9 @@ void adamw(orca_hip_ctx* ctx, float* p, const float* g, float* m, float* v, size
   if (n == 0) return;
   if (!p_src) p_src = p;
   const AdamWScalars k = dev_scalars ? AdamWScalars{} : adamw_scalars(lr, b1, b2, eps, wd, t);
-  ProfScope ps(ctx, "adamw", 0.0, 28.0 * (double)n, stream);
+  // Launches on another stream than the context's run beside other work: their
+  // device time is reported under a name of its own.
+  ProfScope ps(ctx, stream == ctx->stream ? "adamw" : "adamw_overlapped", 0.0, 28.0 * (double)n, stream);
   size_t done = 0;
   if (aligned16(p) && aligned16(p_src) && aligned16(g) && aligned16(m) && aligned16(v)) {
     size_t n4 = n / 4;
@@ -548,7 +550,7 @@ void sgd(orca_hip_ctx* ctx, float* p, const float* g, size_t n, double lr, hipSt
   if (!stream) stream = ctx->stream;
   if (n == 0) return;
   const float flr = (float)lr;
-  ProfScope ps(ctx, "sgd", 0.0, 12.0 * (double)n, stream);
+  ProfScope ps(ctx, stream == ctx->stream ? "sgd" : "sgd_overlapped", 0.0, 12.0 * (double)n, stream);
   size_t done = 0;
   if (aligned16(p) && aligned16(g)) {
     size_t n4 = n / 4;
