@@ -110,10 +110,11 @@ def make_trainer(ctx, wl):
     return MLPTrainer(ctx, w["dims"], w["batch"], kind=o["kind"], lr=o["lr"], weight_decay=o.get("weight_decay", 0.0))
 
 
-@pytest.mark.parametrize("workload", [synth.MLP_SMALL, synth.MLP_MEDIUM])
+@pytest.mark.parametrize("workload", [synth.MLP_SMALL, synth.MLP_MEDIUM, synth.MLP_LARGE])
 def test_trainer_checkpoint_resume_matches_uninterrupted(ctx, tmp_path, workload):
     """3 steps, save, load into a fresh trainer, 2 more steps: the same
-    parameters, moments, step count and metrics as 5 uninterrupted steps."""
+    parameters, moments, step count and metrics as 5 uninterrupted steps
+    (784-4096-4096-10 runs with two parameter arenas that swap each step)."""
     w = synth.WORKLOADS[workload]
     params, x, labels, onehot = synth.mlp_problem(w["seed"], w["dims"], w["batch"])
     a = make_trainer(ctx, workload)
