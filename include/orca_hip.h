@@ -299,8 +299,9 @@ int orca_hip_mlp_set_step_count(orca_hip_mlp* mlp, int64_t t);
 /* ===================== kernel timing ===================== */
 /* When enabled, each GEMM / fused-kernel launch is bracketed by HIP events on
  * the context stream.  The report is a JSON object
- * {"kernels": [{"name", "launches", "total_ms", "flops", "bytes"}...]} with the
- * algorithmic flops / bytes of the launches (synchronises). */
+ * {"num_cus": n, "kernels": [{"name", "launches", "total_ms", "flops", "bytes"}...]}
+ * with the algorithmic flops / bytes of the launches and the device's compute-unit
+ * count, which sizes the GEMM grids and K splits (synchronises). */
 int orca_hip_prof_enable(orca_hip_ctx* ctx, int enable);
 int orca_hip_prof_reset(orca_hip_ctx* ctx);
 int orca_hip_prof_report(orca_hip_ctx* ctx, char* buf, size_t len);

@@ -553,6 +553,41 @@ __global__ void splitk_reduce_kernel(SplitReduceParams p, size_t total) {
   }
 }
 
+// The same sums four columns at a time: N, ldc, sc and ldmask are multiples of
+// 4 and C, the partials and the mask are 16-byte aligned; total4 < 2^31 so the
+// float4 index and its row / column split stay 32-bit.  Each float4 component
+// takes exactly the scalar kernel's adds, in the same split order.
+__global__ void splitk_reduce_vec_kernel(SplitReduceParams p, uint32_t total4) {
+  const uint32_t n4 = (uint32_t)p.N >> 2, mn4 = (uint32_t)p.M * n4;
+  const size_t mn = (size_t)p.M * p.N;
+  const uint32_t stride = gridDim.x * blockDim.x;
+  for (uint32_t idx = blockIdx.x * blockDim.x + threadIdx.x; idx < total4; idx += stride) {
+    const uint32_t b = idx / mn4, rem4 = idx - b * mn4;
+    const uint32_t row = rem4 / n4, col = (rem4 - row * n4) * 4;
+    const float* w = p.ws + b * p.splits * mn + (size_t)rem4 * 4;
+    floatx4 v = *reinterpret_cast<const floatx4*>(w);
+#pragma unroll 4
+    for (int s = 1; s < p.splits; ++s) v = v + *reinterpret_cast<const floatx4*>(w + s * mn);
+    if (p.epi == ORCA_HIP_EPI_BIAS || p.epi == ORCA_HIP_EPI_BIAS_RELU) {
+      const floatx4 bv = {p.bias[col], p.bias[col + 1], p.bias[col + 2], p.bias[col + 3]};
+      v = v + bv;
+      if (p.epi == ORCA_HIP_EPI_BIAS_RELU) {
+        v.x = v.x > 0.0f ? v.x : 0.0f;
+        v.y = v.y > 0.0f ? v.y : 0.0f;
+        v.z = v.z > 0.0f ? v.z : 0.0f;
+        v.w = v.w > 0.0f ? v.w : 0.0f;
+      }
+    } else if (p.epi == ORCA_HIP_EPI_RELU_MASK) {
+      const floatx4 m = *reinterpret_cast<const floatx4*>(p.mask + (int64_t)row * p.ldmask + col);
+      v.x = m.x > 0.0f ? v.x : 0.0f;
+      v.y = m.y > 0.0f ? v.y : 0.0f;
+      v.z = m.z > 0.0f ? v.z : 0.0f;
+      v.w = m.w > 0.0f ? v.w : 0.0f;
+    }
+    *reinterpret_cast<floatx4*>(p.C + b * p.sc + (int64_t)row * p.ldc + col) = v;
+  }
+}
+
 // colsum[n] = sum over K-chunks, in chunk order, of the per-chunk column sums.
 __global__ void colsum_split_reduce_kernel(const float* __restrict__ part, int splits, int N, float* __restrict__ out) {
   int n = blockIdx.x * blockDim.x + threadIdx.x;
@@ -613,10 +648,12 @@ GemmPlan plan_gemm(orca_hip_ctx* ctx, bool trans_a, bool trans_b, size_t M, size
   g.BN = (size_t)bn;
   g.mt = (M + BM - 1) / BM;
   g.nt = (N + g.BN - 1) / g.BN;
-  // Split K when the tile grid cannot fill the CUs and K is long enough.
+  // Split K when the tile grid leaves at least half the CUs idle and K is long
+  // enough (a grid of exactly half the CUs halves its time with two chunks;
+  // between half and all of them a split would not shorten the longest CU).
   g.splits = 1;
   const size_t tiles = g.mt * g.nt * batch;
-  if (tiles < target / 2 && K >= 4 * (size_t)BK) {
+  if (tiles <= target / 2 && K >= 4 * (size_t)BK) {
     size_t want = (target + tiles - 1) / tiles;
     size_t max_by_k = K / (2 * BK);
     g.splits = (int)std::min<size_t>(std::min<size_t>(want, max_by_k), 64);
@@ -767,8 +804,16 @@ void gemm(orca_hip_ctx* ctx, bool trans_a, bool trans_b, size_t M, size_t N, siz
     r.ldmask = (int64_t)epi.ldmask;
     size_t total = batch * M * N;
     ProfScope ps(ctx, "gemm_splitk_reduce", 0.0, 4.0 * (double)total * (splits + 1));
-    unsigned g = grid_for(total, 256, ctx->num_cus * 8);
-    hipLaunchKernelGGL(splitk_reduce_kernel, dim3(g), dim3(256), 0, ctx->stream, r, total);
+    const bool vec = N % 4 == 0 && ldc % 4 == 0 && (batch == 1 || sc % 4 == 0) && aligned16(C) && aligned16(r.ws) &&
+                     (epi.kind != ORCA_HIP_EPI_RELU_MASK || (aligned16(epi.mask) && epi.ldmask % 4 == 0)) &&
+                     total / 4 < (size_t)INT32_MAX;
+    if (vec) {
+      unsigned g = grid_for(total / 4, 256, ctx->num_cus * 8);
+      hipLaunchKernelGGL(splitk_reduce_vec_kernel, dim3(g), dim3(256), 0, ctx->stream, r, (uint32_t)(total / 4));
+    } else {
+      unsigned g = grid_for(total, 256, ctx->num_cus * 8);
+      hipLaunchKernelGGL(splitk_reduce_kernel, dim3(g), dim3(256), 0, ctx->stream, r, total);
+    }
     ORCA_HIP_CHECK(hipGetLastError());
   }
   if (fold_colsum && splits > 1) {

@@ -368,7 +368,7 @@ int orca_hip_prof_report(orca_hip_ctx* ctx, char* buf, size_t len) {
     ORCA_HIP_CHECK(hipStreamSynchronize(ctx->stream));
     ctx->prof.drain();
     std::ostringstream os;
-    os << "{\"kernels\": [";
+    os << "{\"num_cus\": " << ctx->num_cus << ", \"kernels\": [";
     bool first = true;
     for (auto& kv : ctx->prof.agg) {
       os << (first ? "" : ", ") << "{\"name\": \"" << kv.first << "\", \"launches\": " << kv.second.launches

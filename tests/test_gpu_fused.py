@@ -59,7 +59,9 @@ GEMM_SHAPES = [
     (64, 128, 784), (784, 384, 1024), (96, 16, 4), (4, 8, 12), (132, 260, 36), (200, 300, 152),
     # pipelined kernel, tile-aligned: 1..5 and 32 slabs, and split-K launches
     (128, 128, 32), (256, 128, 64), (128, 256, 96), (256, 256, 128), (384, 128, 160), (256, 384, 1024),
-    (128, 128, 4096), (128, 256, 3076)]
+    (128, 128, 4096), (128, 256, 3076),
+    # 128 tiles of 128 x 128: half of MI355X's 256 CUs, so K splits in two
+    (1024, 2048, 128)]
 
 
 @pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False), (True, True)])
@@ -99,9 +101,11 @@ def test_gemm_aligned_shapes_take_pipelined_kernel(ctx, ta, tb, colsum):
             np.testing.assert_array_equal(cs, O.sum_to_shape(B, (1, N)).reshape(N))
 
 
-@pytest.mark.parametrize("M,N,K", [(200, 300, 150), (200, 300, 152), (256, 384, 128)])
+@pytest.mark.parametrize("M,N,K", [(200, 300, 150), (200, 300, 152), (256, 384, 128), (128, 256, 1024),
+                                   (130, 70, 1000), (1024, 2048, 128)])
 def test_gemm_epilogues_match_composed_ops(ctx, M, N, K):
-    """Generic kernel (K = 150), pipelined kernel with edge tiles (152) and aligned (128)."""
+    """Generic kernel (K = 150), pipelined kernel with edge tiles (152) and aligned (128); split-K
+    launches whose epilogue runs in the float4 reduce (N = 256, 2048) or the scalar one (N = 70)."""
     rng = np.random.default_rng(5)
     A = rng.standard_normal((M, K)).astype(np.float32)
     B = rng.standard_normal((K, N)).astype(np.float32)
@@ -117,6 +121,23 @@ def test_gemm_epilogues_match_composed_ops(ctx, M, N, K):
     mask[::7, ::3] = 0.0
     got = run_gemm(ctx, False, False, A, B, _lib.EPI_RELU_MASK, mask=mask)
     np.testing.assert_array_equal(got, O.relu_backward(prod, mask))
+
+
+def test_gemm_grid_of_half_the_cus_splits_k(ctx):
+    """A 128 x 128 tile grid that covers exactly half the CUs runs as two K chunks (every CU busy,
+    then the in-order chunk sum); the product stays exact on integers."""
+    cus = ctx.prof_report()["num_cus"]
+    M, N, K = 128, 128 * (cus // 2), 256
+    rng = np.random.default_rng(11)
+    A = int_matrix(rng, (M, K))
+    B = int_matrix(rng, (K, N))
+    ctx.prof_reset()
+    ctx.prof_enable(True)
+    got = run_gemm(ctx, False, False, A, B)
+    ctx.prof_enable(False)
+    names = {k["name"] for k in ctx.prof_report()["kernels"]}
+    assert "gemm_splitk_reduce" in names, names
+    np.testing.assert_array_equal(got, (A.astype(np.int64) @ B.astype(np.int64)).astype(np.float32))
 
 
 @pytest.mark.parametrize("M,N,K,exact", [(128, 256, 64, True), (784, 4096, 1024, True), (4096, 10, 1024, False),
