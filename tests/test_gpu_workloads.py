@@ -144,8 +144,11 @@ def test_mlp784_1024_b256_free_running_within_natural_spread(ctx):
     assert gpu[-1] < 0.05 * gpu[0]  # the fixed batch is memorised
 
 
-def test_mlp784_4096_b1024_one_adamw_step(ctx):
-    """784-4096-4096-10, batch 1024, one AdamW step against the oracle, end to end:
+@pytest.mark.parametrize("batch", [1024, 512])
+def test_mlp784_4096_b1024_one_adamw_step(ctx, batch):
+    """784-4096-4096-10, batch 1024, one AdamW step against the oracle, end to end
+    (and batch 512, where F1, F2 and dX2 each split K in two and sum the chunks
+    in their reduce pass, which also applies the epilogue):
     loss and logits to the path's tolerance (1e-5 abs + 1e-4 rel); gradients and
     updated parameters to that tolerance except for a reported fraction <= 1e-5
     of elements.  Those outliers come from ReLU masks that differ between the
@@ -154,7 +157,7 @@ def test_mlp784_4096_b1024_one_adamw_step(ctx):
     printed, and the shared-input layer-wise test below shows the kernels agree
     when the masks are the same.  Argmax / accuracy are exact outside rows whose
     top-2 margin is within rounding."""
-    w = synth.WORKLOADS[synth.MLP_LARGE]
+    w = dict(synth.WORKLOADS[synth.MLP_LARGE], batch=batch)
     dims = w["dims"]
     params, x, labels, onehot = synth.mlp_problem(w["seed"], dims, w["batch"])
     tr = make_trainer(ctx, w, params)
