@@ -6,6 +6,10 @@ one-hot targets), batch 1024, f32, one forward + backward + AdamW(1e-3, wd
 already resident in HBM.  Prints ONE JSON line (see the keys below).
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--no-secondary]
+                  [--batch B]
+
+--batch measures one GPU's share of the 1024-row batch under data parallelism
+(512, 256, 128 rows); the default is the benchmark workload itself.
 
 `roofline` reports the dominant kernel (largest device time per step; GEMMs
 are told apart by shape): achieved = algorithmic work per launch / mean launch
@@ -90,7 +94,7 @@ def cpu_baseline(params, x, onehot, target_s: float = 8.0) -> dict:
         "sample": f"{steps} full fwd+bwd+AdamW steps of the same workload after 1 warm-up step ({dt:.1f} s wall); "
                   f"C oracle restating orca-backend-cpu (single-threaded packed sgemm as matrixmultiply without "
                   f"threading, OpenMP elementwise ops as rayon), CPU: {cpu_model()}",
-        "samples_per_s": BATCH * steps / dt,
+        "samples_per_s": x.shape[0] * steps / dt,
     }
 
 
@@ -232,6 +236,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=30)  # 5 warm-up steps left the first timed ones ~1 % slower
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true", help="skip the other workloads' measurements")
+    ap.add_argument("--batch", type=int, default=BATCH,
+                    help="rows per step (default 1024, the benchmark workload; 512 / 256 / 128 are one GPU's "
+                         "share of that batch under 2 / 4 / 8-way data parallelism)")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="first run one device-to-device copy of this many MiB (a known-size kernel that "
                          "calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
@@ -245,7 +252,8 @@ def main() -> int:
     from orcaml_amd.device import Context
     from orcaml_amd.mlp import MLPTrainer
 
-    params, x, labels, onehot = synth.mlp_problem(SEED, DIMS, BATCH)
+    batch = args.batch
+    params, x, labels, onehot = synth.mlp_problem(SEED, DIMS, batch)
     ctx = Context(0)
     if args.copy_probe_mib > 0:
         nbytes = args.copy_probe_mib << 20
@@ -255,7 +263,7 @@ def main() -> int:
         ctx.sync()
         src.free()
         dst.free()
-    tr = MLPTrainer(ctx, DIMS, BATCH, kind=OPT["kind"], lr=OPT["lr"], weight_decay=OPT["weight_decay"],
+    tr = MLPTrainer(ctx, DIMS, batch, kind=OPT["kind"], lr=OPT["lr"], weight_decay=OPT["weight_decay"],
                     betas=OPT["betas"], eps=OPT["eps"])
     tr.set_params(params)
     tr.set_batch(x, onehot=onehot)
@@ -318,9 +326,9 @@ def main() -> int:
 
     ms_per_step = wall * 1e3 / args.steps
     steps_per_s = args.steps / wall
-    flops = step_flops(DIMS, BATCH)
+    flops = step_flops(DIMS, batch)
     out = {
-        "metric": "MLP train steps/s (784-4096-4096-10 fp32, B=1024); % fp32 MFMA peak",
+        "metric": f"MLP train steps/s (784-4096-4096-10 fp32, B={batch}); % fp32 MFMA peak",
         "value": steps_per_s,
         "unit": "steps/s",
         "n_gpus": 1,
@@ -332,9 +340,9 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic",
-        "config": {"workload": "mlp_train_step", "dims": list(DIMS), "batch": BATCH, "optimizer": "adamw",
+        "config": {"workload": "mlp_train_step", "dims": list(DIMS), "batch": batch, "optimizer": "adamw",
                    "lr": OPT["lr"], "weight_decay": OPT["weight_decay"], "seed": SEED},
-        "samples_per_s": steps_per_s * BATCH,
+        "samples_per_s": steps_per_s * batch,
         "step_tflops": flops * steps_per_s / 1e12,
         "step_frac_fp32_mfma_peak": flops * steps_per_s / 1e12 / PEAK_FP32_MFMA_TFLOPS,
         "gemm_tflops": gemm_flops / (gemm_ms * 1e-3) / 1e12 if gemm_ms > 0 else None,
