@@ -530,6 +530,8 @@ struct SplitReduceParams {
   const float* bias;
   const float* mask;
   int64_t ldmask;
+  const float* cs_part;  // per-split column sums [splits][N] of a folded bias gradient, or null
+  float* cs_out;         // their in-order sum [N]
 };
 
 __global__ void splitk_reduce_kernel(SplitReduceParams p, size_t total) {
@@ -556,11 +558,20 @@ __global__ void splitk_reduce_kernel(SplitReduceParams p, size_t total) {
 // The same sums four columns at a time: N, ldc, sc and ldmask are multiples of
 // 4 and C, the partials and the mask are 16-byte aligned; total4 < 2^31 so the
 // float4 index and its row / column split stay 32-bit.  Each float4 component
-// takes exactly the scalar kernel's adds, in the same split order.
+// takes exactly the scalar kernel's adds, in the same split order.  With a
+// folded bias gradient the first N threads also sum its per-split column sums
+// in split order (what colsum_split_reduce_kernel does, without its launch).
 __global__ void splitk_reduce_vec_kernel(SplitReduceParams p, uint32_t total4) {
   const uint32_t n4 = (uint32_t)p.N >> 2, mn4 = (uint32_t)p.M * n4;
   const size_t mn = (size_t)p.M * p.N;
   const uint32_t stride = gridDim.x * blockDim.x;
+  if (p.cs_part) {
+    for (uint32_t n = blockIdx.x * blockDim.x + threadIdx.x; n < (uint32_t)p.N; n += stride) {
+      float v = p.cs_part[n];
+      for (int s = 1; s < p.splits; ++s) v = v + p.cs_part[(size_t)s * p.N + n];
+      p.cs_out[n] = v;
+    }
+  }
   for (uint32_t idx = blockIdx.x * blockDim.x + threadIdx.x; idx < total4; idx += stride) {
     const uint32_t b = idx / mn4, rem4 = idx - b * mn4;
     const uint32_t row = rem4 / n4, col = (rem4 - row * n4) * 4;
@@ -789,6 +800,7 @@ void gemm(orca_hip_ctx* ctx, bool trans_a, bool trans_b, size_t M, size_t N, siz
 #undef GEMM_LAUNCH
     ORCA_HIP_CHECK(hipGetLastError());
   }
+  bool colsum_reduced = false;
   if (splits > 1) {
     SplitReduceParams r{};
     r.ws = p.C;
@@ -808,6 +820,11 @@ void gemm(orca_hip_ctx* ctx, bool trans_a, bool trans_b, size_t M, size_t N, siz
                      (epi.kind != ORCA_HIP_EPI_RELU_MASK || (aligned16(epi.mask) && epi.ldmask % 4 == 0)) &&
                      total / 4 < (size_t)INT32_MAX;
     if (vec) {
+      if (fold_colsum) {
+        r.cs_part = p.colsum;
+        r.cs_out = epi.colsum;
+        colsum_reduced = true;
+      }
       unsigned g = grid_for(total / 4, 256, ctx->num_cus * 8);
       hipLaunchKernelGGL(splitk_reduce_vec_kernel, dim3(g), dim3(256), 0, ctx->stream, r, (uint32_t)(total / 4));
     } else {
@@ -816,7 +833,7 @@ void gemm(orca_hip_ctx* ctx, bool trans_a, bool trans_b, size_t M, size_t N, siz
     }
     ORCA_HIP_CHECK(hipGetLastError());
   }
-  if (fold_colsum && splits > 1) {
+  if (fold_colsum && splits > 1 && !colsum_reduced) {
     hipLaunchKernelGGL(colsum_split_reduce_kernel, dim3((unsigned)((N + 255) / 256)), dim3(256), 0, ctx->stream,
                        p.colsum, splits, (int)N, epi.colsum);
     ORCA_HIP_CHECK(hipGetLastError());
