@@ -784,8 +784,11 @@ void gemm(orca_hip_ctx* ctx, bool trans_a, bool trans_b, size_t M, size_t N, siz
 #define FAST_LAUNCH(TA_, TB_, CS_) \
   hipLaunchKernelGGL((gemm_mfma_f32_fast_kernel<TA_, TB_, CS_>), grid, dim3(NTHREADS), 0, ctx->stream, p)
     if (fast) {
+      // The column sum reads only B's LDS tile (row-major B), so it folds in
+      // whatever A's layout is.
       const bool cs = p.colsum != nullptr;
-      if (!trans_a && !trans_b) FAST_LAUNCH(false, false, false);
+      if (!trans_a && !trans_b && cs) FAST_LAUNCH(false, false, true);
+      else if (!trans_a && !trans_b) FAST_LAUNCH(false, false, false);
       else if (!trans_a && trans_b) FAST_LAUNCH(false, true, false);
       else if (trans_a && !trans_b && cs) FAST_LAUNCH(true, false, true);
       else if (trans_a && !trans_b) FAST_LAUNCH(true, false, false);

@@ -75,8 +75,8 @@ def test_gemm_exact_on_integers(ctx, ta, tb, M, N, K):
     np.testing.assert_array_equal(got, want)
 
 
-@pytest.mark.parametrize("ta,tb,colsum", [(False, False, False), (False, True, False), (True, False, True),
-                                          (True, False, False), (True, True, False)])
+@pytest.mark.parametrize("ta,tb,colsum", [(False, False, False), (False, False, True), (False, True, False),
+                                          (True, False, True), (True, False, False), (True, True, False)])
 def test_gemm_aligned_shapes_take_pipelined_kernel(ctx, ta, tb, colsum):
     """Products whose M, N, K are multiples of 4 run on the pipelined 128 x 128
     kernel (profiler name *_pipe), the rest on the generic kernel; both exact

@@ -239,6 +239,7 @@ def test_composed_step_mlp784_128_on_hip(hb, kind, steps):
 
 @pytest.mark.parametrize("M,K,N,view", [(784, 1024, 4096, True), (128, 64, 128, True), (64, 2048, 64, True),
                                         (33, 300, 70, True), (1000, 100, 1030, True), (96, 256, 160, False),
+                                        (784, 64, 128, False), (64, 64, 128, False), (130, 72, 70, False),
                                         (0, 16, 8, True), (8, 0, 12, True)])
 def test_matmul_colsum_equals_matmul_and_sum_to_shape(hb, M, K, N, view):
     """orca_hip_matmul_colsum (via a pending sum_to_shape consumed by matmul): the product bit

@@ -193,3 +193,118 @@ def test_synth_generator_fixed_values():
     # chunked generation (used for 2^28-element buffers) reproduces the flat stream
     np.testing.assert_array_equal(synth.normal_range(5, 1, 1024, 2048, 0.0, 0.02),
                                   synth.normal(5, 1, (4096,), 0.0, 0.02)[1024:3072])
+
+
+# ---- independent pins of the functions the MLP step does not exercise ----------
+# Each check below is chosen so that a plausible slip in the restatement (a sign,
+# a dropped factor, a swapped operand, a wrong comparison) fails it; none of them
+# re-types the oracle's own expression.
+
+def _ulps(got: np.ndarray, want64: np.ndarray) -> np.ndarray:
+    """|got - want| in units of the f32 spacing at want."""
+    want32 = want64.astype(np.float32)
+    spacing = np.spacing(np.abs(want32)).astype(np.float64)
+    return np.abs(got.astype(np.float64) - want64) / spacing
+
+
+def test_argmax_rows_first_maximum_and_nan():
+    """python/orca/nn/model.py:65-75: first maximum on strict `>`.  NaN-free rows with planted
+    ties agree with np.argmax (which also returns the first maximum); a NaN in column 0 wins
+    (nothing compares greater than it); a NaN later is never taken (np.nanargmax)."""
+    rng = np.random.default_rng(21)
+    x = rng.integers(-3, 4, (400, 10)).astype(np.float32)  # many ties among 7 values
+    x[5] = 2.0                                              # all equal -> 0
+    x[6] = -np.inf                                          # all -inf -> 0
+    x[7, 9] = np.inf
+    np.testing.assert_array_equal(O.argmax_rows(x), np.argmax(x, axis=1))
+    y = rng.standard_normal((300, 7)).astype(np.float32)
+    y[:100, 0] = np.nan
+    np.testing.assert_array_equal(O.argmax_rows(y[:100]), np.zeros(100, np.int32))
+    cols = rng.integers(1, 7, 200)
+    y[100 + np.arange(200), cols] = np.nan
+    np.testing.assert_array_equal(O.argmax_rows(y[100:]), np.nanargmax(y[100:], axis=1))
+    assert O.argmax_rows(np.array([[3.0]], np.float32)).tolist() == [0]
+
+
+def test_sigmoid_against_fp64_and_limits():
+    """backend.rs:392-412 in f32: sigmoid(0) = 0.5 exactly, within 3 ulp of the fp64 logistic
+    over [-30, 30] (expf's error below 1 ulp, then one rounding each for the add and the
+    division; measured 2.2 ulp at worst), monotone, sigmoid(x) + sigmoid(-x) = 1 to rounding, and the f32 limits
+    (exp overflows to inf below -88.7, so the result is exactly 0; above 17 it rounds to 1)."""
+    assert O.sigmoid(np.zeros(3, np.float32)).tolist() == [0.5, 0.5, 0.5]
+    x = np.linspace(-30, 30, 200001, dtype=np.float32)
+    got = O.sigmoid(x)
+    want = 1.0 / (1.0 + np.exp(-x.astype(np.float64)))
+    assert _ulps(got, want).max() <= 3.0
+    assert (np.diff(got) >= 0).all()
+    np.testing.assert_allclose(got.astype(np.float64) + O.sigmoid(-x), 1.0, atol=2 ** -23)
+    assert (O.sigmoid(np.array([-89.0, -1e4, -np.inf], np.float32)) == 0.0).all()
+    assert (O.sigmoid(np.array([17.0, 1e4, np.inf], np.float32)) == 1.0).all()
+    assert np.isnan(O.sigmoid(np.array([np.nan], np.float32))[0])
+
+
+def test_sigmoid_backward_exact_on_dyadic_values():
+    """backend.rs:440-464: g * y * (1 - y).  With y = k/64 and g a small integer over 8 every
+    intermediate fits in f32 exactly, so the result must equal the fp64 value bit for bit."""
+    k = np.arange(0, 65, dtype=np.float64)
+    y = np.tile(k / 64.0, 31)
+    g = np.repeat(np.arange(-15, 16, dtype=np.float64) / 8.0, 65)
+    got = O.sigmoid_backward(g.astype(np.float32), y.astype(np.float32))
+    np.testing.assert_array_equal(got, (g * y * (1.0 - y)).astype(np.float32))
+    # the derivative of the logistic at x is s(x)(1 - s(x)): a central difference in fp64
+    x = np.linspace(-6, 6, 97)
+    s = lambda t: 1.0 / (1.0 + np.exp(-t))  # noqa: E731
+    h = 1e-6
+    fd = (s(x + h) - s(x - h)) / (2 * h)
+    got = O.sigmoid_backward(np.ones_like(x, np.float32), s(x).astype(np.float32))
+    # y is rounded to f32 first (absolute error up to 6e-8 near 1, which 1 - y keeps)
+    np.testing.assert_allclose(got, fd, rtol=2e-6, atol=1e-7)
+
+
+def test_sqrt_backward_is_the_derivative_of_sqrt():
+    """backend.rs:734-759: with y = sqrt(x) stored, d sqrt(x)/dx = 1 / (2 y); checked against an
+    fp64 central difference of sqrt, scaled by the incoming gradient."""
+    rng = np.random.default_rng(22)
+    x = rng.uniform(0.01, 100.0, 5000)
+    g = rng.standard_normal(5000)
+    y = np.sqrt(x).astype(np.float32)
+    h = 1e-6 * x
+    fd = (np.sqrt(x + h) - np.sqrt(x - h)) / (2 * h)
+    got = O.sqrt_backward(g.astype(np.float32), y)
+    np.testing.assert_allclose(got, g * fd, rtol=1e-5, atol=1e-12)
+
+
+def test_div_backward_are_the_partial_derivatives_of_a_quotient():
+    """backend.rs:678-732: d(l/r)/dl = 1/r and d(l/r)/dr = -l/r^2, each times the incoming
+    gradient; checked against fp64 central differences of l/r in each operand."""
+    rng = np.random.default_rng(23)
+    l = rng.uniform(-10, 10, 5000)
+    r = rng.uniform(0.5, 10, 5000) * rng.choice([-1.0, 1.0], 5000)
+    g = rng.standard_normal(5000)
+    l32, r32, g32 = (v.astype(np.float32) for v in (l, r, g))
+    l, r, g = (v.astype(np.float64) for v in (l32, r32, g32))
+    h = 1e-6
+    fd_l = ((l + h) / r - (l - h) / r) / (2 * h)
+    fd_r = (l / (r + h) - l / (r - h)) / (2 * h)
+    np.testing.assert_allclose(O.div_backward_lhs(g32, r32), g * fd_l, rtol=1e-5, atol=1e-9)
+    np.testing.assert_allclose(O.div_backward_rhs(g32, l32, r32), g * fd_r, rtol=1e-4, atol=1e-8)
+
+
+def test_has_nan_or_inf_matches_isfinite():
+    """backend.rs:1319-1334: true exactly when some element is NaN or +-inf.  FLT_MAX,
+    denormals and -0 are finite; a single bad value at the first or last position counts."""
+    rng = np.random.default_rng(24)
+    fmax = np.finfo(np.float32).max
+    finite_specials = np.array([fmax, -fmax, 1e-45, -1e-45, -0.0, 0.0], np.float32)
+    assert not O.has_nan_or_inf(finite_specials)
+    assert not O.has_nan_or_inf(np.zeros(0, np.float32))
+    for bad in (np.nan, np.inf, -np.inf):
+        for pos in (0, 999, 517):
+            a = rng.standard_normal(1000).astype(np.float32)
+            a[pos] = bad
+            assert O.has_nan_or_inf(a) == (not np.isfinite(a).all()) == True  # noqa: E712
+    for _ in range(50):
+        a = rng.standard_normal(257).astype(np.float32)
+        if rng.random() < 0.5:
+            a[rng.integers(0, 257)] = rng.choice([np.nan, np.inf, -np.inf, fmax])
+        assert O.has_nan_or_inf(a) == (not np.isfinite(a).all())
