@@ -88,6 +88,11 @@ int orca_hip_d2h(orca_hip_ctx* ctx, void* dst, const void* src, size_t bytes); /
 int orca_hip_d2d(orca_hip_ctx* ctx, void* dst, const void* src, size_t bytes); /* stream-ordered */
 int orca_hip_fill(orca_hip_ctx* ctx, float* dst, float value, size_t n);       /* stream-ordered kernel */
 int orca_hip_sync(orca_hip_ctx* ctx);
+/* Number of host waits on this context's work so far (every stream or event
+ * synchronisation the library performed, including the host-reading calls).
+ * No counterpart in the reference: it lets a caller check that a span of calls,
+ * such as a backward pass and an optimizer step, never waited for the device. */
+int orca_hip_sync_count(const orca_hip_ctx* ctx, uint64_t* count);
 
 /* =========================== Backend trait ops =========================== */
 /* `shape`/`rank` are the logical shape (Shape, orca-core/src/shape.rs:6).
@@ -95,12 +100,15 @@ int orca_hip_sync(orca_hip_ctx* ctx);
 
 /* Backend::zeros (backend.rs:27) */
 int orca_hip_zeros(orca_hip_ctx* ctx, const size_t* shape, size_t rank, int dtype, void** out);
-/* Backend::from_f32_slice (backend.rs:30-31); n must equal the shape's elements */
+/* Backend::from_f32_slice (backend.rs:30-31); n must equal the shape's elements.
+ * Stream-ordered without a host wait: up to 1 KiB travels as a kernel argument,
+ * more through the context's pinned staging ring; `data` may be reused on return. */
 int orca_hip_from_f32_slice(orca_hip_ctx* ctx, const size_t* shape, size_t rank, const float* data,
                             size_t n, void** out);
 /* Backend::to_f32_vec (backend.rs:34): copies n floats to host (synchronises) */
 int orca_hip_to_f32_vec(orca_hip_ctx* ctx, const void* storage, size_t n, float* host_out);
-/* Backend::from_bytes / to_bytes (backend.rs:296-297), f32 payload */
+/* Backend::from_bytes / to_bytes (backend.rs:296-297), f32 payload; from_bytes
+ * uploads like from_f32_slice (no host wait), to_bytes synchronises. */
 int orca_hip_from_bytes(orca_hip_ctx* ctx, const size_t* shape, size_t rank, const uint8_t* bytes,
                         size_t n_bytes, int dtype, void** out);
 int orca_hip_to_bytes(orca_hip_ctx* ctx, const void* storage, size_t n_bytes, uint8_t* host_out);

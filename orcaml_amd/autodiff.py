@@ -783,10 +783,16 @@ class AdamW(Optimizer):
         self.v = [Tensor.zeros(p.tensor.ad, p.tensor.shape) for p in self.parameters]
 
     def state_dict(self) -> dict:
-        """{"m.<i>": Tensor, "v.<i>": Tensor, "t": int} for parameter i in optimizer order."""
+        """{"m.<i>": Tensor, "v.<i>": Tensor, "t": int} for parameter i in optimizer order.
+        With fused=True the moments are updated in place by later steps, so the
+        returned tensors are copies: a snapshot stays what it was when taken."""
         out = {"t": self.t}
         for i in range(len(self.parameters)):
-            out[f"m.{i}"], out[f"v.{i}"] = self.m[i], self.v[i]
+            m, v = self.m[i], self.v[i]
+            if self.fused and hasattr(m.ad.inner, "clone"):
+                m = Tensor(m.ad, AdStorage(m.ad.inner.clone(m.storage.primal)), m.shape)
+                v = Tensor(v.ad, AdStorage(v.ad.inner.clone(v.storage.primal)), v.shape)
+            out[f"m.{i}"], out[f"v.{i}"] = m, v
         return out
 
     def load_state_dict(self, state: dict) -> None:

@@ -610,12 +610,6 @@ __global__ void colsum_split_reduce_kernel(const float* __restrict__ part, int s
 
 inline bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; }
 
-// ORCA_HIP_GEMM_FAST=0 sends every product through the generic kernel (tuning / A-B runs).
-bool fast_env_off() {
-  static const char* v = std::getenv("ORCA_HIP_GEMM_FAST");
-  return v && v[0] == '0';
-}
-
 // Profiler names: "gemm_<op(A)><op(B)>", "_pipe" for the pipelined 128 x 128 kernel.
 const char* kernel_name(bool ta, bool tb, bool pipelined) {
   static const char* names[2][4] = {{"gemm_nn", "gemm_nt", "gemm_tn", "gemm_tt"},
@@ -644,16 +638,13 @@ GemmPlan plan_gemm(orca_hip_ctx* ctx, bool trans_a, bool trans_b, size_t M, size
   // within one operand.
   const size_t a_rows = trans_a ? K : M, b_rows = trans_b ? N : K;
   g.fast = M % 4 == 0 && N % 4 == 0 && K % 4 == 0 && vec_a && vec_b && a_rows * lda * 4 < 0xffffffffull &&
-           b_rows * ldb * 4 < 0xffffffffull && !fast_env_off();
+           b_rows * ldb * 4 < 0xffffffffull && !ctx->gemm_generic_only;
   // Generic kernel tile: 128 x 128 when that gives every CU a block, else
-  // 128 x 64 (twice the blocks).  ORCA_HIP_GEMM_TILE=128x128|128x64 overrides
-  // the generic kernel's choice (tuning).
+  // 128 x 64 (twice the blocks), unless the context fixes it (tuning).
   const size_t target = (size_t)ctx->num_cus;
   const size_t t128 = ((M + 127) / 128) * ((N + 127) / 128) * batch;
   int bn = t128 >= target ? 128 : 64;
-  static const char* tile_env = std::getenv("ORCA_HIP_GEMM_TILE");
-  if (tile_env && std::string(tile_env) == "128x128") bn = 128;
-  if (tile_env && std::string(tile_env) == "128x64") bn = 64;
+  if (ctx->gemm_tile_bn) bn = ctx->gemm_tile_bn;
   if (g.fast) bn = 128;
   const size_t BM = 128;
   g.BN = (size_t)bn;

@@ -382,7 +382,7 @@ int orca_hip_mlp_create(orca_hip_ctx* ctx, const size_t* dims, size_t n_layers, 
       const size_t span = o - m->off[2];
       m->side_a = std::min(span, (size_t)(frac * (double)span) / 64 * 64);
     }
-    ORCA_HIP_CHECK(hipStreamSynchronize(ctx->stream));
+    host_sync(ctx);
     *out = m.release();
   });
 }
@@ -391,7 +391,7 @@ int orca_hip_mlp_destroy(orca_hip_mlp* mlp) {
   return guard([&] {
     if (!mlp) return;
     bind(mlp->ctx);
-    ORCA_HIP_CHECK(hipStreamSynchronize(mlp->ctx->stream));
+    host_sync(mlp->ctx);
     delete mlp;
   });
 }
@@ -410,7 +410,7 @@ int orca_hip_mlp_set_param(orca_hip_mlp* mlp, size_t index, const float* host, s
     check_index(mlp, index, n);
     ORCA_HIP_CHECK(hipMemcpyAsync(mlp->P + mlp->off[index], host, n * sizeof(float), hipMemcpyHostToDevice,
                                   mlp->ctx->stream));
-    ORCA_HIP_CHECK(hipStreamSynchronize(mlp->ctx->stream));
+    host_sync(mlp->ctx);
   });
 }
 
@@ -421,7 +421,7 @@ static int read_arena(orca_hip_mlp* mlp, const float* arena, size_t index, float
     if (!arena) fail(ORCA_HIP_ERR_INTERNAL, "state not present for this optimizer");
     ORCA_HIP_CHECK(hipMemcpyAsync(host, arena + mlp->off[index], n * sizeof(float), hipMemcpyDeviceToHost,
                                   mlp->ctx->stream));
-    ORCA_HIP_CHECK(hipStreamSynchronize(mlp->ctx->stream));
+    host_sync(mlp->ctx);
   });
 }
 
@@ -448,7 +448,7 @@ int orca_hip_mlp_set_moment(orca_hip_mlp* mlp, int which, size_t index, const fl
     if (!arena) fail(ORCA_HIP_ERR_INTERNAL, "state not present for this optimizer");
     ORCA_HIP_CHECK(hipMemcpyAsync(arena + mlp->off[index], host, n * sizeof(float), hipMemcpyHostToDevice,
                                   mlp->ctx->stream));
-    ORCA_HIP_CHECK(hipStreamSynchronize(mlp->ctx->stream));
+    host_sync(mlp->ctx);
   });
 }
 
@@ -475,7 +475,7 @@ int orca_hip_mlp_set_batch(orca_hip_mlp* mlp, const float* x, const float* oneho
         mlp->onehot = nullptr;
       }
     }
-    ORCA_HIP_CHECK(hipStreamSynchronize(s));
+    host_sync(mlp->ctx, s);
     mlp->have_batch = true;
   });
 }
@@ -502,7 +502,7 @@ int orca_hip_mlp_read_metrics(orca_hip_mlp* mlp, float* loss, int64_t* correct) 
     hipStream_t s = mlp->ctx->stream;
     if (loss) ORCA_HIP_CHECK(hipMemcpyAsync(loss, mlp->loss, sizeof(float), hipMemcpyDeviceToHost, s));
     if (correct) ORCA_HIP_CHECK(hipMemcpyAsync(correct, mlp->correct, sizeof(int64_t), hipMemcpyDeviceToHost, s));
-    ORCA_HIP_CHECK(hipStreamSynchronize(s));
+    host_sync(mlp->ctx, s);
   });
 }
 
@@ -512,7 +512,7 @@ int orca_hip_mlp_get_logits(orca_hip_mlp* mlp, float* host, size_t n) {
     size_t want = mlp->B * mlp->dims[mlp->L];
     if (n != want) fail(ORCA_HIP_ERR_SHAPE, "Shape mismatch during mlp_get_logits: expected " + std::to_string(want));
     ORCA_HIP_CHECK(hipMemcpyAsync(host, mlp->logits, n * sizeof(float), hipMemcpyDeviceToHost, mlp->ctx->stream));
-    ORCA_HIP_CHECK(hipStreamSynchronize(mlp->ctx->stream));
+    host_sync(mlp->ctx);
   });
 }
 
@@ -521,7 +521,7 @@ int orca_hip_mlp_get_preds(orca_hip_mlp* mlp, int32_t* host, size_t n) {
     checked(mlp);
     if (n != mlp->B) fail(ORCA_HIP_ERR_SHAPE, "Shape mismatch during mlp_get_preds: expected " + std::to_string(mlp->B));
     ORCA_HIP_CHECK(hipMemcpyAsync(host, mlp->preds, n * sizeof(int32_t), hipMemcpyDeviceToHost, mlp->ctx->stream));
-    ORCA_HIP_CHECK(hipStreamSynchronize(mlp->ctx->stream));
+    host_sync(mlp->ctx);
   });
 }
 
@@ -533,7 +533,7 @@ int orca_hip_mlp_get_activation(orca_hip_mlp* mlp, size_t layer, float* host, si
     if (n != want) fail(ORCA_HIP_ERR_SHAPE, "Shape mismatch during mlp_get_activation: expected " + std::to_string(want));
     const float* src = layer + 1 < mlp->L ? mlp->H[layer] : mlp->logits;
     ORCA_HIP_CHECK(hipMemcpyAsync(host, src, n * sizeof(float), hipMemcpyDeviceToHost, mlp->ctx->stream));
-    ORCA_HIP_CHECK(hipStreamSynchronize(mlp->ctx->stream));
+    host_sync(mlp->ctx);
   });
 }
 

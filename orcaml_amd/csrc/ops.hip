@@ -629,10 +629,7 @@ int orca_hip_from_f32_slice(orca_hip_ctx* ctx, const size_t* shape, size_t rank,
       fail(ORCA_HIP_ERR_SHAPE, "Shape mismatch during from_f32_slice: expected " + std::to_string(want) +
                                    " elements, got " + std::to_string(n));
     float* o = new_output(ctx, n);
-    if (n) {
-      ORCA_HIP_CHECK(hipMemcpyAsync(o, data, n * sizeof(float), hipMemcpyHostToDevice, ctx->stream));
-      ORCA_HIP_CHECK(hipStreamSynchronize(ctx->stream));
-    }
+    upload_async(ctx, o, data, n * sizeof(float));  // stream-ordered, no host wait
     *out = o;
   });
 }
@@ -644,7 +641,7 @@ int orca_hip_to_f32_vec(orca_hip_ctx* ctx, const void* s, size_t n, float* host_
     if (!n) return;
     check_extent(ctx, s, n * sizeof(float), "to_f32_vec");
     ORCA_HIP_CHECK(hipMemcpyAsync(host_out, s, n * sizeof(float), hipMemcpyDeviceToHost, ctx->stream));
-    ORCA_HIP_CHECK(hipStreamSynchronize(ctx->stream));
+    host_sync(ctx);
   });
 }
 
@@ -658,10 +655,7 @@ int orca_hip_from_bytes(orca_hip_ctx* ctx, const size_t* shape, size_t rank, con
       fail(ORCA_HIP_ERR_SHAPE, "Shape mismatch during from_bytes: expected " + std::to_string(want) +
                                    " bytes, got " + std::to_string(n_bytes));
     float* o = new_output(ctx, want / sizeof(float));
-    if (want) {
-      ORCA_HIP_CHECK(hipMemcpyAsync(o, bytes, want, hipMemcpyHostToDevice, ctx->stream));
-      ORCA_HIP_CHECK(hipStreamSynchronize(ctx->stream));
-    }
+    upload_async(ctx, o, bytes, want);  // stream-ordered, no host wait
     *out = o;
   });
 }
@@ -672,7 +666,7 @@ int orca_hip_to_bytes(orca_hip_ctx* ctx, const void* s, size_t n_bytes, uint8_t*
     if (!n_bytes) return;
     check_extent(ctx, s, n_bytes, "to_bytes");
     ORCA_HIP_CHECK(hipMemcpyAsync(host_out, s, n_bytes, hipMemcpyDeviceToHost, ctx->stream));
-    ORCA_HIP_CHECK(hipStreamSynchronize(ctx->stream));
+    host_sync(ctx);
   });
 }
 
@@ -903,7 +897,7 @@ int orca_hip_has_nan_or_inf(orca_hip_ctx* ctx, const void* s, size_t n, int dtyp
     ORCA_HIP_CHECK(hipGetLastError());
     int h = 0;
     ORCA_HIP_CHECK(hipMemcpyAsync(&h, flag.as<int>(), sizeof(int), hipMemcpyDeviceToHost, ctx->stream));
-    ORCA_HIP_CHECK(hipStreamSynchronize(ctx->stream));
+    host_sync(ctx);
     *result = h;
   });
 }

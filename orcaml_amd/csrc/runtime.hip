@@ -2,6 +2,7 @@
 // kernels of liborca_hip.so.
 #include <algorithm>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <sstream>
 
@@ -50,6 +51,7 @@ void* CachingAllocator::allocate(size_t bytes, hipStream_t stream) {
     if (it != cached_.end()) {
       void* p = it->second;
       cached_.erase(it);
+      cached_at_.erase(p);
       cached_bytes_ -= r;
       live_[p] = r;
       live_bytes_ += r;
@@ -84,6 +86,7 @@ void CachingAllocator::release(void* p) {
   live_.erase(it);
   live_bytes_ -= r;
   cached_.emplace(r, p);
+  cached_at_[p] = r;
   cached_bytes_ += r;
 }
 
@@ -93,10 +96,10 @@ size_t CachingAllocator::size_of(void* p) {
   return it == live_.end() ? 0 : it->second;
 }
 
-size_t CachingAllocator::extent_from(const void* p) {
-  std::lock_guard<std::mutex> lk(mu_);
-  auto it = live_.upper_bound(const_cast<void*>(p));
-  if (it == live_.begin()) return 0;
+// Bytes from p to the end of the block of `blocks` (address -> size) that contains p, or 0.
+static size_t extent_in(const std::map<void*, size_t>& blocks, const void* p) {
+  auto it = blocks.upper_bound(const_cast<void*>(p));
+  if (it == blocks.begin()) return 0;
   --it;
   const char* base = static_cast<const char*>(it->first);
   const char* q = static_cast<const char*>(p);
@@ -104,20 +107,48 @@ size_t CachingAllocator::extent_from(const void* p) {
   return 0;
 }
 
+CachingAllocator::Where CachingAllocator::locate(const void* p, size_t* extent) {
+  std::lock_guard<std::mutex> lk(mu_);
+  if (size_t e = extent_in(live_, p)) {
+    *extent = e;
+    return Where::kLive;
+  }
+  *extent = 0;
+  return extent_in(cached_at_, p) ? Where::kFreed : Where::kUnknown;
+}
+
+size_t CachingAllocator::extent_from(const void* p) {
+  std::lock_guard<std::mutex> lk(mu_);
+  return extent_in(live_, p);
+}
+
 void check_extent(orca_hip_ctx* ctx, const void* p, size_t bytes, const char* what) {
   if (!p || !bytes) return;
-  const size_t have = ctx->alloc.extent_from(p);
-  if (have && bytes > have)
-    fail(ORCA_HIP_ERR_SHAPE, std::string("Shape mismatch during ") + what + ": the access spans " +
-                                 std::to_string(bytes) + " bytes but the buffer has " + std::to_string(have) +
-                                 " from this pointer");
+  size_t have = 0;
+  switch (ctx->alloc.locate(p, &have)) {
+    case CachingAllocator::Where::kLive:
+      if (bytes > have)
+        fail(ORCA_HIP_ERR_SHAPE, std::string("Shape mismatch during ") + what + ": the access spans " +
+                                     std::to_string(bytes) + " bytes but the buffer has " + std::to_string(have) +
+                                     " from this pointer");
+      break;
+    case CachingAllocator::Where::kFreed:
+      fail(ORCA_HIP_ERR_INTERNAL, std::string("Internal error: ") + what +
+                                      " was given a pointer into a buffer that has been freed");
+    case CachingAllocator::Where::kUnknown:
+      break;
+  }
 }
 
 void CachingAllocator::empty(hipStream_t stream) {
-  if (stream) (void)hipStreamSynchronize(stream);
+  if (stream) {
+    if (sync_counter) sync_counter->fetch_add(1, std::memory_order_relaxed);
+    (void)hipStreamSynchronize(stream);
+  }
   std::lock_guard<std::mutex> lk(mu_);
   for (auto& kv : cached_) (void)hipFree(kv.second);
   cached_.clear();
+  cached_at_.clear();
   cached_bytes_ = 0;
 }
 
@@ -184,6 +215,105 @@ ProfScope::~ProfScope() {
   if (hipEventRecord(rec_.stop, stream_) == hipSuccess) ctx_->prof.pending.push_back(rec_);
 }
 
+// ------------------------------------------------------------ host waits and uploads
+void host_sync(orca_hip_ctx* ctx, hipStream_t stream) {
+  ctx->host_syncs.fetch_add(1, std::memory_order_relaxed);
+  ORCA_HIP_CHECK(hipStreamSynchronize(stream ? stream : ctx->stream));
+}
+
+void host_wait_event(orca_hip_ctx* ctx, hipEvent_t ev) {
+  ctx->host_syncs.fetch_add(1, std::memory_order_relaxed);
+  ORCA_HIP_CHECK(hipEventSynchronize(ev));
+}
+
+void StagingRing::retire_finished() {
+  while (!inflight_.empty()) {
+    const hipError_t q = hipEventQuery(inflight_.front().done);
+    if (q == hipErrorNotReady) return;
+    ORCA_HIP_CHECK(q);
+    spare_.push_back(inflight_.front().done);
+    inflight_.pop_front();
+  }
+}
+
+size_t StagingRing::reserve(orca_hip_ctx* ctx, size_t need) {
+  for (;;) {
+    retire_finished();
+    if (inflight_.empty()) {
+      head_ = 0;
+      return 0;
+    }
+    // The regions in flight occupy [tail, head_) in ring order; head_ == tail
+    // with regions in flight means the ring is full.
+    const size_t tail = inflight_.front().begin;
+    if (head_ > tail) {
+      if (kCapacity - head_ >= need) return head_;
+      if (tail >= need) return 0;
+    } else if (head_ < tail && tail - head_ >= need) {
+      return head_;
+    }
+    host_wait_event(ctx, inflight_.front().done);  // back-pressure: wait for the oldest copy
+  }
+}
+
+void StagingRing::upload(orca_hip_ctx* ctx, void* dst, const void* src, size_t bytes, hipStream_t stream) {
+  std::lock_guard<std::mutex> lk(mu_);
+  if (!base_) ORCA_HIP_CHECK(hipHostMalloc(reinterpret_cast<void**>(&base_), kCapacity, hipHostMallocDefault));
+  char* d = static_cast<char*>(dst);
+  const char* h = static_cast<const char*>(src);
+  while (bytes) {
+    const size_t part = std::min(bytes, kChunk);
+    const size_t need = (part + 255) & ~size_t(255);
+    const size_t off = reserve(ctx, need);
+    std::memcpy(base_ + off, h, part);
+    ORCA_HIP_CHECK(hipMemcpyAsync(d, base_ + off, part, hipMemcpyHostToDevice, stream));
+    hipEvent_t ev;
+    if (spare_.empty()) {
+      ORCA_HIP_CHECK(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
+    } else {
+      ev = spare_.back();
+      spare_.pop_back();
+    }
+    ORCA_HIP_CHECK(hipEventRecord(ev, stream));
+    inflight_.push_back(Region{off, off + need, ev});
+    head_ = off + need;
+    d += part;
+    h += part;
+    bytes -= part;
+  }
+}
+
+StagingRing::~StagingRing() {
+  // The owning context has synchronised its stream before it is destroyed.
+  for (auto& r : inflight_) (void)hipEventDestroy(r.done);
+  for (auto e : spare_) (void)hipEventDestroy(e);
+  if (base_) (void)hipHostFree(base_);
+}
+
+// Up to 1 KiB of host data handed to the device as a kernel argument: it is
+// captured at launch, so nothing is left for the host to keep alive or wait for.
+struct SmallPayload {
+  uint32_t words;
+  uint32_t data[256];
+};
+
+__global__ void store_payload_kernel(uint32_t* __restrict__ dst, SmallPayload p) {
+  for (uint32_t i = threadIdx.x; i < p.words; i += blockDim.x) dst[i] = p.data[i];
+}
+
+void upload_async(orca_hip_ctx* ctx, void* dst, const void* src, size_t bytes) {
+  if (!bytes) return;
+  if (bytes % 4 == 0 && bytes <= sizeof(SmallPayload::data) && reinterpret_cast<uintptr_t>(dst) % 4 == 0) {
+    SmallPayload p;
+    p.words = static_cast<uint32_t>(bytes / 4);
+    std::memcpy(p.data, src, bytes);
+    hipLaunchKernelGGL(store_payload_kernel, dim3(1), dim3(64), 0, ctx->stream, static_cast<uint32_t*>(dst), p);
+    ORCA_HIP_CHECK(hipGetLastError());
+    return;
+  }
+  ctx->staging.upload(ctx, dst, src, bytes, ctx->stream);
+}
+
 // ------------------------------------------------------------ small kernels
 __global__ void fill_kernel(float* __restrict__ dst, float v, size_t n) {
   size_t stride = (size_t)gridDim.x * blockDim.x;
@@ -213,8 +343,37 @@ void launch_copy(orca_hip_ctx* ctx, float* dst, const float* src, size_t n) {
 }
 
 
+namespace {
+struct CallOutputs {
+  int depth = 0;
+  std::vector<std::pair<orca_hip_ctx*, void*>> made;
+};
+thread_local CallOutputs g_outputs;
+}  // namespace
+
+void outputs_begin() {
+  if (g_outputs.depth++ == 0) g_outputs.made.clear();
+}
+
+void outputs_commit() {
+  if (--g_outputs.depth == 0) g_outputs.made.clear();
+}
+
+void outputs_abort() {
+  if (--g_outputs.depth != 0) return;
+  for (auto& cp : g_outputs.made) {
+    try {
+      cp.first->alloc.release(cp.second);
+    } catch (...) {
+    }
+  }
+  g_outputs.made.clear();
+}
+
 float* new_output(orca_hip_ctx* ctx, size_t n) {
-  return static_cast<float*>(ctx->alloc.allocate(n * sizeof(float), ctx->stream));
+  void* p = ctx->alloc.allocate(n * sizeof(float), ctx->stream);
+  g_outputs.made.emplace_back(ctx, p);
+  return static_cast<float*>(p);
 }
 
 }  // namespace orca_hip
@@ -240,6 +399,12 @@ int orca_hip_ctx_create(int device, orca_hip_ctx** out) {
     auto* ctx = new orca_hip_ctx();
     ctx->device = device;
     ctx->num_cus = prop.multiProcessorCount;
+    ctx->alloc.sync_counter = &ctx->host_syncs;
+    if (const char* v = std::getenv("ORCA_HIP_GEMM_FAST")) ctx->gemm_generic_only = v[0] == '0';
+    if (const char* v = std::getenv("ORCA_HIP_GEMM_TILE")) {
+      if (std::strcmp(v, "128x128") == 0) ctx->gemm_tile_bn = 128;
+      if (std::strcmp(v, "128x64") == 0) ctx->gemm_tile_bn = 64;
+    }
     hipError_t e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
     if (e == hipSuccess) e = hipEventCreate(&ctx->timer_start);
     if (e == hipSuccess) e = hipEventCreate(&ctx->timer_stop);
@@ -307,7 +472,7 @@ int orca_hip_h2d(orca_hip_ctx* ctx, void* dst, const void* src, size_t bytes) {
     if (!bytes) return;
     check_extent(ctx, dst, bytes, "h2d");
     ORCA_HIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream));
-    ORCA_HIP_CHECK(hipStreamSynchronize(ctx->stream));
+    host_sync(ctx);
   });
 }
 
@@ -317,7 +482,7 @@ int orca_hip_d2h(orca_hip_ctx* ctx, void* dst, const void* src, size_t bytes) {
     if (!bytes) return;
     check_extent(ctx, src, bytes, "d2h");
     ORCA_HIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream));
-    ORCA_HIP_CHECK(hipStreamSynchronize(ctx->stream));
+    host_sync(ctx);
   });
 }
 
@@ -342,7 +507,15 @@ int orca_hip_fill(orca_hip_ctx* ctx, float* dst, float value, size_t n) {
 int orca_hip_sync(orca_hip_ctx* ctx) {
   return guard([&] {
     bind(ctx);
-    ORCA_HIP_CHECK(hipStreamSynchronize(ctx->stream));
+    host_sync(ctx);
+  });
+}
+
+int orca_hip_sync_count(const orca_hip_ctx* ctx, uint64_t* count) {
+  return guard([&] {
+    check_ctx(ctx);
+    if (!count) fail(ORCA_HIP_ERR_INTERNAL, "null output pointer");
+    *count = ctx->host_syncs.load(std::memory_order_relaxed);
   });
 }
 
@@ -356,7 +529,7 @@ int orca_hip_prof_enable(orca_hip_ctx* ctx, int enable) {
 int orca_hip_prof_reset(orca_hip_ctx* ctx) {
   return guard([&] {
     bind(ctx);
-    ORCA_HIP_CHECK(hipStreamSynchronize(ctx->stream));
+    host_sync(ctx);
     ctx->prof.drain();
     ctx->prof.agg.clear();
   });
@@ -365,7 +538,7 @@ int orca_hip_prof_reset(orca_hip_ctx* ctx) {
 int orca_hip_prof_report(orca_hip_ctx* ctx, char* buf, size_t len) {
   return guard([&] {
     bind(ctx);
-    ORCA_HIP_CHECK(hipStreamSynchronize(ctx->stream));
+    host_sync(ctx);
     ctx->prof.drain();
     std::ostringstream os;
     os << "{\"num_cus\": " << ctx->num_cus << ", \"kernels\": [";
@@ -394,7 +567,7 @@ int orca_hip_timer_stop(orca_hip_ctx* ctx, float* ms) {
   return guard([&] {
     bind(ctx);
     ORCA_HIP_CHECK(hipEventRecord(ctx->timer_stop, ctx->stream));
-    ORCA_HIP_CHECK(hipEventSynchronize(ctx->timer_stop));
+    host_wait_event(ctx, ctx->timer_stop);
     ORCA_HIP_CHECK(hipEventElapsedTime(ms, ctx->timer_start, ctx->timer_stop));
   });
 }

@@ -6,7 +6,9 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cstdint>
+#include <deque>
 #include <map>
 #include <memory>
 #include <mutex>
@@ -36,19 +38,31 @@ void set_last_error(const std::string& msg);
       ::orca_hip::fail(ORCA_HIP_ERR_INTERNAL, std::string(#expr) + ": " + hipGetErrorString(e_)); \
   } while (0)
 
+// Output buffers allocated by the entry point that is running on this thread
+// (new_output): kept when it succeeds, returned to the allocator when it fails,
+// so an op that rejects its arguments after allocating its result leaks nothing.
+void outputs_begin();
+void outputs_commit();
+void outputs_abort();
+
 // Runs f, converting exceptions into a status code + thread-local message.
 template <class F>
 int guard(F&& f) {
+  outputs_begin();
   try {
     f();
+    outputs_commit();
     return ORCA_HIP_OK;
   } catch (const Error& e) {
+    outputs_abort();
     set_last_error(e.what());
     return e.code;
   } catch (const std::exception& e) {
+    outputs_abort();
     set_last_error(std::string("internal error: ") + e.what());
     return ORCA_HIP_ERR_INTERNAL;
   } catch (...) {
+    outputs_abort();
     set_last_error("internal error: unknown exception");
     return ORCA_HIP_ERR_INTERNAL;
   }
@@ -64,18 +78,56 @@ class CachingAllocator {
   void release(void* p);
   void empty(hipStream_t stream);
   size_t size_of(void* p);
+  // Where p points: into a live block (*extent = bytes from p to its end), into
+  // a block that was freed and is held in the cache, or into neither (memory
+  // this allocator did not hand out).
+  enum class Where { kLive, kFreed, kUnknown };
+  Where locate(const void* p, size_t* extent);
   // Bytes from p to the end of the live allocation containing p (0 if none does).
   size_t extent_from(const void* p);
   void stats(size_t* live, size_t* cached, size_t* mallocs);
   ~CachingAllocator();
 
   static size_t round_size(size_t bytes);
+  // Counts the stream synchronisation that empty() performs (the owning context's counter).
+  std::atomic<uint64_t>* sync_counter = nullptr;
 
  private:
   std::mutex mu_;
   std::map<void*, size_t> live_;  // ordered: extent_from finds the block around an interior pointer
   std::multimap<size_t, void*> cached_;
+  std::map<void*, size_t> cached_at_;  // the cached blocks by address, for locate()
   size_t live_bytes_ = 0, cached_bytes_ = 0, mallocs_ = 0;
+};
+
+// Pinned host memory through which uploads reach the device without a host
+// wait: the caller's bytes are copied into a free region of the ring, the
+// region is copied to the device on the stream, and an event recorded after
+// that copy marks when the region may be reused.  The host waits only when
+// every region is still in flight (back-pressure), and each such wait is
+// counted like any other.
+class StagingRing {
+ public:
+  // Enqueues dst <- src (bytes) on `stream`; src may be reused on return.
+  void upload(orca_hip_ctx* ctx, void* dst, const void* src, size_t bytes, hipStream_t stream);
+  ~StagingRing();
+
+  static constexpr size_t kCapacity = size_t(16) << 20;  // pinned bytes held per context
+  static constexpr size_t kChunk = size_t(4) << 20;      // largest single region
+
+ private:
+  struct Region {
+    size_t begin, end;
+    hipEvent_t done;
+  };
+  // Offset of a free region of `need` bytes, waiting for the oldest copies if none is free.
+  size_t reserve(orca_hip_ctx* ctx, size_t need);
+  void retire_finished();
+  std::mutex mu_;
+  char* base_ = nullptr;
+  size_t head_ = 0;
+  std::deque<Region> inflight_;
+  std::vector<hipEvent_t> spare_;
 };
 
 // Per-kernel timing aggregation (enabled by orca_hip_prof_enable).
@@ -109,6 +161,14 @@ struct orca_hip_ctx {
   orca_hip::Profiler prof;
   hipEvent_t timer_start = nullptr, timer_stop = nullptr;
   std::mutex mu;
+  // Tuning switches read once when the context is created (environment):
+  // ORCA_HIP_GEMM_FAST=0 sends every product through the generic GEMM kernel,
+  // ORCA_HIP_GEMM_TILE=128x128|128x64 fixes the generic kernel's tile (0 = by grid size).
+  bool gemm_generic_only = false;
+  int gemm_tile_bn = 0;
+  // Host waits on this context's work so far (stream or event synchronisations).
+  std::atomic<uint64_t> host_syncs{0};
+  orca_hip::StagingRing staging;
 };
 
 namespace orca_hip {
@@ -151,8 +211,9 @@ class Scratch {
 
 // Fails with ShapeMismatch when [p, p + bytes) runs past the end of the
 // context allocation that contains p, so a wrong size or leading dimension
-// is reported instead of launching out of bounds.  Memory the context did
-// not allocate is not checked.
+// is reported instead of launching out of bounds, and with InternalError when
+// p points into a block that was freed (a use after free through the ABI).
+// Memory the context did not allocate is not checked.
 void check_extent(orca_hip_ctx* ctx, const void* p, size_t bytes, const char* what);
 // Extent of a row-major [rows][ld] operand whose rows hold `cols` used values.
 inline size_t matrix_bytes(size_t rows, size_t cols, size_t ld) {
@@ -179,6 +240,15 @@ inline unsigned grid_for(size_t work_items, unsigned block, unsigned max_blocks)
   if (g > max_blocks) g = max_blocks;
   return static_cast<unsigned>(g);
 }
+
+// Every host wait the library performs goes through these two, which count it
+// in ctx->host_syncs (reported by orca_hip_sync_count).
+void host_sync(orca_hip_ctx* ctx, hipStream_t stream = nullptr);
+void host_wait_event(orca_hip_ctx* ctx, hipEvent_t ev);
+// Stream-ordered host-to-device copy that does not wait for the device: small
+// payloads travel as a kernel argument, larger ones through the staging ring.
+// The host buffer may be reused as soon as this returns.
+void upload_async(orca_hip_ctx* ctx, void* dst, const void* src, size_t bytes);
 
 // Allocates a fresh output buffer of n floats for a trait op.
 float* new_output(orca_hip_ctx* ctx, size_t n);

@@ -53,6 +53,12 @@ class Context:
     def sync(self) -> None:
         _lib.call("orca_hip_sync", self.handle)
 
+    def sync_count(self) -> int:
+        """Host waits on this context's work so far (orca_hip_sync_count)."""
+        n = ctypes.c_uint64()
+        _lib.call("orca_hip_sync_count", self.handle, ctypes.byref(n))
+        return n.value
+
     def mem_stats(self) -> dict:
         live, cached, mallocs = ctypes.c_size_t(), ctypes.c_size_t(), ctypes.c_size_t()
         _lib.call("orca_hip_mem_stats", self.handle, ctypes.byref(live), ctypes.byref(cached), ctypes.byref(mallocs))
