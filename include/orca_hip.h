@@ -247,6 +247,17 @@ int orca_hip_head_backward(orca_hip_ctx* ctx, const float* H, size_t B, size_t K
  * orca-autograd/src/backend.rs:1633-1645, 1684-1697). */
 int orca_hip_relu_bw_colsum(orca_hip_ctx* ctx, const float* grad, const float* pre, size_t rows, size_t cols,
                             float* dpre, float* colsum);
+/* The same results as orca_hip_relu_bw_colsum, with no device allocation: no
+ * counterpart in the reference (whose backends allocate freely); it is for
+ * callers that cannot allocate -- code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc.  The column-sum partials live in a
+ * fixed device array of 2^20 floats (4 MiB) per GPU, held until the process
+ * ends, so with colsum != NULL ceil(rows / 64) * cols must not exceed 1048576
+ * (larger calls fail with ORCA_HIP_ERR_INTERNAL before anything is launched).
+ * Every call on a GPU shares that GPU's array: calls that overlap on one GPU
+ * (other streams or contexts) race and must be ordered by the caller. */
+int orca_hip_relu_bw_colsum_noalloc(orca_hip_ctx* ctx, const float* grad, const float* pre, size_t rows,
+                                    size_t cols, float* dpre, float* colsum);
 
 /* One AdamW step over flat buffers, same f32 op order as
  * python/orca/optim/adamw.py:71-94 with the f64 scalars rounded to f32 as

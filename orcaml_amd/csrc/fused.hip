@@ -9,8 +9,22 @@
 #include <cfloat>
 #include <cmath>
 
+#include <map>
+#include <mutex>
+
 #include "ce_row.hpp"
 #include "runtime.hpp"
+
+namespace orca_hip {
+// Fixed device scratch of orca_hip_relu_bw_colsum_noalloc: 2^20 floats (4 MiB)
+// per GPU, held until the process ends.
+constexpr size_t kStaticScratchFloats = size_t(1) << 20;
+}  // namespace orca_hip
+
+// One copy per GPU the library runs on.  In host code this name only stands in
+// for the symbol: kernels receive the per-device address that static_scratch()
+// resolves with hipGetSymbolAddress.
+static __device__ __align__(256) float scratch[orca_hip::kStaticScratchFloats];
 
 namespace orca_hip {
 namespace {
@@ -199,6 +213,8 @@ __global__ void __launch_bounds__(1024) ce_finish_kernel(const float* __restrict
     if (correct) *correct = cs[0];
   }
 }
+
+constexpr int kRowsPerChunk = 64;  // rows per column-sum partial of the ReLU-backward kernels
 
 // dpre = pre > 0 ? g : 0 and per-chunk column partial sums (4 columns per
 // thread).  Rows go RB_UNROLL at a time, all loads issued before any use;
@@ -569,6 +585,30 @@ void sgd(orca_hip_ctx* ctx, float* p, const float* g, size_t n, double lr, hipSt
   ORCA_HIP_CHECK(hipGetLastError());
 }
 
+// ReLU-backward + bias column sum, shared by the allocating and the
+// allocation-free entry points.
+void relu_bw_colsum_check(orca_hip_ctx* ctx, const float* grad, const float* pre, size_t rows, size_t cols,
+                          const float* dpre, const float* colsum);
+size_t relu_bw_colsum_partial_floats(size_t rows, size_t cols, bool colsum);
+void relu_bw_colsum_launch(orca_hip_ctx* ctx, const float* grad, const float* pre, size_t rows, size_t cols,
+                           float* dpre, float* colsum, float* part);
+
+// Device address of `scratch` on `device` (which the caller has made current),
+// resolved once per device and kept for the life of the process.
+float* static_scratch(int device) {
+  static std::mutex mu;
+  static std::map<int, float*> by_device;
+  std::lock_guard<std::mutex> lk(mu);
+  auto it = by_device.find(device);
+  if (it != by_device.end()) return it->second;
+  float* ptr = nullptr;
+  const hipError_t e = hipGetSymbolAddress((void**)&ptr, HIP_SYMBOL(scratch));
+  if (e != hipSuccess || !ptr)
+    fail(ORCA_HIP_ERR_INTERNAL, std::string("hipGetSymbolAddress(scratch) failed: ") + hipGetErrorString(e));
+  by_device[device] = ptr;
+  return ptr;
+}
+
 }  // namespace orca_hip
 
 using namespace orca_hip;
@@ -594,20 +634,59 @@ int orca_hip_relu_bw_colsum(orca_hip_ctx* ctx, const float* grad, const float* p
                             float* dpre, float* colsum) {
   return guard([&] {
     bind(ctx);
-    check_extent(ctx, grad, rows * cols * sizeof(float), "relu_bw_colsum (grad)");
-    check_extent(ctx, pre, rows * cols * sizeof(float), "relu_bw_colsum (pre)");
-    check_extent(ctx, dpre, rows * cols * sizeof(float), "relu_bw_colsum (dpre)");
-    check_extent(ctx, colsum, cols * sizeof(float), "relu_bw_colsum (colsum)");
+    relu_bw_colsum_check(ctx, grad, pre, rows, cols, dpre, colsum);
+    const size_t need = relu_bw_colsum_partial_floats(rows, cols, colsum != nullptr);
+    std::unique_ptr<Scratch> partial;
+    if (need) partial.reset(new Scratch(ctx, sizeof(float) * need));
+    relu_bw_colsum_launch(ctx, grad, pre, rows, cols, dpre, colsum, need ? partial->as<float>() : nullptr);
+  });
+}
+
+int orca_hip_relu_bw_colsum_noalloc(orca_hip_ctx* ctx, const float* grad, const float* pre, size_t rows,
+                                    size_t cols, float* dpre, float* colsum) {
+  return guard([&] {
+    bind(ctx);
+    const size_t need = relu_bw_colsum_partial_floats(rows, cols, colsum != nullptr);
+    if (need > kStaticScratchFloats)
+      fail(ORCA_HIP_ERR_INTERNAL, "relu_bw_colsum_noalloc: ceil(rows / 64) * cols = " + std::to_string(need) +
+                                      " column-sum partials exceed the fixed device scratch of " +
+                                      std::to_string(kStaticScratchFloats) + " floats");
+    relu_bw_colsum_check(ctx, grad, pre, rows, cols, dpre, colsum);
+    // The kernels overwrite every partial they later read: nothing has to start at zero.
+    relu_bw_colsum_launch(ctx, grad, pre, rows, cols, dpre, colsum, need ? static_scratch(ctx->device) : nullptr);
+  });
+}
+
+}  // extern "C"
+
+namespace orca_hip {
+
+void relu_bw_colsum_check(orca_hip_ctx* ctx, const float* grad, const float* pre, size_t rows, size_t cols,
+                          const float* dpre, const float* colsum) {
+  check_extent(ctx, grad, rows * cols * sizeof(float), "relu_bw_colsum (grad)");
+  check_extent(ctx, pre, rows * cols * sizeof(float), "relu_bw_colsum (pre)");
+  check_extent(ctx, dpre, rows * cols * sizeof(float), "relu_bw_colsum (dpre)");
+  check_extent(ctx, colsum, cols * sizeof(float), "relu_bw_colsum (colsum)");
+  if ((rows * cols != 0) && (!grad || !pre || !dpre))
+    fail(ORCA_HIP_ERR_INTERNAL, "relu_bw_colsum: null grad, pre-activation or output");
+  if ((rows + kRowsPerChunk - 1) / kRowsPerChunk > 65535) fail(ORCA_HIP_ERR_INTERNAL, "relu_bw_colsum: too many rows");
+}
+
+size_t relu_bw_colsum_partial_floats(size_t rows, size_t cols, bool colsum) {
+  if (!colsum || rows == 0 || cols == 0) return 0;
+  return (rows + kRowsPerChunk - 1) / kRowsPerChunk * cols;
+}
+
+// dpre (and colsum when non-null) on the context stream; `part` holds the
+// per-chunk column partials (relu_bw_colsum_partial_floats of them).
+void relu_bw_colsum_launch(orca_hip_ctx* ctx, const float* grad, const float* pre, size_t rows, size_t cols,
+                           float* dpre, float* colsum, float* part) {
     if (rows == 0 || cols == 0) {
       if (colsum) launch_fill(ctx, colsum, 0.0f, cols);
       return;
     }
-    const int rows_per_chunk = 64;
+    const int rows_per_chunk = kRowsPerChunk;
     const size_t chunks = (rows + rows_per_chunk - 1) / rows_per_chunk;
-    if (chunks > 65535) fail(ORCA_HIP_ERR_INTERNAL, "relu_bw_colsum: too many rows");
-    std::unique_ptr<Scratch> partial;
-    if (colsum) partial.reset(new Scratch(ctx, sizeof(float) * chunks * cols));
-    float* part = colsum ? partial->as<float>() : nullptr;
     {
       ProfScope ps(ctx, "relu_bw_colsum", 0.0, 12.0 * (double)rows * cols + (colsum ? 4.0 * cols : 0.0));
       if (cols % 4 == 0 && aligned16(grad) && aligned16(pre) && aligned16(dpre)) {
@@ -629,8 +708,11 @@ int orca_hip_relu_bw_colsum(orca_hip_ctx* ctx, const float* grad, const float* p
                          0, ctx->stream, part, (int)chunks, cols, colsum);
       ORCA_HIP_CHECK(hipGetLastError());
     }
-  });
 }
+
+}  // namespace orca_hip
+
+extern "C" {
 
 int orca_hip_adamw_step(orca_hip_ctx* ctx, float* p, const float* g, float* m, float* v, size_t n, double lr,
                         double beta1, double beta2, double eps, double weight_decay, int64_t t) {
