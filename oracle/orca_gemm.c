@@ -14,6 +14,7 @@
  */
 #include "orca_oracle.h"
 
+#include <math.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -101,31 +102,89 @@ __attribute__((target("avx2,fma"))) static int sgemm_avx2(size_t M, size_t N, si
 
 static int sgemm_generic(size_t M, size_t N, size_t K, const float* A, const float* B, float* C) GEMM_BODY
 
-/* Summation-order variant used only to measure how far two valid f32 GEMMs
- * drive a training run apart: 0 = packed/blocked f32 (default), 1 = each dot
- * product accumulated in f64 and rounded once. */
+/* Summation-order variants used only to measure how far valid f32 GEMMs drive
+ * a training run apart: 0 = packed/blocked f32 with fused multiply-adds
+ * (default), 1 = each dot product accumulated in f64 and rounded once, 2 = each
+ * dot product in f32 in ascending k with a separate multiply and add (the
+ * textbook loop), 3 = each dot product in f32 in descending k with fused
+ * multiply-adds.  Variants 1-3 split the rows over OpenMP threads, which does
+ * not change any element's order. */
 static int g_variant = 0;
 void orc_set_gemm_variant(int v) { g_variant = v; }
 
-static int sgemm_f64acc(size_t M, size_t N, size_t K, const float* A, const float* B, float* C) {
-  double* row = (double*)malloc(sizeof(double) * N);
-  if (!row) return -1;
+__attribute__((optimize("fp-contract=off"))) static int sgemm_f32_ascending(size_t M, size_t N, size_t K,
+                                                                           const float* A, const float* B, float* C) {
+#pragma omp parallel for schedule(static)
   for (size_t i = 0; i < M; ++i) {
-    for (size_t j = 0; j < N; ++j) row[j] = 0.0;
+    float* c = C + i * N;
+    for (size_t j = 0; j < N; ++j) c[j] = 0.0f;
     for (size_t k = 0; k < K; ++k) {
-      double a = A[i * K + k];
+      const float a = A[i * K + k];
       const float* b = B + k * N;
-      for (size_t j = 0; j < N; ++j) row[j] += a * (double)b[j];
+      for (size_t j = 0; j < N; ++j) {
+        const float prod = a * b[j];
+        c[j] = c[j] + prod;
+      }
     }
-    for (size_t j = 0; j < N; ++j) C[i * N + j] = (float)row[j];
   }
-  free(row);
   return 0;
+}
+
+#define DESCENDING_FMA_BODY                                                        \
+  {                                                                                \
+    _Pragma("omp parallel for schedule(static)") for (size_t i = 0; i < M; ++i) {  \
+      float* c = C + i * N;                                                        \
+      for (size_t j = 0; j < N; ++j) c[j] = 0.0f;                                  \
+      for (size_t k = K; k-- > 0;) {                                               \
+        const float a = A[i * K + k];                                              \
+        const float* b = B + k * N;                                                \
+        for (size_t j = 0; j < N; ++j) c[j] = fmaf(a, b[j], c[j]);                 \
+      }                                                                            \
+    }                                                                              \
+    return 0;                                                                      \
+  }
+
+__attribute__((target("avx2,fma"))) static int sgemm_desc_avx2(size_t M, size_t N, size_t K, const float* A,
+                                                               const float* B, float* C) DESCENDING_FMA_BODY
+static int sgemm_desc_generic(size_t M, size_t N, size_t K, const float* A, const float* B,
+                              float* C) DESCENDING_FMA_BODY
+
+static int sgemm_f32_descending_fma(size_t M, size_t N, size_t K, const float* A, const float* B, float* C) {
+  __builtin_cpu_init();
+  if (__builtin_cpu_supports("avx2") && __builtin_cpu_supports("fma")) return sgemm_desc_avx2(M, N, K, A, B, C);
+  return sgemm_desc_generic(M, N, K, A, B, C);
+}
+
+static int sgemm_f64acc(size_t M, size_t N, size_t K, const float* A, const float* B, float* C) {
+  int failed = 0;
+#pragma omp parallel
+  {
+    double* row = (double*)malloc(sizeof(double) * N);
+    if (!row) {
+#pragma omp atomic write
+      failed = 1;
+    }
+#pragma omp for schedule(static)
+    for (size_t i = 0; i < M; ++i) {
+      if (!row) continue;
+      for (size_t j = 0; j < N; ++j) row[j] = 0.0;
+      for (size_t k = 0; k < K; ++k) {
+        double a = A[i * K + k];
+        const float* b = B + k * N;
+        for (size_t j = 0; j < N; ++j) row[j] += a * (double)b[j];
+      }
+      for (size_t j = 0; j < N; ++j) C[i * N + j] = (float)row[j];
+    }
+    free(row);
+  }
+  return failed ? -1 : 0;
 }
 
 static int sgemm(size_t M, size_t N, size_t K, const float* A, const float* B, float* C) {
   if (M == 0 || N == 0) return 0;
   if (g_variant == 1) return sgemm_f64acc(M, N, K, A, B, C);
+  if (g_variant == 2) return sgemm_f32_ascending(M, N, K, A, B, C);
+  if (g_variant == 3) return sgemm_f32_descending_fma(M, N, K, A, B, C);
   if (K == 0) {
     memset(C, 0, sizeof(float) * M * N);
     return 0;

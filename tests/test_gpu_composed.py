@@ -1,0 +1,100 @@
+"""The unchanged composed drop-in path at full size -- the reference frontend
+(python/orca/nn/{linear,activation,container,loss}.py, python/orca/optim/adamw.py)
+replayed through the tape (orca-autograd/src/tape.rs:107-118) onto HipBackend's
+trait ops -- against the oracle, as it runs in the bench: plain, and with the
+opt-in fused loss and AdamW (CrossEntropyLoss(fused=True), AdamW(fused=True))."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from orcaml_amd import autodiff as A
+from orcaml_amd import synth
+from tests.parity import check_one_adamw_step, check_teacher_forced_adamw_step, oracle_hidden
+
+pytestmark = pytest.mark.gpu
+
+
+class Composed:
+    """nn.Sequential + CrossEntropyLoss + AdamW on HipBackend, stepping like a user
+    script, keeping the ReLU outputs of the forward pass for the mask-flip count."""
+
+    def __init__(self, hb, dims, params, x, onehot, opt, fused):
+        self.ad = A.Autodiff(hb)
+        self.model = A.build_mlp(self.ad, params)
+        self.opt = A.AdamW(self.model.parameters(), lr=opt["lr"], betas=opt.get("betas", (0.9, 0.999)),
+                           eps=opt.get("eps", 1e-8), weight_decay=opt["weight_decay"], fused=fused)
+        self.loss_fn = A.CrossEntropyLoss(fused=fused)
+        self.xt = A.Tensor.from_numpy(self.ad, x)
+        self.tt = A.Tensor.from_numpy(self.ad, onehot)
+
+    def step(self):
+        self.opt.zero_grad()
+        a, hidden = self.xt, []
+        for m in self.model._modules.values():  # Sequential.forward, keeping the ReLU outputs
+            a = m(a)
+            if isinstance(m, A.ReLU):
+                hidden.append(a)
+        loss = self.loss_fn(a, self.tt)
+        loss.backward()
+        grads = [p.tensor.grad().numpy() for p in self.model.parameters()]
+        logits = a.numpy()
+        self.opt.step()
+        return dict(loss=loss.to_list()[0], logits=logits, hidden=[h.numpy() for h in hidden], grads=grads)
+
+    def params(self):
+        return [p.tensor.numpy() for p in self.model.parameters()]
+
+    def moments(self):
+        return [m.numpy() for m in self.opt.m], [v.numpy() for v in self.opt.v]
+
+
+def ref_opt(o):
+    return O.make_opt(o["kind"], o["lr"], o.get("weight_decay", 0.0), o.get("betas", (0.9, 0.999)), o.get("eps", 1e-8))
+
+
+@pytest.mark.parametrize("fused", [False, True], ids=["unchanged", "fused_loss_adamw"])
+def test_composed_mlp784_4096_b1024_one_adamw_step(hb, fused):
+    """784-4096-4096-10, batch 1024, one fwd + bwd + AdamW step through the drop-in path,
+    with the same attribution of outliers as the fused trainer's one-step test."""
+    w = synth.WORKLOADS[synth.MLP_LARGE]
+    dims, o = w["dims"], w["opt"]
+    params, x, labels, onehot = synth.mlp_problem(w["seed"], dims, w["batch"])
+    run = Composed(hb, dims, params, x, onehot, o, fused)
+    out = run.step()
+    ref = O.mlp_train(dims, params, x, onehot, ref_opt(o), steps=1)
+    ref["hidden"] = oracle_hidden(params, x, dims)
+    preds = A.argmax_rows(out["logits"])
+    correct = int((preds == labels).sum())
+    check_one_adamw_step(dims, o, ref, out["loss"], out["logits"], out["hidden"], out["grads"], run.params(), preds,
+                         correct, what=f"composed 784-4096-4096-10 ({'fused' if fused else 'unchanged'})")
+
+
+@pytest.mark.parametrize("fused", [False, True], ids=["unchanged", "fused_loss_adamw"])
+def test_composed_mlp784_1024_b256_teacher_forced(hb, fused):
+    """784-1024-1024-10, batch 256, 12 AdamW steps on one fixed batch through the drop-in
+    path; at every step the oracle steps from the GPU's own parameters, moments and t
+    (loss and gradients to tolerance with counted mask flips, the update bit-exact)."""
+    w = synth.WORKLOADS[synth.MLP_MEDIUM]
+    dims, o = w["dims"], w["opt"]
+    params, x, labels, onehot = synth.mlp_problem(w["seed"], dims, w["batch"])
+    run = Composed(hb, dims, params, x, onehot, o, fused)
+    zeros = [np.zeros_like(p) for p in params]
+    state = dict(params=params, m=zeros, v=zeros, t=0)
+    total = 0
+    for step in range(12):
+        out = run.step()
+        ref = O.mlp_train(dims, state["params"], x, onehot, ref_opt(o), steps=1, m=state["m"], v=state["v"],
+                          t=state["t"], want_grads=True)
+        ref["hidden"] = oracle_hidden(state["params"], x, dims)
+        new_p = run.params()
+        new_m, new_v = run.moments()
+        flips = check_teacher_forced_adamw_step(dims, o, state, ref, out["loss"], out["hidden"], out["grads"], new_p,
+                                                new_m, new_v, what=f"step {step}")
+        total += sum(flips)
+        state = dict(params=[p.reshape(s.shape) for p, s in zip(new_p, params)],
+                     m=[m.reshape(s.shape) for m, s in zip(new_m, params)],
+                     v=[v.reshape(s.shape) for v, s in zip(new_v, params)], t=state["t"] + 1)
+    print(f"composed 784-1024-1024-10 ({'fused' if fused else 'unchanged'}) teacher-forced: {total} mask flips")
+    assert run.opt.t == 12

@@ -12,7 +12,8 @@ import pytest
 from oracle import oracle as O
 from orcaml_amd import _lib, synth
 from orcaml_amd.mlp import MLPTrainer
-from tests.util import assert_close, assert_close_scaled, outside_tolerance
+from tests.parity import check_one_adamw_step, check_teacher_forced_adamw_step, oracle_hidden
+from tests.util import assert_close, assert_close_scaled
 
 pytestmark = pytest.mark.gpu
 
@@ -28,37 +29,6 @@ def make_trainer(ctx, w, params):
 def ref_opt(w):
     o = w["opt"]
     return O.make_opt(o["kind"], o["lr"], o.get("weight_decay", 0.0), o.get("betas", (0.9, 0.999)), o.get("eps", 1e-8))
-
-
-def near_tie_rows(logits_ref: np.ndarray, tol: float) -> np.ndarray:
-    """Rows whose top-2 margin is within rounding: their argmax may
-    legitimately differ when the logits come from differently-rounded GEMMs."""
-    s = np.sort(logits_ref, axis=1)
-    return (s[:, -1] - s[:, -2]) <= tol * np.maximum(1.0, np.abs(s[:, -1]))
-
-
-def oracle_hidden(params, x, dims):
-    """The oracle's ReLU outputs of layers 0..L-2 (its own forward pass)."""
-    B = x.shape[0]
-    hs, a = [], x
-    for l in range(len(dims) - 2):
-        a = O.relu(O.add(O.matmul(a, params[2 * l]), O.expand(params[2 * l + 1], (B, dims[l + 1]))))
-        hs.append(a)
-    return hs
-
-
-def mask_flips(tr, hidden):
-    """Per layer, entries whose ReLU mask differs between the GPU's forward and
-    the oracle's (pre-activations within rounding of zero); 0 for the last
-    layer, which has no mask."""
-    return [int(((h > 0) != (tr.activation(l) > 0)).sum()) for l, h in enumerate(hidden)] + [0]
-
-
-def allowed_outliers(i, size, flips, dims):
-    """A flip at (b, j) of layer l's mask changes dZ_l[b, j]: column j of dW_l
-    (dims[l] entries) and entry j of db_l; plus a 1e-5 fraction of slack."""
-    l = i // 2
-    return int(np.ceil(1e-5 * size)) + flips[l] * (dims[l] if i % 2 == 0 else 1)
 
 
 def test_mlp784_1024_b256_hundred_adamw_steps_teacher_forced(ctx):
@@ -87,36 +57,36 @@ def test_mlp784_1024_b256_hundred_adamw_steps_teacher_forced(ctx):
         loss, _ = tr.metrics()
         ref = O.mlp_train(dims, state["params"], x, onehot, ref_opt(w), steps=1, m=state["m"], v=state["v"],
                           t=state["t"], want_grads=True)
-        assert_close(loss, ref["losses"][0], what=f"step {step} loss")
-        flips = mask_flips(tr, oracle_hidden(state["params"], x, dims))
-        total_flips += sum(flips)
+        ref["hidden"] = oracle_hidden(state["params"], x, dims)
+        hidden = [tr.activation(l) for l in range(len(dims) - 2)]
         got_g, got_p, got_m, got_v = tr.grads(), tr.params(), tr.moments(0), tr.moments(1)
+        flips = check_teacher_forced_adamw_step(dims, o, state, ref, loss, hidden, got_g, got_p, got_m, got_v,
+                                                what=f"step {step}")
+        total_flips += sum(flips)
         t = state["t"] + 1
-        for i in range(len(got_p)):
-            n_out = outside_tolerance(got_g[i], ref["grads"][i])
-            allowed = allowed_outliers(i, got_g[i].size, flips, dims)
-            assert n_out <= allowed, (f"step {step} grad {i}: {n_out} of {got_g[i].size} outside tolerance "
-                                      f"(ReLU mask flips {flips}, allowed {allowed})")
-            p1, m1, v1 = O.adamw_update(state["params"][i], got_g[i], state["m"][i], state["v"][i], t, lr=o["lr"],
-                                        weight_decay=o["weight_decay"], betas=o.get("betas", (0.9, 0.999)),
-                                        eps=o.get("eps", 1e-8))
-            np.testing.assert_array_equal(got_p[i], p1, err_msg=f"step {step} param {i}")
-            np.testing.assert_array_equal(got_m[i], m1, err_msg=f"step {step} m {i}")
-            np.testing.assert_array_equal(got_v[i], v1, err_msg=f"step {step} v {i}")
         state = dict(params=got_p, m=got_m, v=got_v, t=t)
     print(f"784-1024-1024-10 teacher-forced: {total_flips} ReLU mask flips over {w['steps']} steps")
     assert tr.step_count() == state["t"] == 100
 
 
+def _fraction_outside(got, want):
+    bad = sum(int((np.abs(g.astype(np.float64) - w) > 1e-5 + 1e-4 * np.abs(w.astype(np.float64))).sum())
+              for g, w in zip(got, want))
+    return bad / sum(w.size for w in want)
+
+
 def test_mlp784_1024_b256_free_running_within_natural_spread(ctx):
-    """Free-running, 100 AdamW steps amplify rounding (near-zero gradients get
-    +-lr updates while t is small), so trajectories from different valid
-    summation orders drift apart; per-step parity is the teacher-forced test
-    above.  Here the loss curves must agree to 1e-4 over the first steps and,
-    on the scale of the initial loss L0, stay within 2% of L0 at every step.
-    Measured: two CPU GEMM orders (blocked f32, f64-accumulated) differ by up
-    to 0.16% of L0 (2.6% of the step's own loss late in training, where it is
-    ~1e-3); the GPU differs from the oracle by up to 0.55% of L0."""
+    """Free-running, 100 AdamW steps amplify rounding (near-zero gradients get +-lr
+    updates while t is small), so trajectories from different valid f32 summation
+    orders drift apart; per-step parity is the teacher-forced test above.  The natural
+    envelope is measured here, on the same box, from three more valid GEMM orders of the
+    oracle (f64-accumulated, ascending f32, descending f32 with FMA) against its default
+    blocked order: the GPU's loss drift (max over steps of |L - L_oracle| / L0) must stay
+    within twice the largest drift among them, and its fraction of final parameters
+    outside 1e-5 + 1e-4|x| within 1.25 times theirs.  Measured on one box: loss drift
+    f64-acc 0.16 %, ascending f32 0.94 %, descending FMA 0.02 %, GPU 0.55 % of L0; final
+    parameters outside tolerance 53 %, 56 %, 30 %, GPU 54 %.  The first steps agree to
+    1e-4 relative, and the fixed batch is memorised."""
     w = synth.WORKLOADS[synth.MLP_MEDIUM]
     params, x, labels, onehot = synth.mlp_problem(w["seed"], w["dims"], w["batch"])
     tr = make_trainer(ctx, w, params)
@@ -126,21 +96,27 @@ def test_mlp784_1024_b256_free_running_within_natural_spread(ctx):
         tr.step()
         losses.append(tr.metrics()[0])
     gpu = np.array(losses, np.float64)
-    a = O.mlp_train(w["dims"], params, x, onehot, ref_opt(w), steps=w["steps"], want_grads=False)
-    O.lib().orc_set_gemm_variant(1)
+    gpu_params = tr.params()
+    runs = []
     try:
-        b = O.mlp_train(w["dims"], params, x, onehot, ref_opt(w), steps=w["steps"], want_grads=False)
+        for variant in range(4):
+            O.lib().orc_set_gemm_variant(variant)
+            runs.append(O.mlp_train(w["dims"], params, x, onehot, ref_opt(w), steps=w["steps"], want_grads=False))
     finally:
         O.lib().orc_set_gemm_variant(0)
-    ref = a["losses"].astype(np.float64)
+    ref = runs[0]["losses"].astype(np.float64)
     l0 = ref[0]
-    spread = np.abs(ref - b["losses"]) / l0
-    dev = np.abs(gpu - ref) / l0
-    print(f"784-1024-1024-10 free-running: max |dL|/L0 GPU {dev.max():.2e}, oracle orders {spread.max():.2e}; "
+    loss_env = max(float((np.abs(r["losses"] - ref) / l0).max()) for r in runs[1:])
+    param_env = max(_fraction_outside(r["params"], runs[0]["params"]) for r in runs[1:])
+    dev = float((np.abs(gpu - ref) / l0).max())
+    frac = _fraction_outside(gpu_params, runs[0]["params"])
+    print(f"784-1024-1024-10 free-running: loss drift / L0 GPU {dev:.2e}, envelope of valid orders {loss_env:.2e}; "
+          f"final parameters outside tolerance GPU {frac:.3f}, envelope {param_env:.3f}; "
           f"final loss gpu {gpu[-1]:.6f} oracle {ref[-1]:.6f}")
     assert np.isfinite(gpu).all()
     assert (np.abs(gpu[:5] - ref[:5]) <= 1e-4 * ref[:5]).all()  # identical until rounding differences can act
-    assert (dev <= 0.02).all()
+    assert dev <= 2.0 * loss_env
+    assert frac <= 1.25 * param_env
     assert gpu[-1] < 0.05 * gpu[0]  # the fixed batch is memorised
 
 
@@ -165,50 +141,10 @@ def test_mlp784_4096_b1024_one_adamw_step(ctx, batch):
     tr.step()
     loss, correct = tr.metrics()
     ref = O.mlp_train(dims, params, x, onehot, ref_opt(w), steps=1)
-    assert_close(loss, ref["losses"][0], what="loss")
-    assert_close(tr.logits(), ref["logits"], what="logits")
-    B = w["batch"]
-    h1 = O.relu(O.add(O.matmul(x, params[0]), O.expand(params[1], (B, dims[1]))))
-    h2 = O.relu(O.add(O.matmul(h1, params[2]), O.expand(params[3], (B, dims[2]))))
-    # ReLU outputs of the oracle's own forward pass; the last layer has no mask.
-    flips = [int(((h1 > 0) != (tr.activation(0) > 0)).sum()), int(((h2 > 0) != (tr.activation(1) > 0)).sum()), 0]
-    report, over = [], []
-    grads = tr.grads()
-    for kind, got_all, ref_all in (("grad", grads, ref["grads"]), ("param", tr.params(), ref["params"])):
-        for i, (g, r) in enumerate(zip(got_all, ref_all)):
-            bad = np.abs(g.astype(np.float64) - r) > 1e-5 + 1e-4 * np.abs(r.astype(np.float64))
-            n_out = int(bad.sum())
-            if kind == "param":
-                # AdamW's first update is lr * u(g) with u(g) = g / (|g| + eps): a
-                # normalisation that turns gradient differences well inside the tolerance
-                # (mask flips upstream perturb all of dW1 by ~1e-8, and near-zero entries
-                # can change sign) into parameter differences of up to 2 lr wherever |g| is
-                # within a few orders of eps.  Such an element is explained when the
-                # closed form alone, fed the two gradients, predicts a difference of at
-                # least half the tolerance; the AdamW kernel itself is bit-exact.
-                gg, gr = grads[i].astype(np.float64), ref["grads"][i].astype(np.float64)
-                lr, eps = w["opt"]["lr"], w["opt"]["eps"]
-                predicted = lr * np.abs(gg / (np.abs(gg) + eps) - gr / (np.abs(gr) + eps))
-                amplified = predicted >= 0.5 * (1e-5 + 1e-4 * np.abs(r.astype(np.float64)))
-                report.append(f"param{i}-from-grad:{int((bad & amplified).sum())}")
-                bad = bad & ~amplified
-                n_out = int(bad.sum())
-            # A flip at (b, j) of layer l's mask changes dZ_l[b, j]: column j of dW_l
-            # (dims[l] entries) and entry j of db_l.
-            l = i // 2
-            allowed = int(np.ceil(1e-5 * g.size)) + flips[l] * (dims[l] if i % 2 == 0 else 1)
-            report.append(f"{kind}{i}:{n_out}/{allowed}")
-            if n_out > allowed:
-                over.append(f"{kind} {i}: {n_out} of {g.size} outside tolerance (allowed {allowed})")
-    print(f"784-4096-4096-10 end-to-end: ReLU mask flips layer1 {flips[0]}, layer2 {flips[1]}; "
-          f"elements outside 1e-5+1e-4|x| / allowed: {' '.join(report)}")
-    assert not over, over
-    for i, (gg, gr) in enumerate(zip(grads, ref["grads"])):  # sign noise itself is rare
-        assert (np.sign(gg) != np.sign(gr)).mean() <= 2e-3, f"grad {i}: too many sign disagreements"
-    ties = near_tie_rows(ref["logits"], 1e-5)
-    preds = tr.preds()
-    np.testing.assert_array_equal(preds[~ties], ref["preds"][~ties])
-    assert abs(correct - ref["correct"]) <= int(ties.sum())
+    ref["hidden"] = oracle_hidden(params, x, dims)
+    hidden = [tr.activation(l) for l in range(len(dims) - 2)]
+    check_one_adamw_step(dims, w["opt"], ref, loss, tr.logits(), hidden, tr.grads(), tr.params(), tr.preds(), correct,
+                         what=f"784-4096-4096-10 b{batch} end-to-end")
 
 
 def test_mlp784_4096_b1024_second_arena_changes_no_bit(ctx, monkeypatch):

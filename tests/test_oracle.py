@@ -100,7 +100,18 @@ def test_sgd_closed_form():
     np.testing.assert_array_equal(O.sgd_update(p, g, 0.1), p - g * np.float32(0.1))
 
 
-def test_gemm_integer_exact_and_fp64_bound():
+@pytest.mark.parametrize("variant", [0, 1, 2, 3])
+def test_gemm_integer_exact_and_fp64_bound(variant):
+    """Every summation-order variant (blocked f32 with FMA, f64-accumulated, ascending f32,
+    descending f32 with FMA) is exact on small integers and within the gamma_K bound."""
+    O.lib().orc_set_gemm_variant(variant)
+    try:
+        _gemm_checks()
+    finally:
+        O.lib().orc_set_gemm_variant(0)
+
+
+def _gemm_checks():
     rng = np.random.default_rng(4)
     for (m, k, n) in [(1, 1, 1), (5, 3, 2), (130, 257, 67), (64, 784, 128)]:
         a = rng.integers(-8, 8, (m, k)).astype(np.float32)
