@@ -111,8 +111,9 @@ void orc_adamw_update(float* p, const float* g, float* m, float* v, size_t n, co
                       int64_t t);
 void orc_sgd_update(float* p, const float* g, size_t n, const orc_opt* opt);
 
-/* Selects the GEMM summation order (0 = blocked f32, 1 = f64-accumulated
- * dot products); used to measure the spread between two valid orders. */
+/* Selects the GEMM summation order (0 = blocked f32 with FMA, 1 = f64-accumulated
+ * dot products, 2 = ascending f32, 3 = descending f32 with FMA); used to measure
+ * the spread between valid orders. */
 void orc_set_gemm_variant(int variant);
 
 /* Thread count of the OpenMP elementwise ops. */

@@ -18,7 +18,7 @@ PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(PKG_DIR, "csrc")
 BUILD_DIR = os.path.join(PKG_DIR, "_build")
 LIB_PATH = os.path.join(PKG_DIR, "liborca_hip.so")
-SOURCES = ["runtime.hip", "ops.hip", "gemm.hip", "fused.hip", "head.hip", "mlp.hip"]
+SOURCES = ["runtime_host.cpp", "runtime.hip", "ops.hip", "gemm.hip", "fused.hip", "head.hip", "mlp.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
@@ -30,7 +30,7 @@ COMMON_FLAGS = [
 
 
 def _compile(src: str) -> str:
-    obj = os.path.join(BUILD_DIR, os.path.splitext(src)[0] + ".o")
+    obj = os.path.join(BUILD_DIR, src.replace(".", "_") + ".o")
     cmd = [HIPCC, *COMMON_FLAGS, "-c", os.path.join(CSRC, src), "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:

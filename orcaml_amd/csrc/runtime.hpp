@@ -28,6 +28,7 @@ struct Error : std::runtime_error {
 };
 
 void set_last_error(const std::string& msg);
+const char* last_error_cstr();  // the calling thread's last message
 
 [[noreturn]] inline void fail(int code, const std::string& msg) { throw Error(code, msg); }
 
