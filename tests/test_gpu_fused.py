@@ -161,6 +161,55 @@ def test_gemm_colsum_is_bias_gradient(ctx, M, N, K, exact):
     assert_gemm_error_bound(dW, X.T, dY)
 
 
+def _relu_bw_colsum_order(g, pre):
+    """The column sums in the kernels' own f32 order: rows summed in ascending order
+    within chunks of 64, then for each column four threads add a contiguous quarter of
+    the chunk partials each (in chunk order) and the quarters are added in order."""
+    rows, cols = g.shape
+    d = np.where(pre > 0, g, np.float32(0)).astype(np.float32)
+    chunks = -(-rows // 64)
+    part = np.zeros((chunks, cols), np.float32)
+    for c in range(chunks):
+        s = np.zeros(cols, np.float32)
+        for r in range(c * 64, min(rows, c * 64 + 64)):
+            s = (s + d[r]).astype(np.float32)
+        part[c] = s
+    per = -(-chunks // 4)
+    quarters = []
+    for q in range(4):
+        s = np.zeros(cols, np.float32)
+        for c in range(q * per, min(chunks, q * per + per)):
+            s = (s + part[c]).astype(np.float32)
+        quarters.append(s)
+    t = quarters[0]
+    for q in quarters[1:]:
+        t = (t + q).astype(np.float32)
+    return d, t
+
+
+@pytest.mark.parametrize("rows,cols", [(8192, 4096), (1000, 1032), (3, 8), (130, 260), (4099, 256), (77, 5)])
+def test_relu_bw_colsum_order_and_bound(ctx, rows, cols):
+    """ReLU backward + bias column sum: the mask exact; the column sums equal the kernels'
+    own summation order reproduced in f32 bit for bit (shapes up to 2^20 elements), and
+    the exact sum within the f32 bound n * 2^-24 * sum|x| (N(0, 1) data cancels, so a
+    relative check against the sequential order would test the data)."""
+    rng = np.random.default_rng(rows + cols)
+    g = rng.standard_normal((rows, cols)).astype(np.float32)
+    pre = rng.standard_normal((rows, cols)).astype(np.float32)
+    pre.reshape(-1)[::11] = 0.0
+    dg, dp = ctx.upload(g), ctx.upload(pre)
+    dpre, cs = ctx.alloc(4 * rows * cols), ctx.alloc(4 * cols)
+    _lib.call("orca_hip_relu_bw_colsum", ctx.handle, dg.ptr, dp.ptr, rows, cols, dpre.ptr, cs.ptr)
+    got = cs.download(count=cols)
+    d_ref = O.relu_backward(g, pre)
+    np.testing.assert_array_equal(dpre.download(count=rows * cols).reshape(rows, cols), d_ref)
+    if rows * cols <= 1 << 20:
+        np.testing.assert_array_equal(got, _relu_bw_colsum_order(g, pre)[1])
+    d64 = d_ref.astype(np.float64)
+    bound = rows * 2.0 ** -24 * np.abs(d64).sum(0) + 1e-30
+    assert (np.abs(got.astype(np.float64) - d64.sum(0)) <= bound).all()
+
+
 def run_ce(ctx, logits, onehot=None, labels=None, want_grad=True):
     B, C = logits.shape
     dl = ctx.upload(logits)
