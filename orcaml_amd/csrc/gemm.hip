@@ -608,6 +608,123 @@ __global__ void colsum_split_reduce_kernel(const float* __restrict__ part, int s
   out[n] = v;
 }
 
+// Skinny products (few rows, short K, A row-major): C[M, N] = A[M, K] op(B),
+// op(B) = B [K][N] (TB = false) or B stored [N][K] (TB = true).  One 32 x 32
+// tile of C per block of SK_WAVES waves, so an M = 256, N = 1024 product is
+// 256 blocks with no K split.  Wave w multiplies the k range [w kq, (w + 1) kq)
+// straight from global memory in MFMA fragment order: for each group of 8 k,
+// lane (i, h) = (l % 32, l / 32) holds A[m0 + i][k8 + 4h .. + 3] (one float4)
+// and the four B values of the same k for column n0 + i, and MFMA step j
+// (0..3) multiplies k = k8 + 4h + j.  Steps 0 and 2 accumulate into one
+// register block and 1 and 3 into another (two independent chains), added at
+// the end; the waves' tiles are summed through LDS in wave order.  SK_DEPTH
+// groups of loads are in flight while one is multiplied.
+// Rows and columns past M / N are clamped to the last valid one (never
+// stored); k past the wave's range reads as zero.
+struct SkinnyParams {
+  const float* A;
+  const float* B;
+  float* C;
+  int64_t lda, ldb, ldc;
+  int M, N, K, kq;
+  int vec;  // A (and B when TB) rows 16-byte aligned with lda, ldb multiples of 4
+  int epi;
+  const float* bias;
+  const float* mask;
+  int64_t ldmask;
+};
+
+template <bool TB>
+__device__ __forceinline__ void skinny_load(const SkinnyParams& p, int row_a, int col_b, int k, int kend, floatx4& a,
+                                            floatx4& b) {
+  if (p.vec && k + 4 <= kend) {
+    a = *reinterpret_cast<const floatx4*>(p.A + (int64_t)row_a * p.lda + k);
+    if (TB) {
+      b = *reinterpret_cast<const floatx4*>(p.B + (int64_t)col_b * p.ldb + k);
+    } else {
+      const float* bp = p.B + (int64_t)k * p.ldb + col_b;
+      b = floatx4{bp[0], bp[p.ldb], bp[2 * p.ldb], bp[3 * p.ldb]};
+    }
+  } else {
+    float av[4], bv[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const bool in = k + e < kend;
+      av[e] = in ? p.A[(int64_t)row_a * p.lda + k + e] : 0.0f;
+      bv[e] = in ? (TB ? p.B[(int64_t)col_b * p.ldb + k + e] : p.B[(int64_t)(k + e) * p.ldb + col_b]) : 0.0f;
+    }
+    a = floatx4{av[0], av[1], av[2], av[3]};
+    b = floatx4{bv[0], bv[1], bv[2], bv[3]};
+  }
+}
+
+constexpr int SK_WAVES = 8;   // waves per skinny block, each an eighth of K
+constexpr int SK_DEPTH = 4;   // 8-k groups of loads in flight per wave
+
+template <bool TB>
+__global__ void __launch_bounds__(64 * SK_WAVES) gemm_skinny_kernel(SkinnyParams p) {
+  __shared__ float red[SK_WAVES][32 * 32];
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, i = lane & 31, h = lane >> 5;
+  const int m0 = blockIdx.y * 32, n0 = blockIdx.x * 32;
+  const int row_a = min(m0 + i, p.M - 1), col_b = min(n0 + i, p.N - 1);
+  const int kbeg = w * p.kq, kend = min(p.K, kbeg + p.kq);
+  floatx16 acc0, acc1;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    acc0[r] = 0.0f;
+    acc1[r] = 0.0f;
+  }
+  if (kbeg < kend) {
+    floatx4 a[SK_DEPTH], b[SK_DEPTH];
+#pragma unroll
+    for (int d = 0; d < SK_DEPTH; ++d) skinny_load<TB>(p, row_a, col_b, kbeg + 8 * d + 4 * h, kend, a[d], b[d]);
+    for (int base = kbeg; base < kend; base += 8 * SK_DEPTH) {
+#pragma unroll
+      for (int d = 0; d < SK_DEPTH; ++d) {
+        acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(a[d].x, b[d].x, acc0, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(a[d].y, b[d].y, acc1, 0, 0, 0);
+        acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(a[d].z, b[d].z, acc0, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(a[d].w, b[d].w, acc1, 0, 0, 0);
+        // refill this slot with the group SK_DEPTH ahead (zeros past the wave's range)
+        skinny_load<TB>(p, row_a, col_b, base + 8 * (d + SK_DEPTH) + 4 * h, kend, a[d], b[d]);
+      }
+    }
+  }
+  // register r of lane (i, h) holds C[(r / 4) * 8 + h * 4 + r % 4][i] of this wave's tile
+#pragma unroll
+  for (int r = 0; r < 16; ++r) red[w][((r >> 2) * 8 + h * 4 + (r & 3)) * 32 + i] = acc0[r] + acc1[r];
+  __syncthreads();
+  // thread t < 256: row t / 8, columns 4 (t % 8) .. + 3
+  if (tid >= 256) return;
+  const int row = tid >> 3, c4 = (tid & 7) * 4;
+  const int m = m0 + row;
+  if (m >= p.M) return;
+  float v[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int o = row * 32 + c4 + e;
+    float t = red[0][o];
+#pragma unroll
+    for (int q = 1; q < SK_WAVES; ++q) t = t + red[q][o];
+    v[e] = t;
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int n = n0 + c4 + e;
+    if (n >= p.N) break;
+    float x = v[e];
+    if (p.epi == ORCA_HIP_EPI_BIAS) {
+      x = x + p.bias[n];
+    } else if (p.epi == ORCA_HIP_EPI_BIAS_RELU) {
+      x = x + p.bias[n];
+      x = x > 0.0f ? x : 0.0f;
+    } else if (p.epi == ORCA_HIP_EPI_RELU_MASK) {
+      x = p.mask[(int64_t)m * p.ldmask + n] > 0.0f ? x : 0.0f;
+    }
+    p.C[(int64_t)m * p.ldc + n] = x;
+  }
+}
+
 inline bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; }
 
 // Profiler names: "gemm_<op(A)><op(B)>", "_pipe" for the pipelined 128 x 128 kernel.
@@ -624,7 +741,8 @@ namespace {
 // Kernel, tile and K split of one product.
 struct GemmPlan {
   bool fast;
-  size_t BN, mt, nt;
+  bool skinny;  // 32 x 32 tiles on gemm_skinny_kernel, no K split
+  size_t BM, BN, mt, nt;
   int splits, k_chunk;
 };
 
@@ -646,7 +764,31 @@ GemmPlan plan_gemm(orca_hip_ctx* ctx, bool trans_a, bool trans_b, size_t M, size
   int bn = t128 >= target ? 128 : 64;
   if (ctx->gemm_tile_bn) bn = ctx->gemm_tile_bn;
   if (g.fast) bn = 128;
-  const size_t BM = 128;
+  size_t BM = 128;
+  // Short products (K <= 512) whose 128 x 128 grid leaves at least half the
+  // CUs idle take 64 x 64 tiles on the generic kernel instead of splitting K,
+  // when those tiles alone give three quarters of the CUs a block: the K
+  // split's partial sums and their reduce launch are gone (the weight
+  // gradients of a 256-row batch).  With fewer tiles, or a long K, the
+  // generic kernel's K loop costs more than the split saves.
+  const size_t t64 = ((M + 63) / 64) * ((N + 63) / 64) * batch;
+  if (ctx->gemm_small_tiles && K <= 512 && t128 <= target / 2 && 4 * t64 >= 3 * target) {
+    g.fast = false;
+    BM = 64;
+    bn = 64;
+  }
+  // Few rows and a short K (A row-major): when 32 x 32 tiles give between a
+  // half and two blocks per CU, the skinny kernel takes the product whole, with
+  // no K split (with more of its tiles the 128 x 128 split is faster).
+  const size_t t32 = ((M + 31) / 32) * ((N + 31) / 32);
+  if (ctx->gemm_skinny && !trans_a && batch == 1 && BM == 128 && t128 <= target / 2 && M <= 256 && K <= 1024 &&
+      2 * t32 >= target && t32 <= 2 * target) {
+    g.skinny = true;
+    g.fast = false;
+    BM = 32;
+    bn = 32;
+  }
+  g.BM = BM;
   g.BN = (size_t)bn;
   g.mt = (M + BM - 1) / BM;
   g.nt = (N + g.BN - 1) / g.BN;
@@ -655,7 +797,7 @@ GemmPlan plan_gemm(orca_hip_ctx* ctx, bool trans_a, bool trans_b, size_t M, size
   // between half and all of them a split would not shorten the longest CU).
   g.splits = 1;
   const size_t tiles = g.mt * g.nt * batch;
-  if (tiles <= target / 2 && K >= 4 * (size_t)BK) {
+  if (BM == 128 && !g.skinny && tiles <= target / 2 && K >= 4 * (size_t)BK) {
     size_t want = (target + tiles - 1) / tiles;
     size_t max_by_k = K / (2 * BK);
     g.splits = (int)std::min<size_t>(std::min<size_t>(want, max_by_k), 64);
@@ -706,6 +848,42 @@ void gemm(orca_hip_ctx* ctx, bool trans_a, bool trans_b, size_t M, size_t N, siz
     return;
   }
   const GemmPlan plan = plan_gemm(ctx, trans_a, trans_b, M, N, K, A, lda, sa, B, ldb, sb, batch);
+  if (plan.skinny) {
+    SkinnyParams q{};
+    q.A = A;
+    q.B = B;
+    q.C = C;
+    q.lda = (int64_t)lda;
+    q.ldb = (int64_t)ldb;
+    q.ldc = (int64_t)ldc;
+    q.M = (int)M;
+    q.N = (int)N;
+    q.K = (int)K;
+    q.kq = (int)(((K + SK_WAVES - 1) / SK_WAVES + 7) / 8 * 8);
+    q.vec = aligned16(A) && lda % 4 == 0 && (!trans_b || (aligned16(B) && ldb % 4 == 0));
+    q.epi = epi.kind;
+    q.bias = epi.bias;
+    q.mask = epi.mask;
+    q.ldmask = (int64_t)epi.ldmask;
+    {
+      std::string pname;
+      if (ctx->prof.enabled)
+        pname = std::string(trans_b ? "gemm_nt_skinny " : "gemm_nn_skinny ") + std::to_string(M) + "x" +
+                std::to_string(N) + "x" + std::to_string(K);
+      ProfScope ps(ctx, pname.c_str(), 2.0 * (double)M * N * K, 4.0 * (double)(M * K + K * N + M * N));
+      dim3 grid((unsigned)plan.nt, (unsigned)plan.mt);
+      if (trans_b)
+        hipLaunchKernelGGL(gemm_skinny_kernel<true>, grid, dim3(64 * SK_WAVES), 0, ctx->stream, q);
+      else
+        hipLaunchKernelGGL(gemm_skinny_kernel<false>, grid, dim3(64 * SK_WAVES), 0, ctx->stream, q);
+      ORCA_HIP_CHECK(hipGetLastError());
+    }
+    if (epi.colsum) {  // only a row-major B has one (the bias gradient of X^T dY, which is not skinny)
+      if (trans_b) fail(ORCA_HIP_ERR_INTERNAL, "gemm colsum epilogue requires row-major B");
+      launch_colsum(ctx, B, K, N, ldb, epi.colsum);
+    }
+    return;
+  }
   const bool fast = plan.fast;
   const int bn = (int)plan.BN;
   const size_t mt = plan.mt, nt = plan.nt;
@@ -763,14 +941,14 @@ void gemm(orca_hip_ctx* ctx, bool trans_a, bool trans_b, size_t M, size_t N, siz
     }
     ProfScope ps(ctx, pname.c_str(), 2.0 * (double)M * N * K * batch,
                  4.0 * (double)batch * (M * K + K * N + M * N));
-#define GEMM_LAUNCH(BN_, TA_, TB_) \
-  hipLaunchKernelGGL((gemm_mfma_f32_kernel<128, BN_, TA_, TB_>), grid, dim3(NTHREADS), 0, ctx->stream, p)
-#define GEMM_DISPATCH(BN_)                                      \
-  do {                                                          \
-    if (!trans_a && !trans_b) GEMM_LAUNCH(BN_, false, false);   \
-    else if (!trans_a && trans_b) GEMM_LAUNCH(BN_, false, true); \
-    else if (trans_a && !trans_b) GEMM_LAUNCH(BN_, true, false); \
-    else GEMM_LAUNCH(BN_, true, true);                          \
+#define GEMM_LAUNCH(BM_, BN_, TA_, TB_) \
+  hipLaunchKernelGGL((gemm_mfma_f32_kernel<BM_, BN_, TA_, TB_>), grid, dim3(NTHREADS), 0, ctx->stream, p)
+#define GEMM_DISPATCH(BM_, BN_)                                      \
+  do {                                                               \
+    if (!trans_a && !trans_b) GEMM_LAUNCH(BM_, BN_, false, false);   \
+    else if (!trans_a && trans_b) GEMM_LAUNCH(BM_, BN_, false, true); \
+    else if (trans_a && !trans_b) GEMM_LAUNCH(BM_, BN_, true, false); \
+    else GEMM_LAUNCH(BM_, BN_, true, true);                          \
   } while (0)
 #define FAST_LAUNCH(TA_, TB_, CS_) \
   hipLaunchKernelGGL((gemm_mfma_f32_fast_kernel<TA_, TB_, CS_>), grid, dim3(NTHREADS), 0, ctx->stream, p)
@@ -784,10 +962,12 @@ void gemm(orca_hip_ctx* ctx, bool trans_a, bool trans_b, size_t M, size_t N, siz
       else if (trans_a && !trans_b && cs) FAST_LAUNCH(true, false, true);
       else if (trans_a && !trans_b) FAST_LAUNCH(true, false, false);
       else FAST_LAUNCH(true, true, false);
+    } else if (plan.BM == 64) {
+      GEMM_DISPATCH(64, 64);
     } else if (bn == 128) {
-      GEMM_DISPATCH(128);
+      GEMM_DISPATCH(128, 128);
     } else {
-      GEMM_DISPATCH(64);
+      GEMM_DISPATCH(128, 64);
     }
 #undef FAST_LAUNCH
 #undef GEMM_DISPATCH

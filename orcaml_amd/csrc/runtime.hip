@@ -88,6 +88,8 @@ int orca_hip_ctx_create(int device, orca_hip_ctx** out) {
     ctx->num_cus = prop.multiProcessorCount;
     ctx->alloc.sync_counter = &ctx->host_syncs;
     if (const char* v = std::getenv("ORCA_HIP_GEMM_FAST")) ctx->gemm_generic_only = v[0] == '0';
+    if (const char* v = std::getenv("ORCA_HIP_GEMM_SMALL_TILES")) ctx->gemm_small_tiles = v[0] != '0';
+    if (const char* v = std::getenv("ORCA_HIP_GEMM_SKINNY")) ctx->gemm_skinny = v[0] != '0';
     if (const char* v = std::getenv("ORCA_HIP_GEMM_TILE")) {
       if (std::strcmp(v, "128x128") == 0) ctx->gemm_tile_bn = 128;
       if (std::strcmp(v, "128x64") == 0) ctx->gemm_tile_bn = 64;

@@ -167,6 +167,10 @@ struct orca_hip_ctx {
   // ORCA_HIP_GEMM_TILE=128x128|128x64 fixes the generic kernel's tile (0 = by grid size).
   bool gemm_generic_only = false;
   int gemm_tile_bn = 0;
+  // ORCA_HIP_GEMM_SMALL_TILES=0 keeps the K split for small products instead of 64 x 64 tiles.
+  bool gemm_small_tiles = true;
+  // ORCA_HIP_GEMM_SKINNY=0 keeps the K split for few-row products instead of the skinny kernel.
+  bool gemm_skinny = true;
   // Host waits on this context's work so far (stream or event synchronisations).
   std::atomic<uint64_t> host_syncs{0};
   orca_hip::StagingRing staging;

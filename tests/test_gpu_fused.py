@@ -101,6 +101,86 @@ def test_gemm_aligned_shapes_take_pipelined_kernel(ctx, ta, tb, colsum):
             np.testing.assert_array_equal(cs, O.sum_to_shape(B, (1, N)).reshape(N))
 
 
+SKINNY_SHAPES = [(256, 1024, 784), (256, 1024, 1024), (200, 1000, 1000), (256, 1024, 30), (130, 1030, 777),
+                 (129, 1029, 1021)]
+
+
+@pytest.mark.parametrize("tb", [False, True])
+@pytest.mark.parametrize("M,N,K", SKINNY_SHAPES)
+def test_gemm_skinny_exact_on_integers(ctx, tb, M, N, K):
+    """Few-row, short-K products with row-major A (the 784-1024-1024-10 / B = 256 forward and
+    dX products; ragged M, N, K; K shorter than a wave's 8-k group) run whole on the skinny
+    32 x 32 kernel (no K split, no reduce launch); exact on integers, with the column sum of
+    a row-major B taken by its own pass."""
+    cus = ctx.prof_report()["num_cus"]
+    if cus != 256:
+        pytest.skip("tile counts chosen for 256 compute units")
+    rng = np.random.default_rng(M + N + K + tb)
+    A = int_matrix(rng, (M, K))
+    B = int_matrix(rng, (K, N))
+    ctx.prof_reset()
+    ctx.prof_enable(True)
+    out = run_gemm(ctx, False, tb, A, np.ascontiguousarray(B.T) if tb else B, colsum=not tb)
+    ctx.prof_enable(False)
+    names = {k["name"] for k in ctx.prof_report()["kernels"]}
+    assert ("gemm_nt_skinny" if tb else "gemm_nn_skinny") + f" {M}x{N}x{K}" in names, names
+    assert "gemm_splitk_reduce" not in names
+    C, cs = out if not tb else (out, None)
+    np.testing.assert_array_equal(C, (A.astype(np.float64) @ B.astype(np.float64)).astype(np.float32))
+    if cs is not None:
+        np.testing.assert_array_equal(cs, B.astype(np.float64).sum(0).astype(np.float32))
+
+
+@pytest.mark.parametrize("M,N,K", [(256, 1024, 1024), (130, 1030, 777)])
+def test_gemm_skinny_epilogues_match_composed_ops(ctx, M, N, K):
+    """The skinny kernel's bias, bias + ReLU and ReLU-mask epilogues equal the composed ops
+    applied to its own product, bit for bit; the product is within the f32 dot-product bound."""
+    rng = np.random.default_rng(M + K)
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    B = rng.standard_normal((K, N)).astype(np.float32)
+    bias = rng.standard_normal(N).astype(np.float32)
+    prod = run_gemm(ctx, False, False, A, B)
+    assert_gemm_error_bound(prod, A, B)
+    np.testing.assert_array_equal(run_gemm(ctx, False, False, A, B, _lib.EPI_BIAS, bias=bias),
+                                  O.add(prod, O.expand(bias.reshape(1, N), (M, N))))
+    np.testing.assert_array_equal(run_gemm(ctx, False, False, A, B, _lib.EPI_BIAS_RELU, bias=bias),
+                                  O.relu(O.add(prod, O.expand(bias.reshape(1, N), (M, N)))))
+    mask = rng.standard_normal((M, N)).astype(np.float32)
+    mask[::7, ::3] = 0.0
+    np.testing.assert_array_equal(run_gemm(ctx, False, False, A, B, _lib.EPI_RELU_MASK, mask=mask),
+                                  O.relu_backward(prod, mask))
+    # the transposed-B form on the same data: same product bits
+    np.testing.assert_array_equal(run_gemm(ctx, False, True, A, np.ascontiguousarray(B.T)), prod)
+
+
+@pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False), (True, True)])
+@pytest.mark.parametrize("M,N,K", [(1024, 1024, 256), (784, 1024, 256), (1000, 1030, 250), (1024, 1024, 33)])
+def test_gemm_small_tiles_exact_on_integers(ctx, ta, tb, M, N, K):
+    """Short products (K <= 512) whose 128 x 128 grid leaves half the CUs idle but whose
+    64 x 64 grid covers three quarters of them run unsplit on 64 x 64 tiles (profiler name
+    without _pipe, no reduce launch): the 784-1024-1024-10 / B = 256 weight gradients,
+    ragged edges and a K that is not a multiple of the slab.  Exact on integers, with the
+    folded column sum."""
+    cus = ctx.prof_report()["num_cus"]
+    if cus != 256:
+        pytest.skip("tile counts chosen for 256 compute units")
+    rng = np.random.default_rng(M + N + K)
+    A = int_matrix(rng, (M, K))
+    B = int_matrix(rng, (K, N))
+    ctx.prof_reset()
+    ctx.prof_enable(True)
+    out = run_gemm(ctx, ta, tb, np.ascontiguousarray(A.T) if ta else A, np.ascontiguousarray(B.T) if tb else B,
+                   colsum=not tb)
+    ctx.prof_enable(False)
+    names = {k["name"] for k in ctx.prof_report()["kernels"]}
+    name = "gemm_" + ("t" if ta else "n") + ("t" if tb else "n") + f" {M}x{N}x{K}"
+    assert name in names and "gemm_splitk_reduce" not in names, names
+    C, cs = out if not tb else (out, None)
+    np.testing.assert_array_equal(C, (A.astype(np.float64) @ B.astype(np.float64)).astype(np.float32))
+    if cs is not None:
+        np.testing.assert_array_equal(cs, B.astype(np.float64).sum(0).astype(np.float32))
+
+
 @pytest.mark.parametrize("M,N,K", [(200, 300, 150), (200, 300, 152), (256, 384, 128), (128, 256, 1024),
                                    (130, 70, 1000), (1024, 2048, 128)])
 def test_gemm_epilogues_match_composed_ops(ctx, M, N, K):
@@ -127,7 +207,7 @@ def test_gemm_grid_of_half_the_cus_splits_k(ctx):
     """A 128 x 128 tile grid that covers exactly half the CUs runs as two K chunks (every CU busy,
     then the in-order chunk sum); the product stays exact on integers."""
     cus = ctx.prof_report()["num_cus"]
-    M, N, K = 128, 128 * (cus // 2), 256
+    M, N, K = 128, 128 * (cus // 2), 2048  # K > 1024: neither 64 x 64 tiles nor the skinny kernel
     rng = np.random.default_rng(11)
     A = int_matrix(rng, (M, K))
     B = int_matrix(rng, (K, N))
