@@ -189,6 +189,65 @@ int orca_hip_max_to_shape_backward(orca_hip_ctx* ctx, const void* grad_out, cons
 /* Backend::has_nan_or_inf (backend.rs:298); synchronises */
 int orca_hip_has_nan_or_inf(orca_hip_ctx* ctx, const void* s, size_t n, int dtype, int* result);
 
+/* ================ fused elementwise programs (lazy trait ops) ================ */
+/* The elementwise trait ops (Backend::add ... div_backward_rhs, accumulate_grad,
+ * and sum_to_shape / max_to_shape onto the input's own shape) applied per
+ * element as a straight-line program over registers, one launch for a whole
+ * chain: the backend's storages defer elementwise ops and run them together
+ * at their first non-elementwise use, which the tape never sees
+ * (orca-autograd/src/backend.rs:74-118 records each op as usual).  Each
+ * instruction is the same f32 operation as the op's own kernel, so results are
+ * bit-identical to running the ops one by one. */
+#define ORCA_HIP_EW_ADD 0          /* a + b (also accumulate_grad) */
+#define ORCA_HIP_EW_SUB 1          /* a - b */
+#define ORCA_HIP_EW_MUL 2          /* a * b */
+#define ORCA_HIP_EW_DIV 3          /* a / b (also div_backward_lhs) */
+#define ORCA_HIP_EW_MUL_SCALAR 4   /* a * scalar */
+#define ORCA_HIP_EW_RELU 5         /* a > 0 ? a : 0 */
+#define ORCA_HIP_EW_RELU_BW 6      /* b > 0 ? a : 0   (a = grad, b = input) */
+#define ORCA_HIP_EW_EXP 7
+#define ORCA_HIP_EW_LOG 8          /* ln(max(a, 1e-7)) */
+#define ORCA_HIP_EW_SQRT 9
+#define ORCA_HIP_EW_SIGMOID 10
+#define ORCA_HIP_EW_EXP_BW 11      /* a * b   (b = output) */
+#define ORCA_HIP_EW_LOG_BW 12      /* a / b   (b = input) */
+#define ORCA_HIP_EW_SQRT_BW 13     /* a / (2 b) */
+#define ORCA_HIP_EW_SIGMOID_BW 14  /* (a * b) * (1 - b) */
+#define ORCA_HIP_EW_DIV_BW_RHS 15  /* a * (-b / (c * c)) */
+#define ORCA_HIP_EW_SUM_VISIT 16   /* 0 + a   (sum_to_shape onto the same shape) */
+#define ORCA_HIP_EW_MAX_VISIT 17   /* a > -FLT_MAX ? a : -FLT_MAX   (max_to_shape onto the same shape) */
+#define ORCA_HIP_EW_COPY 18        /* a   (Backend::expand: the broadcast is the input's index map) */
+#define ORCA_HIP_EW_MAX_INPUTS 8
+#define ORCA_HIP_EW_MAX_OUTPUTS 8
+#define ORCA_HIP_EW_MAX_OPS 64
+#define ORCA_HIP_EW_MAX_REGS 16
+
+typedef struct {
+  uint8_t op;       /* ORCA_HIP_EW_* */
+  uint8_t dst;      /* register written */
+  uint8_t a, b, c;  /* registers read (b, c when the op takes them) */
+  uint8_t pad[3];
+  float scalar;     /* ORCA_HIP_EW_MUL_SCALAR's factor */
+} orca_hip_ew_instr;
+
+/* An input of a program: element e of the n reads ptr[(e / div) % mod], so a
+ * plain input has div = 1, mod = n, and a broadcast of a contiguous block of
+ * dims (Backend::expand, orca-backend-cpu/src/backend.rs:466-497: a bias row
+ * [1, N] -> [B, N] is div = 1, mod = N; a column [B, 1] -> [B, N] is div = N,
+ * mod = B; a single value is mod = 1) reads its mod values in place. */
+typedef struct {
+  const float* ptr;
+  uint64_t div, mod;
+} orca_hip_ew_input;
+
+/* Runs one program over n elements: input i is loaded into register i, the
+ * instructions run in order, and output o (n floats) receives register
+ * out_regs[o].  No counterpart in the reference (its backend runs each op as
+ * its own pass); the Backend trait's storages call it. */
+int orca_hip_ew_program(orca_hip_ctx* ctx, size_t n, const orca_hip_ew_input* inputs, size_t n_inputs,
+                        float* const* outputs, const uint8_t* out_regs, size_t n_outputs,
+                        const orca_hip_ew_instr* instrs, size_t n_instrs, size_t n_regs);
+
 /* ===================== fused kernels beyond the trait ===================== */
 /* Buffer-level entry points: the caller owns every output buffer. */
 

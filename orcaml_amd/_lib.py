@@ -128,6 +128,7 @@ SIGNATURES = {
     "orca_hip_softmax_ce": [_P, _P, _SZ, _SZ, _P, _P, _P, _P, _P, _P],
     "orca_hip_head_forward_ce": [_P, _P, _SZ, _SZ, _P, _P, _SZ, _P, _P, _P, _P, _P, _P, _P],
     "orca_hip_head_backward": [_P, _P, _SZ, _SZ, _P, _SZ, _P, _I, _P, _P, _P],
+    "orca_hip_ew_program": [_P, _SZ, _P, _SZ, _P, _P, _SZ, _P, _SZ, _SZ],
     "orca_hip_relu_bw_colsum": [_P, _P, _P, _SZ, _SZ, _P, _P],
     "orca_hip_relu_bw_colsum_noalloc": [_P, _P, _P, _SZ, _SZ, _P, _P],
     "orca_hip_adamw_step": [_P, _P, _P, _P, _P, _SZ, _D, _D, _D, _D, _D, ctypes.c_int64],

@@ -24,11 +24,23 @@ orca-autograd/src/backend.rs:1684-1697, 1448-1499):
   next `matmul(X^T, G)` on that storage computes it inside the product
   (orca_hip_matmul_colsum, the same bits as the sum_to_shape kernel), and any
   other use computes it with the sum_to_shape kernel first.
+
+And elementwise ops are lazy: add ... div_backward_rhs, accumulate_grad and
+the identity sum_to_shape / max_to_shape return a storage holding the op and
+its operands.  The first use that needs its values (any other op, a host
+read, an in-place update of one of its inputs) compiles the pending chain into
+one program of per-element instructions (orca_hip_ew_program): one launch and
+one pass over memory instead of one per op.  Pending values that something
+outside the chain still references (a tape node's saved primal, an optimizer's
+moment) are written by the same launch.  Each instruction is the op's own f32
+operation, so every value has the bits the ops run one by one would give.
 """
 from __future__ import annotations
 
 import ctypes
 import math
+import struct
+import sys
 import weakref
 
 import numpy as np
@@ -37,8 +49,55 @@ from . import _lib
 from .device import Buffer, Context
 
 
+# Elementwise program opcodes (include/orca_hip.h ORCA_HIP_EW_*) and interpreter limits.
+EW_ADD, EW_SUB, EW_MUL, EW_DIV, EW_MUL_SCALAR, EW_RELU, EW_RELU_BW, EW_EXP, EW_LOG, EW_SQRT = range(10)
+EW_SIGMOID, EW_EXP_BW, EW_LOG_BW, EW_SQRT_BW, EW_SIGMOID_BW, EW_DIV_BW_RHS, EW_SUM_VISIT, EW_MAX_VISIT = range(10, 18)
+EW_COPY = 18
+EW_MAX_INPUTS, EW_MAX_OUTPUTS, EW_MAX_OPS, EW_MAX_REGS = 8, 8, 64, 16
+_INSTR = struct.Struct("<BBBBBxxxf")  # orca_hip_ew_instr
+_SCALAR = struct.Struct("<f")  # its scalar field, at byte 8
+
+
+class EwInput(ctypes.Structure):
+    """orca_hip_ew_input: element e of a program reads ptr[(e / div) % mod]."""
+    _fields_ = [("ptr", ctypes.c_void_p), ("div", ctypes.c_uint64), ("mod", ctypes.c_uint64)]
+
+
+class _Broadcast:
+    """A program input that reads `src` broadcast to `n` elements through the index map
+    (e / div) % mod -- Backend::expand of a contiguous block of dims, run in place."""
+
+    __slots__ = ("src", "n", "div", "mod", "_expr", "_ew_ops", "_ew_leaves", "__weakref__")
+
+    def __init__(self, src, n, div, mod):
+        self.src, self.n, self.div, self.mod = src, n, div, mod
+        self._expr, self._ew_ops, self._ew_leaves = None, 0, 1
+
+    @property
+    def ptr(self) -> int:
+        return self.src.ptr
+
+
+def _broadcast_map(in_shape, out_shape):
+    """(div, mod) when expanding in_shape to out_shape reads input element (e / div) % mod for
+    output element e (the input's non-broadcast dims are one contiguous block of the output's),
+    else None."""
+    r = len(out_shape)
+    pin = (1,) * (r - len(in_shape)) + tuple(in_shape)
+    kept = [d for d in range(r) if pin[d] != 1]
+    if any(pin[d] != out_shape[d] for d in kept):
+        return None
+    if not kept:
+        return 1, 1
+    i0, i1 = kept[0], kept[-1] + 1
+    if any(pin[d] == 1 and out_shape[d] != 1 for d in range(i0, i1)):
+        return None
+    return math.prod(out_shape[i1:]), math.prod(out_shape[i0:i1])
+
+
 class HipStorage:
-    __slots__ = ("_buf", "n", "transposed_shape", "_fill", "colsum_waiters", "ident", "__weakref__")
+    __slots__ = ("_buf", "n", "transposed_shape", "_fill", "colsum_waiters", "ident", "_expr", "_ew_ops",
+                 "_ew_leaves", "__weakref__")
 
     def __init__(self, buf: Buffer | None, n: int, transposed_shape=None):
         self._buf = buf
@@ -52,16 +111,23 @@ class HipStorage:
         self.colsum_waiters = None
         # This storage's identity sum_to_shape result, once computed.
         self.ident = None
+        # A pending elementwise op: (backend, opcode, operand storages, scalar), with
+        # upper bounds of the ops and distinct inputs of its pending chain.
+        self._expr = None
+        self._ew_ops = 0
+        self._ew_leaves = 1
 
     def __len__(self) -> int:
         return self.n
 
     @property
     def pending(self) -> bool:
-        return self._fill is not None
+        return self._fill is not None or self._expr is not None
 
     @property
     def buf(self) -> Buffer:
+        if self._expr is not None:
+            self._expr[0]._flush(self)
         if self._fill is not None:
             fill, self._fill = self._fill, None
             fill(self)
@@ -83,11 +149,16 @@ def _numel(shape) -> int:
 class HipBackend:
     """Drop-in for `GpuBackend` (orca-backend-gpu/src/backend.rs:45-50)."""
 
-    def __init__(self, ctx: Context | None = None, deferred: bool = True):
+    def __init__(self, ctx: Context | None = None, deferred: bool = True, lazy: bool = True):
         self.ctx = ctx if ctx is not None else Context(0)
         # The identity-reduction memo and the deferred column sum (module
         # docstring); off, every sum_to_shape runs its kernel at once.
         self.deferred = deferred
+        # Lazy elementwise ops run as fused programs (module docstring); off,
+        # every elementwise op runs its own kernel at once.
+        self.lazy = lazy
+        self._pending = weakref.WeakSet()  # storages holding a pending elementwise op
+        self._programs = {}  # compiled elementwise programs by chain structure
 
     def __repr__(self) -> str:
         return f"HipBackend(device=gpu:{self.ctx.device})"
@@ -206,19 +277,176 @@ class HipBackend:
         _lib.call("orca_hip_transpose", self.ctx.handle, s.ptr, d, r, dim0, dim1, dtype, ctypes.byref(out))
         return self._wrap(out, s.n)
 
+    # ---- lazy elementwise ops ----
+    def _ew(self, op: int, operands, n: int, scalar: float = 0.0) -> HipStorage:
+        """A pending elementwise op over equally long operands (lazy transposes are
+        materialised first).  Operands whose pending chains would push this one past the
+        interpreter's limits are run first."""
+        for o in operands:
+            if type(o) is HipStorage and o.transposed_shape is not None:
+                operands = tuple(o if type(o) is _Broadcast else self._plain(o) for o in operands)
+                break
+        while True:
+            ops, leaves = 1, 0
+            for o in operands:
+                if o._expr is not None:
+                    ops += o._ew_ops
+                    leaves += o._ew_leaves
+                else:
+                    leaves += 1
+            if ops <= EW_MAX_OPS // 2 and leaves <= EW_MAX_INPUTS:
+                break
+            biggest = max((o for o in operands if o._expr is not None), key=lambda o: o._ew_ops)
+            self._flush(biggest)
+        out = HipStorage(None, n)
+        out._expr = (self, op, operands, scalar)
+        out._ew_ops = ops
+        out._ew_leaves = leaves
+        self._pending.add(out)
+        return out
+
+    def _lazy_ok(self, dtype, *operands) -> bool:
+        if not self.lazy or dtype != _lib.F32:
+            return False
+        n = operands[0].n
+        for o in operands:
+            if o.n != n:
+                return False
+        return True
+
+    def _flush(self, root: HipStorage) -> None:
+        """Runs root's pending elementwise chain as one program; pending values in the chain
+        that are referenced from outside it (beyond the chain's own operand links) are
+        written too.  A chain's program (register allocation and instructions) is compiled
+        once per structure -- opcodes, operand slots, outputs -- and reused with the
+        chain's scalars written into it.  Falls back to running the operands' chains first
+        when the program would exceed the interpreter's registers or outputs."""
+        order, leaves, ref, inner, sig, scalars = [], [], {}, {}, [], []
+
+        def visit(node):  # post-order (chains hold at most EW_MAX_OPS / 2 ops)
+            refs = []
+            for c in node._expr[2]:
+                i = ref.get(id(c))
+                if c._expr is None:  # an input: -1, -2, ...
+                    if i is None:
+                        i = ref[id(c)] = -1 - len(leaves)
+                        leaves.append(c)
+                else:
+                    inner[id(c)] = inner.get(id(c), 0) + 1
+                    if i is None:
+                        i = ref[id(c)] = visit(c)
+                refs.append(i)
+            k = len(order)
+            order.append(node)
+            e = node._expr
+            sig.append((e[1], *refs))
+            scalars.append(e[3])
+            return k
+
+        visit(root)
+        visit = None  # the closure refers to itself: break that cycle, which holds the chain's storages
+        # externally referenced: references beyond the chain's links, the `order` list and
+        # getrefcount's own argument
+        out_idx = []
+        for k in range(len(order) - 1):
+            if sys.getrefcount(order[k]) > inner.get(id(order[k]), 0) + 2:
+                out_idx.append(k)
+        out_idx.append(len(order) - 1)  # the root
+        key = (tuple(sig), tuple(out_idx), len(leaves))
+        prog = self._programs.get(key)
+        if prog is None:
+            prog = self._programs[key] = self._compile(sig, out_idx, len(leaves))
+        if prog is False:
+            return self._flush_operands_first(root)
+        instrs, oregs, n_regs, scalar_at, written = prog
+        if scalar_at:
+            cur = [scalars[k] for k in scalar_at]
+            if cur != written:
+                for k, v in zip(scalar_at, cur):
+                    _SCALAR.pack_into(instrs, _INSTR.size * k + 8, v)
+                prog[4] = cur
+        n = root.n
+        bufs = [self.ctx.alloc(4 * max(n, 1)) for _ in out_idx]
+        ins = (EwInput * max(1, len(leaves)))(
+            *[(lf.ptr, lf.div, lf.mod) if type(lf) is _Broadcast else (lf.ptr, 1, n) for lf in leaves])
+        outs = (ctypes.c_void_p * len(out_idx))(*[b.ptr for b in bufs])
+        _lib.call("orca_hip_ew_program", self.ctx.handle, n, ins, len(leaves), outs, oregs, len(out_idx), instrs,
+                  len(order), n_regs)
+        pending = self._pending
+        for k, b in zip(out_idx, bufs):
+            X = order[k]
+            X._buf, X._expr, X._ew_ops, X._ew_leaves = b, None, 0, 1
+            pending.discard(X)
+
+    @staticmethod
+    def _compile(sig, out_idx, n_leaves):
+        """[instructions, output registers, register count, indices of the instructions
+        that carry a scalar, the scalars last written into them] of a chain, or False when
+        it needs more registers or outputs than the interpreter has.  Inputs take registers
+        0..n_leaves-1; each op result takes the lowest free register; a register is freed
+        after its value's last use (an output keeps its register to the end)."""
+        if len(out_idx) > EW_MAX_OUTPUTS or len(sig) > EW_MAX_OPS:
+            return False
+        last = {}
+        for k, (_, *refs) in enumerate(sig):
+            for r in refs:
+                last[r] = k
+        outs = set(out_idx)
+        free, reg, n_regs = [], {}, n_leaves
+        instrs = bytearray()
+        scalar_at = []
+        for k, (op, *refs) in enumerate(sig):
+            regs = [(-1 - r) if r < 0 else reg[r] for r in refs]
+            for r in set(refs):
+                if last[r] == k and (r < 0 or r not in outs):
+                    free.append((-1 - r) if r < 0 else reg[r])
+            if free:
+                free.sort()
+                dst = free.pop(0)
+            else:
+                dst = n_regs
+                n_regs += 1
+            reg[k] = dst
+            regs += [regs[0]] * (3 - len(regs))
+            instrs += _INSTR.pack(op, dst, regs[0], regs[1], regs[2], 0.0)
+            if op == EW_MUL_SCALAR:
+                scalar_at.append(k)
+        if n_regs > EW_MAX_REGS:
+            return False
+        oregs = (ctypes.c_uint8 * len(out_idx))(*[reg[k] for k in out_idx])
+        return [ctypes.create_string_buffer(bytes(instrs), max(1, len(instrs))), oregs, n_regs, scalar_at, None]
+
+    def _flush_operands_first(self, root: HipStorage) -> None:
+        for c in root._expr[2]:
+            if c._expr is not None:
+                self._flush(c)
+        self._flush(root)
+
+    def _unary(self, name, op, s, shape, dtype):
+        if self._lazy_ok(dtype, s):
+            return self._ew(op, (s,), s.n)
+        return self._op1(name, s, shape, dtype)
+
+    def _binary(self, name, op, a, b, shape, dtype):
+        if self._lazy_ok(dtype, a, b):
+            return self._ew(op, (a, b), a.n)
+        return self._op2(name, a, b, shape, dtype)
+
     def add(self, a, b, shape, dtype=_lib.F32):
-        return self._op2("add", a, b, shape, dtype)
+        return self._binary("add", EW_ADD, a, b, shape, dtype)
 
     def sub(self, a, b, shape, dtype=_lib.F32):
-        return self._op2("sub", a, b, shape, dtype)
+        return self._binary("sub", EW_SUB, a, b, shape, dtype)
 
     def mul(self, a, b, shape, dtype=_lib.F32):
-        return self._op2("mul", a, b, shape, dtype)
+        return self._binary("mul", EW_MUL, a, b, shape, dtype)
 
     def div(self, a, b, shape, dtype=_lib.F32):
-        return self._op2("div", a, b, shape, dtype)
+        return self._binary("div", EW_DIV, a, b, shape, dtype)
 
     def mul_scalar(self, s, scalar: float, shape, dtype=_lib.F32):
+        if self._lazy_ok(dtype, s):
+            return self._ew(EW_MUL_SCALAR, (s,), s.n, float(ctypes.c_float(scalar).value))
         s = self._plain(s)
         out = ctypes.c_void_p()
         d, r = _dims(shape)
@@ -227,39 +455,41 @@ class HipBackend:
         return self._wrap(out, _numel(shape))
 
     def relu(self, s, shape, dtype=_lib.F32):
-        return self._op1("relu", s, shape, dtype)
+        return self._unary("relu", EW_RELU, s, shape, dtype)
 
     def sigmoid(self, s, shape, dtype=_lib.F32):
-        return self._op1("sigmoid", s, shape, dtype)
+        return self._unary("sigmoid", EW_SIGMOID, s, shape, dtype)
 
     def exp(self, s, shape, dtype=_lib.F32):
-        return self._op1("exp", s, shape, dtype)
+        return self._unary("exp", EW_EXP, s, shape, dtype)
 
     def log(self, s, shape, dtype=_lib.F32):
-        return self._op1("log", s, shape, dtype)
+        return self._unary("log", EW_LOG, s, shape, dtype)
 
     def sqrt(self, s, shape, dtype=_lib.F32):
-        return self._op1("sqrt", s, shape, dtype)
+        return self._unary("sqrt", EW_SQRT, s, shape, dtype)
 
     def relu_backward(self, g, x, shape, dtype=_lib.F32):
-        return self._op2("relu_backward", g, x, shape, dtype)
+        return self._binary("relu_backward", EW_RELU_BW, g, x, shape, dtype)
 
     def sigmoid_backward(self, g, y, shape, dtype=_lib.F32):
-        return self._op2("sigmoid_backward", g, y, shape, dtype)
+        return self._binary("sigmoid_backward", EW_SIGMOID_BW, g, y, shape, dtype)
 
     def exp_backward(self, g, y, shape, dtype=_lib.F32):
-        return self._op2("exp_backward", g, y, shape, dtype)
+        return self._binary("exp_backward", EW_EXP_BW, g, y, shape, dtype)
 
     def log_backward(self, g, x, shape, dtype=_lib.F32):
-        return self._op2("log_backward", g, x, shape, dtype)
+        return self._binary("log_backward", EW_LOG_BW, g, x, shape, dtype)
 
     def sqrt_backward(self, g, y, shape, dtype=_lib.F32):
-        return self._op2("sqrt_backward", g, y, shape, dtype)
+        return self._binary("sqrt_backward", EW_SQRT_BW, g, y, shape, dtype)
 
     def div_backward_lhs(self, g, r, shape, dtype=_lib.F32):
-        return self._op2("div_backward_lhs", g, r, shape, dtype)
+        return self._binary("div_backward_lhs", EW_DIV, g, r, shape, dtype)
 
     def div_backward_rhs(self, g, l, r, shape, dtype=_lib.F32):
+        if self._lazy_ok(dtype, g, l, r):
+            return self._ew(EW_DIV_BW_RHS, (g, l, r), g.n)
         g, l, r = self._plain(g), self._plain(l), self._plain(r)
         out = ctypes.c_void_p()
         d, rk = _dims(shape)
@@ -267,6 +497,8 @@ class HipBackend:
         return self._wrap(out, _numel(shape))
 
     def accumulate_grad(self, a, b):
+        if self._lazy_ok(_lib.F32, a, b):
+            return self._ew(EW_ADD, (a, b), a.n)
         a, b = self._plain(a), self._plain(b)
         out = ctypes.c_void_p()
         _lib.call("orca_hip_accumulate_grad", self.ctx.handle, a.ptr, b.ptr, a.n, ctypes.byref(out))
@@ -275,14 +507,20 @@ class HipBackend:
     def expand(self, s, in_shape, out_shape, dtype=_lib.F32):
         if tuple(in_shape) == tuple(out_shape) and dtype == _lib.F32:
             return s  # identity broadcast: share the storage
+        if self.lazy and dtype == _lib.F32 and len(out_shape) >= len(in_shape):
+            m = _broadcast_map(tuple(int(d) for d in in_shape), tuple(int(d) for d in out_shape))
+            n = _numel(out_shape)
+            if m is not None and n > 0 and s.n == _numel(in_shape):
+                return self._ew(EW_COPY, (_Broadcast(self._plain(s), n, *m),), n)
         return self._reshape_like("expand", s, in_shape, out_shape, dtype)
 
     def sum_to_shape(self, s, in_shape, out_shape, dtype=_lib.F32):
         in_shape, out_shape = tuple(int(d) for d in in_shape), tuple(int(d) for d in out_shape)
-        if self.deferred and dtype == _lib.F32 and s.transposed_shape is None and not s.pending:
+        if self.deferred and dtype == _lib.F32 and s.transposed_shape is None and s._fill is None:
             if in_shape == out_shape:
                 if s.ident is None:
-                    s.ident = self._reshape_like("sum_to_shape", s, in_shape, out_shape, dtype)
+                    s.ident = (self._ew(EW_SUM_VISIT, (s,), s.n) if self.lazy else
+                               self._reshape_like("sum_to_shape", s, in_shape, out_shape, dtype))
                 return s.ident
             if len(in_shape) == 2 and out_shape in ((1, in_shape[1]), (in_shape[1],)):
                 return self._deferred_colsum(s, in_shape)
@@ -318,10 +556,12 @@ class HipBackend:
         s.colsum_waiters = live or None
         return found
 
-    @staticmethod
-    def _mutating(*storages) -> None:
+    def _mutating(self, *storages) -> None:
         """Before an in-place update: values derived lazily from these storages are computed
         from their current contents, and their memoised identity reductions are dropped."""
+        for node in list(self._pending):
+            if node._expr is not None:
+                node.buf  # runs its pending elementwise chain
         for s in storages:
             if s.colsum_waiters:
                 for ref in s.colsum_waiters:
@@ -340,6 +580,8 @@ class HipBackend:
         return self._plain(s)
 
     def max_to_shape(self, s, in_shape, out_shape, dtype=_lib.F32):
+        if tuple(in_shape) == tuple(out_shape) and self._lazy_ok(dtype, s):
+            return self._ew(EW_MAX_VISIT, (s,), s.n)
         return self._reshape_like("max_to_shape", s, in_shape, out_shape, dtype)
 
     def max_to_shape_backward(self, g, x, y, in_shape, out_shape, dtype=_lib.F32):

@@ -1,0 +1,218 @@
+"""Lazy elementwise ops of HipBackend run as fused programs (orca_hip_ew_program):
+bit-identical to the same trait ops run one kernel at a time
+(orca-backend-cpu/src/backend.rs elementwise semantics), for single ops on
+special values, for random chains with shared subexpressions and values
+referenced from outside the chain, for chains larger than the interpreter's
+registers, across in-place updates of an input, and for whole composed
+training steps."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from orcaml_amd import _lib, synth
+from orcaml_amd import autodiff as A
+from orcaml_amd.backend import HipBackend
+
+pytestmark = pytest.mark.gpu
+
+
+def up(hb, a):
+    a = np.ascontiguousarray(a, np.float32)
+    return hb.from_f32_slice(a.shape, a.reshape(-1))
+
+
+def special(rng, n):
+    x = (rng.standard_normal(n) * 3).astype(np.float32)
+    x[::17] = 0.0
+    x[1::19] = -0.0
+    x[2::23] = np.nan
+    x[3::29] = np.inf
+    x[4::31] = -np.inf
+    x[5::37] = 1e-40
+    return x
+
+
+UNARY = ["relu", "sigmoid", "exp", "log", "sqrt"]
+BINARY = ["add", "sub", "mul", "div", "relu_backward", "sigmoid_backward", "exp_backward", "log_backward",
+          "sqrt_backward", "div_backward_lhs"]
+
+
+@pytest.fixture(scope="module")
+def pair(ctx):
+    return HipBackend(ctx), HipBackend(ctx, lazy=False)
+
+
+@pytest.mark.parametrize("n", [1, 7, 4096, 1000003])
+def test_each_op_bit_identical(pair, n):
+    lazy, eager = pair
+    rng = np.random.default_rng(n)
+    a, b, c = special(rng, n), special(rng, n), special(rng, n)
+    shape = (n,)
+    for be in pair:
+        be._a, be._b, be._c = up(be, a), up(be, b), up(be, c)
+    got, want = {}, {}
+    for be, res in ((lazy, got), (eager, want)):
+        for op in UNARY:
+            res[op] = getattr(be, op)(be._a, shape)
+        for op in BINARY:
+            res[op] = getattr(be, op)(be._a, be._b, shape)
+        res["mul_scalar"] = be.mul_scalar(be._a, -0.37, shape)
+        res["div_backward_rhs"] = be.div_backward_rhs(be._a, be._b, be._c, shape)
+        res["accumulate_grad"] = be.accumulate_grad(be._a, be._b)
+        res["sum_ident"] = be.sum_to_shape(be._b, shape, shape)
+        res["max_ident"] = be.max_to_shape(be._c, shape, shape)
+    assert got["relu"].pending and not want["relu"].pending
+    for k in want:
+        np.testing.assert_array_equal(lazy.to_f32_vec(got[k]), eager.to_f32_vec(want[k]), err_msg=k)
+
+
+def _random_chain(be, leaves, rng, n_ops, keep):
+    """A random DAG of elementwise ops over `leaves`; every `keep`-th value is also
+    returned (held from outside the chain)."""
+    vals = list(leaves)
+    held = []
+    shape = (leaves[0].n,)
+    for k in range(n_ops):
+        pick = lambda: vals[int(rng.integers(0, len(vals)))]  # noqa: E731
+        kind = int(rng.integers(0, 6))
+        if kind == 0:
+            v = be.add(pick(), pick(), shape)
+        elif kind == 1:
+            v = be.mul(pick(), pick(), shape)
+        elif kind == 2:
+            v = be.mul_scalar(pick(), float(rng.standard_normal()), shape)
+        elif kind == 3:
+            v = be.sub(pick(), pick(), shape)
+        elif kind == 4:
+            v = be.relu_backward(pick(), pick(), shape)
+        else:
+            v = be.sqrt(be.add(be.mul(pick(), pick(), shape), pick(), shape), shape)
+        vals.append(v)
+        if keep and k % keep == 0:
+            held.append(v)
+    return vals[-1], held
+
+
+@pytest.mark.parametrize("seed,n_leaves,n_ops,keep", [(1, 2, 5, 0), (2, 4, 20, 3), (3, 8, 40, 2), (4, 3, 60, 1),
+                                                      (5, 6, 120, 7)])
+def test_random_chains_bit_identical(pair, seed, n_leaves, n_ops, keep):
+    """Shared subexpressions, values held from outside (written by the same launch), chains
+    past the interpreter's 16 registers and 64 instructions (run in parts)."""
+    n = 10007
+    out = []
+    for be in pair:
+        rng = np.random.default_rng(seed)
+        leaves = [up(be, rng.standard_normal(n).astype(np.float32)) for _ in range(n_leaves)]
+        root, held = _random_chain(be, leaves, rng, n_ops, keep)
+        out.append([be.to_f32_vec(root)] + [be.to_f32_vec(h) for h in held])
+    for g, w in zip(*out):
+        np.testing.assert_array_equal(g, w)
+
+
+def test_pending_value_survives_in_place_update_of_its_input(pair):
+    """adamw_step_ updates p, m, v in place: a pending op reading p is run first, on the old p."""
+    lazy, _ = pair
+    rng = np.random.default_rng(9)
+    n = 5000
+    p0 = rng.standard_normal(n).astype(np.float32)
+    p, g = up(lazy, p0), up(lazy, rng.standard_normal(n).astype(np.float32))
+    m, v = up(lazy, np.zeros(n, np.float32)), up(lazy, np.zeros(n, np.float32))
+    twice = lazy.mul_scalar(p, 2.0, (n,))
+    assert twice.pending
+    lazy.adamw_step_(p, g, m, v, n, 1e-3, 0.9, 0.999, 1e-8, 0.01, 1)
+    np.testing.assert_array_equal(lazy.to_f32_vec(twice), p0 * np.float32(2.0))
+
+
+def test_one_launch_for_a_chain(pair, ctx):
+    lazy, _ = pair
+    rng = np.random.default_rng(3)
+    n = 1 << 20
+    a, b = up(lazy, rng.standard_normal(n).astype(np.float32)), up(lazy, rng.standard_normal(n).astype(np.float32))
+    ctx.sync()
+    ctx.prof_reset()
+    ctx.prof_enable(True)
+    r = lazy.relu(lazy.add(lazy.mul_scalar(a, 0.5, (n,)), b, (n,)), (n,))
+    lazy.to_f32_vec(r)
+    ctx.prof_enable(False)
+    names = {k["name"]: k["launches"] for k in ctx.prof_report()["kernels"]}
+    assert names == {"ew_program": 1}, names
+
+
+def _composed(hb, dims, params, x, onehot, kind, fused, steps):
+    ad = A.Autodiff(hb)
+    model = A.build_mlp(ad, params)
+    opt = (A.SGD(model.parameters(), lr=0.1, fused=fused) if kind == "sgd" else
+           A.AdamW(model.parameters(), lr=1e-3, weight_decay=0.01, fused=fused))
+    xt, tt = A.Tensor.from_numpy(ad, x), A.Tensor.from_numpy(ad, onehot)
+    losses, grads = [], None
+    for _ in range(steps):
+        opt.zero_grad()
+        loss = A.CrossEntropyLoss(fused=fused)(model(xt), tt)
+        loss.backward()
+        losses.append(loss.to_list()[0])
+        grads = [p.tensor.grad().numpy() for p in model.parameters()]
+        opt.step()
+    return losses, grads, [p.tensor.numpy() for p in model.parameters()]
+
+
+@pytest.mark.parametrize("kind,fused", [("sgd", False), ("adamw", False), ("adamw", True)])
+@pytest.mark.parametrize("dims,batch", [((784, 128, 128, 10), 64), ((784, 1024, 1024, 10), 256)])
+def test_composed_steps_bit_identical(pair, kind, fused, dims, batch):
+    """Three steps of the reference frontend through the tape: lazy fused programs change no bit
+    of the losses, gradients or parameters."""
+    params, x, labels, onehot = synth.mlp_problem(7, dims, batch)
+    runs = [_composed(be, dims, params, x, onehot, kind, fused, 3) for be in pair]
+    (l1, g1, p1), (l2, g2, p2) = runs
+    assert l1 == l2
+    for a, b in zip(g1 + p1, g2 + p2):
+        np.testing.assert_array_equal(a, b)
+
+
+@pytest.mark.parametrize("in_shape,out_shape", [
+    ((1, 4096), (1024, 4096)),  # row broadcast, float4 loads
+    ((1, 1048576), (4, 1048576)),
+    ((1024, 1), (1024, 10)),  # column broadcast, index per element
+    ((1000, 1), (1000, 12)),  # column broadcast, one value per group of 4
+    ((3, 1), (3, 1048579)),  # a large divisor
+    ((1, 1000003), (3, 1000003)),  # a large odd modulus
+    ((1,), (333, 7)), ((1, 1), (4097, 1)),  # one value
+    ((6,), (2, 5, 6)), ((5, 1), (3, 5, 4)), ((1, 10), (64, 10)),
+    ((7, 1, 3), (7, 4, 3))])
+def test_broadcast_expand_bit_identical(pair, in_shape, out_shape):
+    """expand as a program input read through (e / div) % mod (row, column and single-value
+    broadcasts, a middle block, large divisors and moduli, a rank-3 case the map does not
+    cover) equals the expand kernel's result, also when combined with other ops."""
+    lazy, eager = pair
+    rng = np.random.default_rng(sum(out_shape))
+    a = rng.standard_normal(in_shape).astype(np.float32)
+    b = rng.standard_normal(out_shape).astype(np.float32)
+    n = int(np.prod(out_shape))
+    out = []
+    for be in pair:
+        da, db = up(be, a.reshape(-1)), up(be, b.reshape(-1))
+        e = be.expand(da, in_shape, out_shape)
+        out.append((be.to_f32_vec(be.mul(be.add(e, db, out_shape), e, out_shape)), be.to_f32_vec(e)))
+    np.testing.assert_array_equal(out[0][0], out[1][0])
+    np.testing.assert_array_equal(out[0][1], out[1][1])
+    np.testing.assert_array_equal(out[1][1], O.expand(a, out_shape).reshape(n))
+
+
+def test_broadcast_beyond_2_31_elements(pair):
+    """Past 2^31 output elements the program input's index takes the 64-bit division; the
+    expanded sum equals that of the expand kernel (its column-broadcast kernel, another
+    implementation), compared on the device: the sum of squared differences of the
+    2^31 + 10 elements is zero only when every element agrees."""
+    lazy, eager = pair
+    rows = (2 ** 31 + 10) // 3
+    in_shape, out_shape = (rows, 1), (rows, 3)
+    n = rows * 3
+    assert n >= 2 ** 31
+    a = np.random.default_rng(77).standard_normal(rows).astype(np.float32)
+    da = up(lazy, a)
+    got = lazy.add(lazy.expand(da, in_shape, out_shape), lazy.expand(da, in_shape, out_shape), out_shape)
+    want = eager.add(eager.expand(da, in_shape, out_shape), eager.expand(da, in_shape, out_shape), out_shape)
+    d = eager.sub(got, want, out_shape)
+    ss = eager.sum_to_shape(eager.mul(d, d, out_shape), out_shape, (1,))
+    assert eager.to_f32_vec(ss)[0] == 0.0
