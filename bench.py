@@ -6,10 +6,13 @@ one-hot targets), batch 1024, f32, one forward + backward + AdamW(1e-3, wd
 already resident in HBM.  Prints ONE JSON line (see the keys below).
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--no-secondary]
-                  [--batch B]
+                  [--batch B] [--workload NAME] [--path trainer|composed|composed-fused]
+                  [--sustained-s S]
 
 --batch measures one GPU's share of the 1024-row batch under data parallelism
-(512, 256, 128 rows); the default is the benchmark workload itself.
+(512, 256, 128 rows); the default is the benchmark workload itself.  --workload
+and --path step another configuration or the drop-in path instead (for
+profiling them); the defaults are the benchmark.
 
 `roofline` reports the dominant kernel (largest device time per step; GEMMs
 are told apart by shape): achieved = algorithmic work per launch / mean launch
@@ -38,10 +41,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 if HERE not in sys.path:
     sys.path.insert(0, HERE)
 
-DIMS = (784, 4096, 4096, 10)
-BATCH = 1024
 OPT = dict(kind="adamw", lr=1e-3, weight_decay=0.01, betas=(0.9, 0.999), eps=1e-8)
-SEED = 3
 # MI355X published peaks.
 PEAK_FP32_MFMA_TFLOPS = 157.3
 PEAK_HBM_GBS = 8000.0
@@ -67,20 +67,23 @@ def cpu_model() -> str:
     return platform.processor() or "unknown"
 
 
-def cpu_baseline(params, x, onehot, target_s: float = 8.0) -> dict:
+def cpu_baseline(dims, params, x, onehot, o=OPT, target_s: float = 8.0) -> dict:
     """Reference-semantics CPU steps of the same workload (the C oracle): one
     untimed warm-up step, then whole steps until about `target_s` seconds."""
     threads = len(os.sched_getaffinity(0))
     os.environ.setdefault("OMP_NUM_THREADS", str(threads))
     from oracle import oracle as O
 
-    opt = O.make_opt("adamw", OPT["lr"], OPT["weight_decay"], OPT["betas"], OPT["eps"])
-    r = O.mlp_train(DIMS, params, x, onehot, opt, steps=1, want_grads=False)  # warm-up (page-in, allocation)
+    if o["kind"] == "adamw":
+        opt = O.make_opt("adamw", o["lr"], o.get("weight_decay", 0.0), o.get("betas", (0.9, 0.999)), o.get("eps", 1e-8))
+    else:
+        opt = O.make_opt(o["kind"], o["lr"])
+    r = O.mlp_train(dims, params, x, onehot, opt, steps=1, want_grads=False)  # warm-up (page-in, allocation)
     state = dict(m=r["m"], v=r["v"], t=r["t"])
     cur = r["params"]
     steps, t0 = 0, time.perf_counter()
     while True:
-        r = O.mlp_train(DIMS, cur, x, onehot, opt, steps=1, m=state["m"], v=state["v"], t=state["t"], want_grads=False)
+        r = O.mlp_train(dims, cur, x, onehot, opt, steps=1, m=state["m"], v=state["v"], t=state["t"], want_grads=False)
         cur, state = r["params"], dict(m=r["m"], v=r["v"], t=r["t"])
         steps += 1
         dt = time.perf_counter() - t0
@@ -91,7 +94,7 @@ def cpu_baseline(params, x, onehot, target_s: float = 8.0) -> dict:
         "unit": "steps/s",
         "cores": O.num_threads(),
         "kind": "port",
-        "sample": f"{steps} full fwd+bwd+AdamW steps of the same workload after 1 warm-up step ({dt:.1f} s wall); "
+        "sample": f"{steps} full fwd+bwd+{o['kind']} steps of the same workload after 1 warm-up step ({dt:.1f} s wall); "
                   f"C oracle restating orca-backend-cpu (single-threaded packed sgemm as matrixmultiply without "
                   f"threading, OpenMP elementwise ops as rayon), CPU: {cpu_model()}",
         "samples_per_s": x.shape[0] * steps / dt,
@@ -229,16 +232,46 @@ def secondary(ctx) -> dict:
     return out
 
 
+def _composed_step(ctx, dims, batch, o, params, x, onehot, fused: bool):
+    """One step of the drop-in path: the reference frontend (nn.Sequential of Linear/ReLU,
+    CrossEntropyLoss, SGD/AdamW) and the autodiff tape over HipBackend's trait ops."""
+    from orcaml_amd import autodiff as A
+    from orcaml_amd.backend import HipBackend
+
+    ad = A.Autodiff(HipBackend(ctx))
+    model = A.build_mlp(ad, params)
+    if o["kind"] == "adamw":
+        opt = A.AdamW(model.parameters(), lr=o["lr"], weight_decay=o.get("weight_decay", 0.0), fused=fused)
+    else:
+        opt = A.SGD(model.parameters(), lr=o["lr"], fused=fused)
+    xt, tt = A.Tensor.from_numpy(ad, x), A.Tensor.from_numpy(ad, onehot)
+
+    def step():
+        opt.zero_grad()
+        A.CrossEntropyLoss(fused=fused)(model(xt), tt).backward()
+        opt.step()
+
+    return step
+
+
 def main() -> int:
+    from orcaml_amd import synth
+
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=30)  # 5 warm-up steps left the first timed ones ~1 % slower
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true", help="skip the other workloads' measurements")
-    ap.add_argument("--batch", type=int, default=BATCH,
-                    help="rows per step (default 1024, the benchmark workload; 512 / 256 / 128 are one GPU's "
-                         "share of that batch under 2 / 4 / 8-way data parallelism)")
+    ap.add_argument("--workload", default=synth.MLP_LARGE, choices=sorted(synth.WORKLOADS),
+                    help="the MLP configuration stepped (default: the benchmark workload)")
+    ap.add_argument("--path", default="trainer", choices=("trainer", "composed", "composed-fused"),
+                    help="trainer: the device-resident training step (the benchmark); composed: the reference "
+                         "frontend and tape over the trait ops; composed-fused: the same with the opt-in fused "
+                         "loss and optimizer")
+    ap.add_argument("--batch", type=int, default=None,
+                    help="rows per step (default: the workload's; for the benchmark workload 512 / 256 / 128 are "
+                         "one GPU's share of its 1024-row batch under 2 / 4 / 8-way data parallelism)")
     ap.add_argument("--sustained-s", type=float, default=3.0,
                     help="after the timed steps, keep stepping for about this many seconds and report that rate "
                          "too (a window long enough for an outside observer of the GPU); 0 skips it")
@@ -251,12 +284,14 @@ def main() -> int:
               file=sys.stderr)
         return 2
 
-    from orcaml_amd import synth
     from orcaml_amd.device import Context
     from orcaml_amd.mlp import MLPTrainer
 
-    batch = args.batch
-    params, x, labels, onehot = synth.mlp_problem(SEED, DIMS, batch)
+    w = synth.WORKLOADS[args.workload]
+    dims, seed = tuple(w["dims"]), w["seed"]
+    o = dict(OPT) if args.workload == synth.MLP_LARGE else dict(w["opt"])
+    batch = args.batch if args.batch is not None else w["batch"]
+    params, x, labels, onehot = synth.mlp_problem(seed, dims, batch)
     ctx = Context(0)
     if args.copy_probe_mib > 0:
         nbytes = args.copy_probe_mib << 20
@@ -266,14 +301,19 @@ def main() -> int:
         ctx.sync()
         src.free()
         dst.free()
-    tr = MLPTrainer(ctx, DIMS, batch, kind=OPT["kind"], lr=OPT["lr"], weight_decay=OPT["weight_decay"],
-                    betas=OPT["betas"], eps=OPT["eps"])
-    tr.set_params(params)
-    tr.set_batch(x, onehot=onehot)
+    tr = None
+    if args.path == "trainer":
+        tr = MLPTrainer(ctx, dims, batch, kind=o["kind"], lr=o["lr"], weight_decay=o.get("weight_decay", 0.0),
+                        betas=o.get("betas", (0.9, 0.999)), eps=o.get("eps", 1e-8))
+        tr.set_params(params)
+        tr.set_batch(x, onehot=onehot)
+        step = tr.step
+    else:
+        step = _composed_step(ctx, dims, batch, o, params, x, onehot, fused=args.path == "composed-fused")
     mallocs_before = None
 
     for _ in range(args.warmup):
-        tr.step()
+        step()
     ctx.sync()
     mallocs_before = ctx.mem_stats()["device_allocs"]
 
@@ -281,10 +321,10 @@ def main() -> int:
     ctx.sync()
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        tr.step()
+        step()
     ctx.sync()
     wall = time.perf_counter() - t0
-    loss, correct = tr.metrics()
+    loss, correct = tr.metrics() if tr is not None else (None, None)
     mallocs_after = ctx.mem_stats()["device_allocs"]
 
     # ---- sustained: the same step for about --sustained-s seconds, in rounds of 100 ----
@@ -293,7 +333,7 @@ def main() -> int:
         done, t0 = 0, time.perf_counter()
         while True:
             for _ in range(100):
-                tr.step()
+                step()
             done += 100
             ctx.sync()
             elapsed = time.perf_counter() - t0
@@ -306,7 +346,7 @@ def main() -> int:
     ctx.prof_reset()
     ctx.prof_enable(True)
     for _ in range(args.steps):
-        tr.step()
+        step()
     report = ctx.prof_report()
     ctx.prof_enable(False)
     kernels = report["kernels"]
@@ -332,7 +372,7 @@ def main() -> int:
     # HBM bytes per launch of this kernel from the committed rocprofv3 FETCH_SIZE + WRITE_SIZE passes
     # (calibrated against a copy of known size); null when the kernel has no such record.
     traffic_file = os.path.join("profiles", "hbm_traffic_mlp784-4096-4096-10_b1024.json")
-    if os.path.exists(os.path.join(HERE, traffic_file)):
+    if args.path == "trainer" and os.path.exists(os.path.join(HERE, traffic_file)):
         with open(os.path.join(HERE, traffic_file)) as fh:
             rec = json.load(fh)["kernels"].get(dominant["name"])
         if rec is not None:
@@ -344,9 +384,9 @@ def main() -> int:
 
     ms_per_step = wall * 1e3 / args.steps
     steps_per_s = args.steps / wall
-    flops = step_flops(DIMS, batch)
+    flops = step_flops(dims, batch)
     out = {
-        "metric": f"MLP train steps/s (784-4096-4096-10 fp32, B={batch}); % fp32 MFMA peak",
+        "metric": f"MLP train steps/s ({'-'.join(str(d) for d in dims)} fp32, B={batch}); % fp32 MFMA peak",
         "value": steps_per_s,
         "unit": "steps/s",
         "n_gpus": 1,
@@ -358,8 +398,8 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic",
-        "config": {"workload": "mlp_train_step", "dims": list(DIMS), "batch": batch, "optimizer": "adamw",
-                   "lr": OPT["lr"], "weight_decay": OPT["weight_decay"], "seed": SEED},
+        "config": {"workload": "mlp_train_step", "dims": list(dims), "batch": batch, "optimizer": o["kind"],
+                   "lr": o["lr"], "weight_decay": o.get("weight_decay", 0.0), "seed": seed, "path": args.path},
         "samples_per_s": steps_per_s * batch,
         "step_tflops": flops * steps_per_s / 1e12,
         "step_frac_fp32_mfma_peak": flops * steps_per_s / 1e12 / PEAK_FP32_MFMA_TFLOPS,
@@ -371,11 +411,13 @@ def main() -> int:
         "roofline": roof,
         "sustained": sustained,
     }
-    tr.close()
+    if tr is not None:
+        tr.close()
+    step = None
     if not args.no_secondary:
         out["secondary"] = secondary(ctx)
     if not args.no_cpu_baseline:
-        out["cpu_baseline"] = cpu_baseline(params, x, onehot)
+        out["cpu_baseline"] = cpu_baseline(dims, params, x, onehot, o)
         out["gpu_over_cpu"] = steps_per_s / out["cpu_baseline"]["value"]
     print(json.dumps(out))
     ctx.close()
