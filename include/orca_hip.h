@@ -248,6 +248,29 @@ int orca_hip_ew_program(orca_hip_ctx* ctx, size_t n, const orca_hip_ew_input* in
                         float* const* outputs, const uint8_t* out_regs, size_t n_outputs,
                         const orca_hip_ew_instr* instrs, size_t n_instrs, size_t n_regs);
 
+/* Run-time compilation of fused programs.  No counterpart in the reference:
+ * controls for callers that want to choose or observe how programs run.  A
+ * program structure that recurs (same opcodes, operand registers, outputs and
+ * input accesses; scalars and sizes may differ) is compiled by hipRTC into a
+ * straight-line kernel with the same per-element functions, so the results
+ * are the interpreter's bit for bit.  mode 0: interpret every program; 1
+ * (default, or ORCA_HIP_EW_JIT at context creation): compile a structure at
+ * its second use; 2: at its first.  Without hipRTC, or when a compile fails,
+ * the structure stays on the interpreter. */
+int orca_hip_ew_set_jit(orca_hip_ctx* ctx, int mode);
+/* Launches so far on the interpreter and on compiled kernels, structures
+ * compiled, and compiles that failed (any output may be null). */
+int orca_hip_ew_jit_stats(orca_hip_ctx* ctx, uint64_t* interpreted, uint64_t* compiled_launches,
+                          uint64_t* compiles, uint64_t* failures);
+/* The HIP source compiled for a program over n elements (inputs' pointers are
+ * not read), NUL-terminated into buf (len bytes; *needed = its full size + 1),
+ * and the text of the functor header it includes as "ew_ops.hpp".  Needs no
+ * GPU. */
+int orca_hip_ew_jit_source(size_t n, const orca_hip_ew_input* inputs, size_t n_inputs, const uint8_t* out_regs,
+                           size_t n_outputs, const orca_hip_ew_instr* instrs, size_t n_instrs, size_t n_regs,
+                           char* buf, size_t len, size_t* needed);
+int orca_hip_ew_jit_headers(const char** ew_ops_text);
+
 /* ===================== fused kernels beyond the trait ===================== */
 /* Buffer-level entry points: the caller owns every output buffer. */
 

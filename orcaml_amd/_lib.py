@@ -129,6 +129,11 @@ SIGNATURES = {
     "orca_hip_head_forward_ce": [_P, _P, _SZ, _SZ, _P, _P, _SZ, _P, _P, _P, _P, _P, _P, _P],
     "orca_hip_head_backward": [_P, _P, _SZ, _SZ, _P, _SZ, _P, _I, _P, _P, _P],
     "orca_hip_ew_program": [_P, _SZ, _P, _SZ, _P, _P, _SZ, _P, _SZ, _SZ],
+    "orca_hip_ew_set_jit": [_P, ctypes.c_int],
+    "orca_hip_ew_jit_stats": [_P, ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64),
+                              ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64)],
+    "orca_hip_ew_jit_source": [_SZ, _P, _SZ, _P, _SZ, _P, _SZ, _SZ, ctypes.c_char_p, _SZ, ctypes.POINTER(_SZ)],
+    "orca_hip_ew_jit_headers": [ctypes.POINTER(ctypes.c_char_p)],
     "orca_hip_relu_bw_colsum": [_P, _P, _P, _SZ, _SZ, _P, _P],
     "orca_hip_relu_bw_colsum_noalloc": [_P, _P, _P, _SZ, _SZ, _P, _P],
     "orca_hip_adamw_step": [_P, _P, _P, _P, _P, _SZ, _D, _D, _D, _D, _D, ctypes.c_int64],

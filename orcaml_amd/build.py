@@ -29,9 +29,23 @@ COMMON_FLAGS = [
 ]
 
 
+def _embed_ew_ops() -> None:
+    """ew_ops.hpp's text as a C++ raw string literal (_build/ew_ops_text.inc): ewprog.hip
+    hands it to hipRTC, so run-time compiled programs use the same functors."""
+    with open(os.path.join(CSRC, "ew_ops.hpp")) as fh:
+        text = fh.read()
+    if ")EWOPS\"" in text:
+        raise RuntimeError("ew_ops.hpp contains the raw-string delimiter")
+    inc = 'R"EWOPS(' + text + ')EWOPS"\n'
+    path = os.path.join(BUILD_DIR, "ew_ops_text.inc")
+    if not os.path.exists(path) or open(path).read() != inc:
+        with open(path, "w") as fh:
+            fh.write(inc)
+
+
 def _compile(src: str) -> str:
     obj = os.path.join(BUILD_DIR, src.replace(".", "_") + ".o")
-    cmd = [HIPCC, *COMMON_FLAGS, "-c", os.path.join(CSRC, src), "-o", obj]
+    cmd = [HIPCC, *COMMON_FLAGS, "-I", BUILD_DIR, "-c", os.path.join(CSRC, src), "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{r.stderr}")
@@ -41,10 +55,11 @@ def _compile(src: str) -> str:
 def build(verbose: bool = False) -> str:
     """Compiles every HIP source and links the shared library; returns its path."""
     os.makedirs(BUILD_DIR, exist_ok=True)
+    _embed_ew_ops()
     with ThreadPoolExecutor(max_workers=min(len(SOURCES), os.cpu_count() or 1)) as ex:
         objs = list(ex.map(_compile, SOURCES))
     tmp = LIB_PATH + ".tmp"
-    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs, "-ldl"]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stderr}")

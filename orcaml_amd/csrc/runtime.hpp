@@ -152,6 +152,8 @@ struct Profiler {
   ~Profiler();
 };
 
+struct EwJitCache;
+
 }  // namespace orca_hip
 
 struct orca_hip_ctx {
@@ -174,9 +176,17 @@ struct orca_hip_ctx {
   // Host waits on this context's work so far (stream or event synchronisations).
   std::atomic<uint64_t> host_syncs{0};
   orca_hip::StagingRing staging;
+  // Fused elementwise programs compiled at run time (ewprog.hip), released with
+  // the context.  ORCA_HIP_EW_JIT (or orca_hip_ew_set_jit): 0 interprets every
+  // program, 1 compiles a program structure at its second use, 2 at its first.
+  orca_hip::EwJitCache* ew_jit = nullptr;
+  int ew_jit_mode = 1;
 };
 
 namespace orca_hip {
+
+// Unloads the context's compiled elementwise programs (ewprog.hip).
+void ew_jit_release(orca_hip_ctx* ctx);
 
 // Makes ctx's device current for the calling thread.
 void bind(orca_hip_ctx* ctx);

@@ -53,6 +53,17 @@ class Context:
     def sync(self) -> None:
         _lib.call("orca_hip_sync", self.handle)
 
+    def set_ew_jit(self, mode: int) -> None:
+        """How fused elementwise programs run (orca_hip_ew_set_jit): 0 interpreted, 1 compiled
+        at a structure's second use (the default), 2 at its first."""
+        _lib.call("orca_hip_ew_set_jit", self.handle, int(mode))
+
+    def ew_jit_stats(self) -> dict:
+        """Interpreted and compiled launches, structures compiled, failed compiles."""
+        v = [ctypes.c_uint64() for _ in range(4)]
+        _lib.call("orca_hip_ew_jit_stats", self.handle, *[ctypes.byref(x) for x in v])
+        return dict(zip(("interpreted", "compiled_launches", "compiles", "failures"), (x.value for x in v)))
+
     def sync_count(self) -> int:
         """Host waits on this context's work so far (orca_hip_sync_count)."""
         n = ctypes.c_uint64()

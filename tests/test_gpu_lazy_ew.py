@@ -44,8 +44,25 @@ def pair(ctx):
     return HipBackend(ctx), HipBackend(ctx, lazy=False)
 
 
+@pytest.fixture(params=[0, 2], ids=["interpreted", "compiled"])
+def jit(request, ctx):
+    """Runs the test with every program interpreted, then with every program compiled at
+    its first use (orca_hip_ew_set_jit); the compiled run must not fall back."""
+    before = ctx.ew_jit_stats()
+    ctx.set_ew_jit(request.param)
+    yield request.param
+    ctx.set_ew_jit(1)
+    after = ctx.ew_jit_stats()
+    assert after["failures"] == before["failures"]
+    if request.param == 2:
+        assert after["compiled_launches"] > before["compiled_launches"]
+        assert after["interpreted"] == before["interpreted"]
+    else:
+        assert after["compiled_launches"] == before["compiled_launches"]
+
+
 @pytest.mark.parametrize("n", [1, 7, 4096, 1000003])
-def test_each_op_bit_identical(pair, n):
+def test_each_op_bit_identical(pair, jit, n):
     lazy, eager = pair
     rng = np.random.default_rng(n)
     a, b, c = special(rng, n), special(rng, n), special(rng, n)
@@ -97,7 +114,7 @@ def _random_chain(be, leaves, rng, n_ops, keep):
 
 @pytest.mark.parametrize("seed,n_leaves,n_ops,keep", [(1, 2, 5, 0), (2, 4, 20, 3), (3, 8, 40, 2), (4, 3, 60, 1),
                                                       (5, 6, 120, 7)])
-def test_random_chains_bit_identical(pair, seed, n_leaves, n_ops, keep):
+def test_random_chains_bit_identical(pair, jit, seed, n_leaves, n_ops, keep):
     """Shared subexpressions, values held from outside (written by the same launch), chains
     past the interpreter's 16 registers and 64 instructions (run in parts)."""
     n = 10007
@@ -140,6 +157,33 @@ def test_one_launch_for_a_chain(pair, ctx):
     assert names == {"ew_program": 1}, names
 
 
+def test_structures_compile_at_their_second_use_and_share_kernels_across_scalars(pair, ctx):
+    """Default mode: a chain's first run is interpreted, its second compiles the structure and
+    runs the compiled kernel; a third run with other scalars and another length reuses it.
+    Every run equals the ops run one by one."""
+    lazy, eager = pair
+    ctx.set_ew_jit(1)
+    rng = np.random.default_rng(21)
+    runs = [(4099, 0.5, -1.25), (4099, 0.75, 2.0), (1 << 16, -3.0, 0.125)]
+    deltas = []
+    for n, s1, s2 in runs:
+        a, b = rng.standard_normal(n).astype(np.float32), rng.standard_normal(n).astype(np.float32)
+        out = []
+        before = ctx.ew_jit_stats()
+        for be in pair:
+            # a structure no other test builds: sigmoid_backward of a scaled sum, then relu
+            x, y = up(be, a), up(be, b)
+            r = be.relu(be.sigmoid_backward(be.mul_scalar(be.add(x, y, (n,)), s1, (n,)), be.mul_scalar(y, s2, (n,)),
+                                            (n,)), (n,))
+            out.append(be.to_f32_vec(r))
+        after = ctx.ew_jit_stats()
+        deltas.append({k: after[k] - before[k] for k in after})
+        np.testing.assert_array_equal(out[0], out[1])
+    assert deltas[0] == {"interpreted": 1, "compiled_launches": 0, "compiles": 0, "failures": 0}
+    assert deltas[1] == {"interpreted": 0, "compiled_launches": 1, "compiles": 1, "failures": 0}
+    assert deltas[2] == {"interpreted": 0, "compiled_launches": 1, "compiles": 0, "failures": 0}
+
+
 def _composed(hb, dims, params, x, onehot, kind, fused, steps):
     ad = A.Autodiff(hb)
     model = A.build_mlp(ad, params)
@@ -159,7 +203,7 @@ def _composed(hb, dims, params, x, onehot, kind, fused, steps):
 
 @pytest.mark.parametrize("kind,fused", [("sgd", False), ("adamw", False), ("adamw", True)])
 @pytest.mark.parametrize("dims,batch", [((784, 128, 128, 10), 64), ((784, 1024, 1024, 10), 256)])
-def test_composed_steps_bit_identical(pair, kind, fused, dims, batch):
+def test_composed_steps_bit_identical(pair, jit, kind, fused, dims, batch):
     """Three steps of the reference frontend through the tape: lazy fused programs change no bit
     of the losses, gradients or parameters."""
     params, x, labels, onehot = synth.mlp_problem(7, dims, batch)
@@ -180,7 +224,7 @@ def test_composed_steps_bit_identical(pair, kind, fused, dims, batch):
     ((1,), (333, 7)), ((1, 1), (4097, 1)),  # one value
     ((6,), (2, 5, 6)), ((5, 1), (3, 5, 4)), ((1, 10), (64, 10)),
     ((7, 1, 3), (7, 4, 3))])
-def test_broadcast_expand_bit_identical(pair, in_shape, out_shape):
+def test_broadcast_expand_bit_identical(pair, jit, in_shape, out_shape):
     """expand as a program input read through (e / div) % mod (row, column and single-value
     broadcasts, a middle block, large divisors and moduli, a rank-3 case the map does not
     cover) equals the expand kernel's result, also when combined with other ops."""
@@ -199,7 +243,7 @@ def test_broadcast_expand_bit_identical(pair, in_shape, out_shape):
     np.testing.assert_array_equal(out[1][1], O.expand(a, out_shape).reshape(n))
 
 
-def test_broadcast_beyond_2_31_elements(pair):
+def test_broadcast_beyond_2_31_elements(pair, jit):
     """Past 2^31 output elements the program input's index takes the 64-bit division; the
     expanded sum equals that of the expand kernel (its column-broadcast kernel, another
     implementation), compared on the device: the sum of squared differences of the
