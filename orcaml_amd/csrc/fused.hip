@@ -218,7 +218,9 @@ constexpr int kRowsPerChunk = 64;  // rows per column-sum partial of the ReLU-ba
 
 // dpre = pre > 0 ? g : 0 and per-chunk column partial sums (4 columns per
 // thread).  Rows go RB_UNROLL at a time, all loads issued before any use;
-// g, pre and dpre are streamed with non-temporal accesses.
+// g and pre are read with ordinary loads, dpre is written with non-temporal
+// stores ([8192, 4096]: 62.0 us against 67.8 with non-temporal loads too,
+// 77.1 with ordinary stores too).
 constexpr int RB_UNROLL = 8;
 
 __global__ void __launch_bounds__(256) relu_bw_colsum_vec_kernel(const float4* __restrict__ g, const float4* __restrict__ pre,
@@ -238,8 +240,8 @@ __global__ void __launch_bounds__(256) relu_bw_colsum_vec_kernel(const float4* _
     for (int u = 0; u < RB_UNROLL; ++u) {
       const size_t r = rb + u;
       if (r < r1) {
-        ga[u] = __builtin_nontemporal_load(gv + r * cols4 + c);
-        pa[u] = __builtin_nontemporal_load(pv + r * cols4 + c);
+        ga[u] = gv[r * cols4 + c];
+        pa[u] = pv[r * cols4 + c];
       }
     }
 #pragma unroll
