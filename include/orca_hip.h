@@ -350,6 +350,25 @@ int orca_hip_adamw_step(orca_hip_ctx* ctx, float* p, const float* g, float* m, f
 /* One vanilla SGD step p -= f32(lr) * g (python/orca/optim/sgd.py:74-79). */
 int orca_hip_sgd_step(orca_hip_ctx* ctx, float* p, const float* g, size_t n, double lr);
 
+/* The optimizer's loop over parameters (python/orca/optim/adamw.py:66-99,
+ * sgd.py:46-79) as one launch per ORCA_HIP_OPT_MAX_SEGMENTS parameters: each
+ * segment reads p_src and g (and m, v for AdamW) and writes p_dst (which may be
+ * p_src) and m, v in place, with the per-element arithmetic of
+ * orca_hip_adamw_step / orca_hip_sgd_step, so the same bits.  Segments must
+ * not overlap one another.  m and v are ignored by SGD. */
+#define ORCA_HIP_OPT_MAX_SEGMENTS 32
+typedef struct {
+  const float* p_src;
+  float* p_dst;
+  const float* g;
+  float* m;
+  float* v;
+  size_t n;
+} orca_hip_opt_segment;
+int orca_hip_adamw_multi(orca_hip_ctx* ctx, const orca_hip_opt_segment* segs, size_t n_segs, double lr, double beta1,
+                         double beta2, double eps, double weight_decay, int64_t t);
+int orca_hip_sgd_multi(orca_hip_ctx* ctx, const orca_hip_opt_segment* segs, size_t n_segs, double lr);
+
 /* ===================== device-resident MLP training step ===================== */
 /* nn.Sequential(Linear, ReLU, ..., Linear) + CrossEntropyLoss + SGD/AdamW
  * (python/orca/nn/{linear,activation,container,loss}.py, python/orca/optim)

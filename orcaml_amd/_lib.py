@@ -130,6 +130,9 @@ SIGNATURES = {
     "orca_hip_head_backward": [_P, _P, _SZ, _SZ, _P, _SZ, _P, _I, _P, _P, _P],
     "orca_hip_ew_program": [_P, _SZ, _P, _SZ, _P, _P, _SZ, _P, _SZ, _SZ],
     "orca_hip_ew_set_jit": [_P, ctypes.c_int],
+    "orca_hip_adamw_multi": [_P, _P, _SZ, ctypes.c_double, ctypes.c_double, ctypes.c_double, ctypes.c_double,
+                             ctypes.c_double, ctypes.c_int64],
+    "orca_hip_sgd_multi": [_P, _P, _SZ, ctypes.c_double],
     "orca_hip_ew_jit_stats": [_P, ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64),
                               ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64)],
     "orca_hip_ew_jit_source": [_SZ, _P, _SZ, _P, _SZ, _P, _SZ, _SZ, ctypes.c_char_p, _SZ, ctypes.POINTER(_SZ)],
@@ -191,6 +194,15 @@ def check(rc: int) -> None:
 
 
 _FNS: dict = {}
+
+
+class OptSegment(ctypes.Structure):
+    """orca_hip_opt_segment."""
+    _fields_ = [("p_src", ctypes.c_void_p), ("p_dst", ctypes.c_void_p), ("g", ctypes.c_void_p),
+                ("m", ctypes.c_void_p), ("v", ctypes.c_void_p), ("n", ctypes.c_size_t)]
+
+
+OPT_MAX_SEGMENTS = 32
 
 
 def call(name: str, *args) -> None:

@@ -23,6 +23,7 @@ from __future__ import annotations
 
 import contextlib
 import math
+import sys
 from typing import Iterable
 
 import numpy as np
@@ -715,22 +716,99 @@ class Optimizer:
         self.parameters[0].tensor.ad.tape.clear()
 
 
+class _FlatParams:
+    """The parameters of a fused optimizer in flat device arenas, each parameter's storage a
+    view of its slice, so one launch updates all of them (orca_hip_adamw_multi /
+    orca_hip_sgd_multi).
+
+    Every step reads the arena that holds the parameters and writes the other, and the
+    parameters are then rebound to views of the written one: a storage of the previous
+    values (a forward's tape, a pending op, the caller) keeps them unchanged, as the
+    reference's functional update does.  The arena written is the one from two steps back
+    only when no view of it is still referenced; otherwise a fresh arena is taken.  The
+    moments live in two more arenas, updated in place (they belong to the optimizer)."""
+
+    ALIGN = 64  # floats: 256-byte aligned slices
+
+    def __init__(self, ad: "Autodiff", params, moments: bool):
+        self.ad, self.be = ad, ad.inner
+        self.params = params
+        self.sizes = [_numel(p.tensor.shape) for p in params]
+        self.offs, total = [], 0
+        for n in self.sizes:
+            self.offs.append(total)
+            total += -(-n // self.ALIGN) * self.ALIGN
+        self.total = total
+        self.cur = self.be.arena(total)
+        self.spare = None
+        # The parameters move into the arena with their values: each tensor keeps its
+        # identity and node id (a gradient already recorded for it stays attached); only
+        # its storage becomes the arena slice.
+        for p, off, n in zip(params, self.offs, self.sizes):
+            view = self.be.view(self.cur, off, n)
+            self.be.copy_into(view, p.tensor.storage.primal)
+            p.tensor.storage.primal = view
+        self.m = self.v = None
+        if moments:
+            self.m, self.v = self.be.arena(total, 0.0), self.be.arena(total, 0.0)
+
+    def moment(self, which: str, i: int):
+        return self.be.view(self.m if which == "m" else self.v, self.offs[i], self.sizes[i])
+
+    def step(self, run) -> None:
+        """run(segments) launches the update; segments are (i, p_src, p_dst, g) of the
+        parameters with a gradient.  Parameters without one are copied across."""
+        # Every view (and every storage derived from one: a lazy transpose, a pending op's
+        # operand) holds a reference to its arena, so an arena referenced only from here
+        # and by getrefcount's argument has no reader left.
+        if self.spare is not None and sys.getrefcount(self.spare) <= 2:
+            dst = self.spare
+        else:
+            dst = self.be.arena(self.total)
+        self.spare = None
+        segs, rebind = [], []
+        for i, p in enumerate(self.params):
+            src = p.tensor.storage.primal
+            view = self.be.view(dst, self.offs[i], self.sizes[i])
+            g = p.tensor.grad() if p.tensor.requires_grad else None
+            if g is None:
+                self.be.copy_into(view, src)
+            else:
+                segs.append((i, src, view, g.storage.primal))
+            rebind.append((p, view))
+        if segs:
+            run(segs)
+        for p, view in rebind:
+            p.update(_new_leaf(self.ad, view, p.tensor.shape))
+        self.spare, self.cur = self.cur, dst
+
+
 class SGD(Optimizer):
     """python/orca/optim/sgd.py:10-79.
 
-    fused=True (opt-in): with momentum = weight_decay = 0 and a backend that
-    has sgd_step_, each parameter's update p - g * f32(lr) is one kernel on
-    a copy of p (the old tensor is left as it was, as the composed update
-    leaves it); the same f32 operations, so the same bits."""
+    fused=True (opt-in): with momentum = weight_decay = 0, the update
+    p - g * f32(lr) of all parameters is one launch over flat parameter
+    arenas (_FlatParams) on a backend that has them, else one kernel per
+    parameter on a copy of p; either way the old tensor is left as it was,
+    as the composed update leaves it, with the same f32 operations, so the
+    same bits."""
 
     def __init__(self, parameters, lr=0.01, momentum=0.0, weight_decay=0.0, dampening=0.0, fused: bool = False):
         super().__init__(parameters)
         self.lr, self.momentum, self.weight_decay, self.dampening = lr, momentum, weight_decay, dampening
         self.fused = fused
         self._velocity = [None] * len(self.parameters)
+        ad = self.parameters[0].tensor.ad
+        self._flat = None
+        if fused and momentum == 0.0 and weight_decay == 0.0 and hasattr(ad.inner, "sgd_multi_"):
+            self._flat = _FlatParams(ad, self.parameters, moments=False)
 
     def step(self) -> None:
         ad = self.parameters[0].tensor.ad
+        if self._flat is not None:
+            n = self._flat.sizes
+            self._flat.step(lambda segs: ad.inner.sgd_multi_([(ps, pd, g, n[i]) for i, ps, pd, g in segs], self.lr))
+            return
         if (self.fused and self.momentum == 0.0 and self.weight_decay == 0.0
                 and hasattr(ad.inner, "sgd_step_")):
             for p in self.parameters:
@@ -766,10 +844,11 @@ class SGD(Optimizer):
 class AdamW(Optimizer):
     """python/orca/optim/adamw.py:12-99.
 
-    fused=True (opt-in): with a backend that has adamw_step_, each
-    parameter's update is one kernel (the same f32 operations in the same
-    order, so the same bits) on a copy of p, with m and v updated in place
-    (they belong to the optimizer alone).
+    fused=True (opt-in): the update of all parameters is one launch over flat
+    parameter and moment arenas (_FlatParams) on a backend that has them,
+    else one kernel per parameter on a copy of p; the same f32 operations in
+    the same order, so the same bits.  m and v are updated in place (they
+    belong to the optimizer alone).
 
     state_dict / load_state_dict carry m, v and t, which the reference does
     not save."""
@@ -779,6 +858,15 @@ class AdamW(Optimizer):
         self.lr, (self.beta1, self.beta2), self.eps, self.weight_decay = lr, betas, eps, weight_decay
         self.fused = fused
         self.t = 0
+        ad = self.parameters[0].tensor.ad
+        self._flat = None
+        if fused and hasattr(ad.inner, "adamw_multi_"):
+            self._flat = _FlatParams(ad, self.parameters, moments=True)
+            self.m = [Tensor(ad, AdStorage(self._flat.moment("m", i)), p.tensor.shape)
+                      for i, p in enumerate(self.parameters)]
+            self.v = [Tensor(ad, AdStorage(self._flat.moment("v", i)), p.tensor.shape)
+                      for i, p in enumerate(self.parameters)]
+            return
         self.m = [Tensor.zeros(p.tensor.ad, p.tensor.shape) for p in self.parameters]
         self.v = [Tensor.zeros(p.tensor.ad, p.tensor.shape) for p in self.parameters]
 
@@ -803,8 +891,10 @@ class AdamW(Optimizer):
                 if tuple(t.shape) != tuple(self.parameters[i].tensor.shape):
                     raise OrcaError(f"Shape mismatch during load_state_dict: {key} expected "
                                     f"{list(self.parameters[i].tensor.shape)}, got {list(t.shape)}")
-                # a private copy: the fused step updates moments in place
-                slots[i] = Tensor(t.ad, AdStorage(t.ad.inner.clone(t.storage.primal)), t.shape)
+                if self._flat is not None:  # into the moment arena's slice
+                    t.ad.inner.copy_into(slots[i].storage.primal, t.storage.primal)
+                else:  # a private copy: the fused step updates moments in place
+                    slots[i] = Tensor(t.ad, AdStorage(t.ad.inner.clone(t.storage.primal)), t.shape)
         self.t = int(state["t"])
 
     def step(self) -> None:
@@ -819,6 +909,17 @@ class AdamW(Optimizer):
             return
         self.t += 1
         ad = self.parameters[0].tensor.ad
+        if self._flat is not None:
+            flat = self._flat
+            active = {i for i, _, _ in grads}
+
+            def run(segs):
+                ad.inner.adamw_multi_([(ps, pd, g, flat.moment("m", i), flat.moment("v", i), flat.sizes[i])
+                                       for i, ps, pd, g in segs if i in active],
+                                      self.lr, self.beta1, self.beta2, self.eps, self.weight_decay, self.t)
+
+            flat.step(run)
+            return
         if self.fused and hasattr(ad.inner, "adamw_step_"):
             for i, p, grad in grads:
                 new = ad.inner.clone(p.tensor.storage.primal)

@@ -138,6 +138,21 @@ class HipStorage:
         return self.buf.ptr
 
 
+class _ArenaView:
+    """n floats at `offset` of a flat device arena: the buffer of one parameter (or moment)
+    of a fused optimizer.  Keeps the arena alive; frees nothing itself."""
+
+    __slots__ = ("arena", "ptr", "nbytes")
+
+    def __init__(self, arena: Buffer, offset: int, n: int):
+        self.arena = arena
+        self.ptr = arena.ptr + 4 * offset
+        self.nbytes = 4 * n
+
+    def free(self) -> None:
+        pass
+
+
 def _dims(shape):
     return _lib.dims(shape)
 
@@ -628,6 +643,43 @@ class HipBackend:
         self._mutating(p, m, v)
         _lib.call("orca_hip_adamw_step", self.ctx.handle, p.ptr, g.ptr, m.ptr, v.ptr, n, lr, beta1, beta2, eps,
                   weight_decay, t)
+
+    # ---- flat arenas and one-launch optimizer passes ----
+    def arena(self, n: int, fill: float | None = None) -> Buffer:
+        """A flat device buffer of n floats (set to `fill` if given)."""
+        buf = self.ctx.alloc(4 * max(n, 1))
+        if fill is not None and n:
+            self.ctx.fill(buf, fill, n)
+        return buf
+
+    @staticmethod
+    def view(arena: Buffer, offset: int, n: int) -> HipStorage:
+        """The storage of n floats at `offset` (floats) of an arena."""
+        return HipStorage(_ArenaView(arena, offset, n), n)
+
+    def copy_into(self, dst: HipStorage, src: HipStorage) -> None:
+        """dst <- src, device to device (dst a fresh arena slice nobody reads yet)."""
+        src = self._plain(src)
+        if src.n:
+            self.ctx.d2d(dst.buf, src.buf, 4 * src.n)
+
+    def adamw_multi_(self, segs, lr: float, beta1: float, beta2: float, eps: float, weight_decay: float,
+                     t: int) -> None:
+        """One AdamW pass over many parameters (orca_hip_adamw_multi): segs holds
+        (p_src, p_dst, g, m, v, n) storages; p_dst, m and v are written."""
+        rows = [(self._plain(ps), pd, self._plain(g), m, v, n) for ps, pd, g, m, v, n in segs]
+        self._mutating(*[r[k] for r in rows for k in (1, 3, 4)])
+        table = (_lib.OptSegment * max(1, len(rows)))(
+            *[(ps.ptr, pd.ptr, g.ptr, m.ptr, v.ptr, n) for ps, pd, g, m, v, n in rows])
+        _lib.call("orca_hip_adamw_multi", self.ctx.handle, table, len(rows), lr, beta1, beta2, eps, weight_decay, t)
+
+    def sgd_multi_(self, segs, lr: float) -> None:
+        """One SGD pass over many parameters (orca_hip_sgd_multi): segs holds (p_src, p_dst, g, n)."""
+        rows = [(self._plain(ps), pd, self._plain(g), n) for ps, pd, g, n in segs]
+        self._mutating(*[r[1] for r in rows])
+        table = (_lib.OptSegment * max(1, len(rows)))(
+            *[(ps.ptr, pd.ptr, g.ptr, None, None, n) for ps, pd, g, n in rows])
+        _lib.call("orca_hip_sgd_multi", self.ctx.handle, table, len(rows), lr)
 
     def sgd_step_(self, p: HipStorage, g: HipStorage, n: int, lr: float) -> None:
         """In place on p (orca_hip_sgd_step)."""

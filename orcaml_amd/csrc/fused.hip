@@ -410,6 +410,81 @@ __global__ void adamw_scalar_kernel(float* p, const float* p_src, const float* _
 
 __global__ void adamw_store_scalars_kernel(AdamWScalars* dst, AdamWScalars s) { *dst = s; }
 
+// Many parameters in one launch (the optimizer's per-parameter loop,
+// python/orca/optim/adamw.py:66-99 and sgd.py:46-79, as one pass): segment i
+// covers float4 groups [start4[i], start4[i + 1]) of the launch's index space
+// and ceil(n / 4) groups of its own arrays.  A thread finds its segment by
+// binary search over the (uniform) table; whole groups of 16-byte-aligned
+// segments take float4 accesses, the rest (a segment's last partial group,
+// unaligned segments) element by element.  Same per-element arithmetic as the
+// one-parameter kernels, so the same bits.
+constexpr int kOptSegs = ORCA_HIP_OPT_MAX_SEGMENTS;
+struct OptSegs {
+  const float* ps[kOptSegs];
+  float* pd[kOptSegs];
+  const float* g[kOptSegs];
+  float* m[kOptSegs];
+  float* v[kOptSegs];
+  uint64_t n[kOptSegs];
+  uint64_t start4[kOptSegs + 1];
+  uint32_t vec_mask;  // bit i: segment i's arrays are all 16-byte aligned
+  int count;
+};
+
+__device__ __forceinline__ int opt_segment(const OptSegs& s, uint64_t q) {
+  int lo = 0, hi = s.count - 1;  // the last i with start4[i] <= q
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (s.start4[mid] <= q) lo = mid;
+    else hi = mid - 1;
+  }
+  return lo;
+}
+
+template <bool ADAMW>
+__global__ void __launch_bounds__(256) opt_multi_kernel(OptSegs s, AdamWScalars k, float lr) {
+  const uint64_t q = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+  if (q >= s.start4[s.count]) return;
+  const int i = opt_segment(s, q);
+  const uint64_t e0 = 4 * (q - s.start4[i]);
+  const uint64_t n = s.n[i];
+  if (((s.vec_mask >> i) & 1) && e0 + 4 <= n) {
+    const uint64_t j = e0 / 4;
+    const floatx4 pp = __builtin_nontemporal_load(reinterpret_cast<const floatx4*>(s.ps[i]) + j);
+    const floatx4 gg = __builtin_nontemporal_load(reinterpret_cast<const floatx4*>(s.g[i]) + j);
+    if (ADAMW) {
+      const floatx4 mm = __builtin_nontemporal_load(reinterpret_cast<const floatx4*>(s.m[i]) + j);
+      const floatx4 vv = __builtin_nontemporal_load(reinterpret_cast<const floatx4*>(s.v[i]) + j);
+      float pa[4] = {pp.x, pp.y, pp.z, pp.w}, ma[4] = {mm.x, mm.y, mm.z, mm.w}, va[4] = {vv.x, vv.y, vv.z, vv.w};
+      const float ga[4] = {gg.x, gg.y, gg.z, gg.w};
+#pragma unroll
+      for (int u = 0; u < 4; ++u) adamw_elem(pa[u], ga[u], ma[u], va[u], k);
+      __builtin_nontemporal_store(floatx4{pa[0], pa[1], pa[2], pa[3]}, reinterpret_cast<floatx4*>(s.pd[i]) + j);
+      __builtin_nontemporal_store(floatx4{ma[0], ma[1], ma[2], ma[3]}, reinterpret_cast<floatx4*>(s.m[i]) + j);
+      __builtin_nontemporal_store(floatx4{va[0], va[1], va[2], va[3]}, reinterpret_cast<floatx4*>(s.v[i]) + j);
+    } else {
+      floatx4 r;
+      r.x = pp.x - gg.x * lr;
+      r.y = pp.y - gg.y * lr;
+      r.z = pp.z - gg.z * lr;
+      r.w = pp.w - gg.w * lr;
+      __builtin_nontemporal_store(r, reinterpret_cast<floatx4*>(s.pd[i]) + j);
+    }
+    return;
+  }
+  for (uint64_t e = e0; e < e0 + 4 && e < n; ++e) {
+    if (ADAMW) {
+      float pp = s.ps[i][e], mm = s.m[i][e], vv = s.v[i][e];
+      adamw_elem(pp, s.g[i][e], mm, vv, k);
+      s.pd[i][e] = pp;
+      s.m[i][e] = mm;
+      s.v[i][e] = vv;
+    } else {
+      s.pd[i][e] = s.ps[i][e] - s.g[i][e] * lr;
+    }
+  }
+}
+
 __global__ void __launch_bounds__(256) sgd_vec_kernel(float4* __restrict__ p, const float4* __restrict__ g, size_t n4, float lr) {
   const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n4) return;
@@ -562,6 +637,54 @@ void adamw(orca_hip_ctx* ctx, float* p, const float* g, float* m, float* v, size
                          dev_scalars);
   }
   ORCA_HIP_CHECK(hipGetLastError());
+}
+
+// One launch per kOptSegs segments; each segment's arrays are checked against
+// the allocations they point into.
+void opt_multi(orca_hip_ctx* ctx, const orca_hip_opt_segment* segs, size_t n_segs, bool adamw_, const AdamWScalars& k,
+               float lr) {
+  if (n_segs && !segs) fail(ORCA_HIP_ERR_INTERNAL, "optimizer: null segment table");
+  for (size_t b = 0; b < n_segs; b += kOptSegs) {
+    OptSegs t{};
+    uint64_t total4 = 0;
+    double bytes = 0.0;
+    for (size_t i = b; i < n_segs && t.count < kOptSegs; ++i) {
+      const orca_hip_opt_segment& sg = segs[i];
+      const size_t nb = sg.n * sizeof(float);
+      check_extent(ctx, sg.p_src, nb, "optimizer (p_src)");
+      check_extent(ctx, sg.p_dst, nb, "optimizer (p_dst)");
+      check_extent(ctx, sg.g, nb, "optimizer (g)");
+      if (adamw_) {
+        check_extent(ctx, sg.m, nb, "optimizer (m)");
+        check_extent(ctx, sg.v, nb, "optimizer (v)");
+      }
+      if (sg.n && (!sg.p_src || !sg.p_dst || !sg.g || (adamw_ && (!sg.m || !sg.v))))
+        fail(ORCA_HIP_ERR_INTERNAL, "optimizer: null array in segment " + std::to_string(i));
+      const int c = t.count++;
+      t.ps[c] = sg.p_src;
+      t.pd[c] = sg.p_dst;
+      t.g[c] = sg.g;
+      t.m[c] = sg.m;
+      t.v[c] = sg.v;
+      t.n[c] = sg.n;
+      t.start4[c] = total4;
+      total4 += (sg.n + 3) / 4;
+      const bool vec = aligned16(sg.p_src) && aligned16(sg.p_dst) && aligned16(sg.g) &&
+                       (!adamw_ || (aligned16(sg.m) && aligned16(sg.v)));
+      if (vec) t.vec_mask |= 1u << c;
+      bytes += (adamw_ ? 28.0 : 12.0) * (double)sg.n;
+    }
+    t.start4[t.count] = total4;
+    if (total4 == 0) continue;
+    const uint64_t blocks = (total4 + 255) / 256;
+    if (blocks > 0x7fffffffu) fail(ORCA_HIP_ERR_INTERNAL, "optimizer: too many parameters for one launch");
+    ProfScope ps(ctx, adamw_ ? "adamw_multi" : "sgd_multi", 0.0, bytes);
+    if (adamw_)
+      hipLaunchKernelGGL(opt_multi_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, ctx->stream, t, k, lr);
+    else
+      hipLaunchKernelGGL(opt_multi_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, ctx->stream, t, k, lr);
+    ORCA_HIP_CHECK(hipGetLastError());
+  }
 }
 
 void sgd(orca_hip_ctx* ctx, float* p, const float* g, size_t n, double lr, hipStream_t stream) {
@@ -732,6 +855,21 @@ int orca_hip_sgd_step(orca_hip_ctx* ctx, float* p, const float* g, size_t n, dou
     check_extent(ctx, p, n * sizeof(float), "sgd_step");
     check_extent(ctx, g, n * sizeof(float), "sgd_step");
     sgd(ctx, p, g, n, lr);
+  });
+}
+
+int orca_hip_adamw_multi(orca_hip_ctx* ctx, const orca_hip_opt_segment* segs, size_t n_segs, double lr, double beta1,
+                         double beta2, double eps, double weight_decay, int64_t t) {
+  return guard([&] {
+    bind(ctx);
+    opt_multi(ctx, segs, n_segs, true, adamw_scalars(lr, beta1, beta2, eps, weight_decay, t), 0.0f);
+  });
+}
+
+int orca_hip_sgd_multi(orca_hip_ctx* ctx, const orca_hip_opt_segment* segs, size_t n_segs, double lr) {
+  return guard([&] {
+    bind(ctx);
+    opt_multi(ctx, segs, n_segs, false, AdamWScalars{}, (float)lr);
   });
 }
 

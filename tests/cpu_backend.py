@@ -129,3 +129,24 @@ class OracleBackend:
 
     def sgd_step_(self, p, g, n, lr):
         p[:] = O.sgd_update(p, g, lr)
+
+    # flat arenas (numpy views of one array) and the one-pass optimizers over them
+    def arena(self, n, fill=None):
+        return np.full(max(n, 1), 0.0 if fill is None else fill, np.float32)
+
+    @staticmethod
+    def view(arena, offset, n):
+        return arena[offset:offset + n]
+
+    def copy_into(self, dst, src):
+        dst[:] = src
+
+    def adamw_multi_(self, segs, lr, beta1, beta2, eps, weight_decay, t):
+        for ps, pd, g, m, v, n in segs:
+            p2, m2, v2 = O.adamw_update(ps, g, m, v, t, lr=lr, weight_decay=weight_decay, betas=(beta1, beta2),
+                                        eps=eps)
+            pd[:], m[:], v[:] = p2, m2, v2
+
+    def sgd_multi_(self, segs, lr):
+        for ps, pd, g, n in segs:
+            pd[:] = O.sgd_update(ps, g, lr)

@@ -168,3 +168,44 @@ def test_fused_loss_under_no_grad_records_nothing():
         n = len(ad.tape.nodes)
         loss = A.CrossEntropyLoss(fused=True)(model(A.Tensor.from_numpy(ad, x)), A.Tensor.from_numpy(ad, onehot))
         assert len(ad.tape.nodes) == n and not loss.requires_grad
+
+
+@pytest.mark.parametrize("kind", ["sgd", "adamw"])
+def test_flat_arenas_alternate_and_keep_held_values(kind):
+    """The fused optimizers keep parameters in flat arenas and write each step into the other
+    one: with no reader left, two arenas alternate; a parameter storage held from an earlier
+    step (a caller, a tape) keeps its values, because the arena it lives in is not written
+    again while it is referenced (a fresh one is taken instead)."""
+    params, x, onehot = problem()
+    ad = A.Autodiff(OracleBackend())
+    model = A.build_mlp(ad, params)
+    optim = make_optim(model, kind, fused=True)
+    flat = optim._flat
+    assert flat is not None
+    ids = []
+    for _ in range(4):
+        run(ad, model, optim, x, onehot, 1)
+        ids.append(id(flat.cur))
+    assert len(set(ids)) == 2 and ids[0] == ids[2] and ids[1] == ids[3]
+    held = list(model.parameters())[0].tensor.storage.primal
+    snapshot = held.copy()
+    run(ad, model, optim, x, onehot, 3)
+    np.testing.assert_array_equal(held, snapshot)
+    assert id(flat.cur) not in ids or id(flat.spare) not in ids  # the held arena was not reused
+
+
+@pytest.mark.parametrize("kind", ["sgd", "adamw"])
+def test_fused_optimizer_made_after_backward_keeps_the_gradients(kind):
+    """Moving the parameters into the arena keeps each tensor and its recorded gradient: an
+    optimizer built between backward and step applies that step."""
+    params, x, onehot = problem()
+    out = []
+    for fused in (False, True):
+        ad = A.Autodiff(OracleBackend())
+        model = A.build_mlp(ad, params)
+        xt, tt = A.Tensor.from_numpy(ad, x), A.Tensor.from_numpy(ad, onehot)
+        A.CrossEntropyLoss()(model(xt), tt).backward()
+        make_optim(model, kind, fused).step()
+        out.append([p.tensor.numpy() for p in model.parameters()])
+    for a, b in zip(*out):
+        np.testing.assert_array_equal(a, b)

@@ -452,3 +452,62 @@ def test_mlp_step_odd_shapes(ctx, dims, batch, kind):
         assert_close(p, pr, what=f"param {i}")
     np.testing.assert_array_equal(tr.preds(), ref["preds"])
     tr.close()
+
+
+@pytest.mark.parametrize("kind", ["adamw", "sgd"])
+def test_multi_segment_optimizer_equals_one_tensor_kernels(ctx, kind):
+    """orca_hip_adamw_multi / orca_hip_sgd_multi over many parameters (more than one launch's
+    table; sizes not multiples of 4; slices at unaligned offsets, which take the element path;
+    p_dst apart from p_src and equal to it) give the bits of orca_hip_adamw_step /
+    orca_hip_sgd_step run parameter by parameter."""
+    from orcaml_amd.backend import HipBackend
+
+    be = HipBackend(ctx, lazy=False)
+    rng = np.random.default_rng(17)
+    sizes = [1, 5, 4, 1023, 4096, 3, 100001] + [7 + i for i in range(30)]
+    assert len(sizes) > _lib.OPT_MAX_SEGMENTS
+    offs, total = [], 0
+    for k, n in enumerate(sizes):
+        offs.append(total + (k % 3 == 1))  # every third slice one float off 16-byte alignment
+        total = offs[-1] + n + 8
+    p0 = rng.standard_normal(total).astype(np.float32)
+    g0 = (rng.standard_normal(total) * 1e-2).astype(np.float32)
+    m0 = (rng.standard_normal(total) * 1e-3).astype(np.float32)
+    v0 = np.abs(rng.standard_normal(total) * 1e-4).astype(np.float32)
+    arenas = {}
+    for name, a in (("p", p0), ("g", g0), ("m", m0), ("v", v0), ("q", np.zeros(total, np.float32))):
+        arenas[name] = be.arena(total)
+        _lib.call("orca_hip_h2d", ctx.handle, arenas[name].ptr, a.ctypes.data_as(ctypes.c_void_p), a.nbytes)
+    views = {k: [be.view(arenas[k], o, n) for o, n in zip(offs, sizes)] for k in arenas}
+    in_place = [k % 2 == 0 for k in range(len(sizes))]  # p_dst = p_src for every other parameter
+    dst = [views["p"][k] if in_place[k] else views["q"][k] for k in range(len(sizes))]
+    want_p, want_m, want_v = [], [], []
+    for k, n in enumerate(sizes):
+        o = offs[k]
+        p, g = be.from_f32_slice((n,), p0[o:o + n]), be.from_f32_slice((n,), g0[o:o + n])
+        m, v = be.from_f32_slice((n,), m0[o:o + n]), be.from_f32_slice((n,), v0[o:o + n])
+        if kind == "adamw":
+            be.adamw_step_(p, g, m, v, n, 1e-3, 0.9, 0.999, 1e-8, 0.01, 3)
+            want_m.append(be.to_f32_vec(m))
+            want_v.append(be.to_f32_vec(v))
+        else:
+            be.sgd_step_(p, g, n, 0.1)
+        want_p.append(be.to_f32_vec(p))
+    if kind == "adamw":
+        be.adamw_multi_([(views["p"][k], dst[k], views["g"][k], views["m"][k], views["v"][k], n)
+                         for k, n in enumerate(sizes)], 1e-3, 0.9, 0.999, 1e-8, 0.01, 3)
+    else:
+        be.sgd_multi_([(views["p"][k], dst[k], views["g"][k], n) for k, n in enumerate(sizes)], 0.1)
+    for k, n in enumerate(sizes):
+        np.testing.assert_array_equal(be.to_f32_vec(dst[k]), want_p[k], err_msg=f"p of segment {k}")
+        if kind == "adamw":
+            np.testing.assert_array_equal(be.to_f32_vec(views["m"][k]), want_m[k], err_msg=f"m of segment {k}")
+            np.testing.assert_array_equal(be.to_f32_vec(views["v"][k]), want_v[k], err_msg=f"v of segment {k}")
+    # the bytes between slices are untouched
+    q = np.empty(total, np.float32)
+    _lib.call("orca_hip_d2h", ctx.handle, q.ctypes.data_as(ctypes.c_void_p), arenas["q"].ptr, q.nbytes)
+    written = np.zeros(total, bool)
+    for k, (o, n) in enumerate(zip(offs, sizes)):
+        if not in_place[k]:
+            written[o:o + n] = True
+    assert not q[~written].any()
