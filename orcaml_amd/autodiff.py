@@ -94,9 +94,10 @@ class Autodiff:
         if not self.grad_enabled:
             return AdStorage(primal)
         out_id = self.tape.generate_id()
-        if any(s.node_id is not None for s in inputs):
-            self.tape.push_node(make_node(out_id))
-            return AdStorage(primal, out_id)
+        for s in inputs:
+            if s.node_id is not None:
+                self.tape.push_node(make_node(out_id))
+                return AdStorage(primal, out_id)
         return AdStorage(primal)
 
     # --- a node with its own backward.  The reference's tape knows a fixed set
@@ -331,7 +332,7 @@ class Tensor:
     def __init__(self, ad: Autodiff, storage: AdStorage, shape):
         self.ad = ad
         self.storage = storage
-        self.shape = tuple(int(d) for d in shape)
+        self.shape = shape if type(shape) is tuple else tuple(int(d) for d in shape)
         self.dtype = F32
 
     # ---- construction / host I/O ----

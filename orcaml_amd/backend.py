@@ -153,6 +153,9 @@ class _ArenaView:
         pass
 
 
+_wref = weakref.ref
+
+
 def _dims(shape):
     return _lib.dims(shape)
 
@@ -172,7 +175,9 @@ class HipBackend:
         # Lazy elementwise ops run as fused programs (module docstring); off,
         # every elementwise op runs its own kernel at once.
         self.lazy = lazy
-        self._pending = weakref.WeakSet()  # storages holding a pending elementwise op
+        # weak references to storages created with a pending elementwise op (some since
+        # computed or gone; pruned when the list grows, emptied by _mutating)
+        self._pending = []
         self._programs = {}  # compiled elementwise programs by chain structure
 
     def __repr__(self) -> str:
@@ -317,7 +322,10 @@ class HipBackend:
         out._expr = (self, op, operands, scalar)
         out._ew_ops = ops
         out._ew_leaves = leaves
-        self._pending.add(out)
+        pending = self._pending
+        pending.append(_wref(out))
+        if len(pending) > 4096:
+            pending[:] = [r for r in pending if (x := r()) is not None and x._expr is not None]
         return out
 
     def _lazy_ok(self, dtype, *operands) -> bool:
@@ -387,11 +395,9 @@ class HipBackend:
         outs = (ctypes.c_void_p * len(out_idx))(*[b.ptr for b in bufs])
         _lib.call("orca_hip_ew_program", self.ctx.handle, n, ins, len(leaves), outs, oregs, len(out_idx), instrs,
                   len(order), n_regs)
-        pending = self._pending
         for k, b in zip(out_idx, bufs):
             X = order[k]
             X._buf, X._expr, X._ew_ops, X._ew_leaves = b, None, 0, 1
-            pending.discard(X)
 
     @staticmethod
     def _compile(sig, out_idx, n_leaves):
@@ -574,8 +580,10 @@ class HipBackend:
     def _mutating(self, *storages) -> None:
         """Before an in-place update: values derived lazily from these storages are computed
         from their current contents, and their memoised identity reductions are dropped."""
-        for node in list(self._pending):
-            if node._expr is not None:
+        pending, self._pending = self._pending, []
+        for r in pending:
+            node = r()
+            if node is not None and node._expr is not None:
                 node.buf  # runs its pending elementwise chain
         for s in storages:
             if s.colsum_waiters:
