@@ -551,7 +551,10 @@ hipFunction_t jit_kernel(orca_hip_ctx* ctx, const EwProgram& p, bool vec) {
   std::lock_guard<std::mutex> lk(c.mu);
   JitEntry& e = c.programs[jit_key(p.n_in, p.mode, p.n_out, p.out_reg, p.ins, p.n_ops)];
   ++e.uses;
-  if (!e.module && !e.failed && (ctx->ew_jit_mode >= 2 || e.uses >= 2)) {
+  // At most kMaxCompiled structures per context get a module of their own; past that
+  // (a workload that keeps building new chain shapes) new structures stay interpreted.
+  constexpr uint64_t kMaxCompiled = 4096;
+  if (!e.module && !e.failed && c.compiles < kMaxCompiled && (ctx->ew_jit_mode >= 2 || e.uses >= 2)) {
     std::string log;
     const std::string code = jit_compile(jit_source(p.n_in, p.mode, p.n_out, p.out_reg, p.ins, p.n_ops), &log);
     hipModule_t m = nullptr;
