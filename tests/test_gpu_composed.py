@@ -54,20 +54,32 @@ def ref_opt(o):
     return O.make_opt(o["kind"], o["lr"], o.get("weight_decay", 0.0), o.get("betas", (0.9, 0.999)), o.get("eps", 1e-8))
 
 
+@pytest.mark.parametrize("jit", [1, 2], ids=["programs_interpreted", "programs_compiled"])
 @pytest.mark.parametrize("fused", [False, True], ids=["unchanged", "fused_loss_adamw"])
-def test_composed_mlp784_4096_b1024_one_adamw_step(hb, fused):
+def test_composed_mlp784_4096_b1024_one_adamw_step(ctx, hb, fused, jit):
     """784-4096-4096-10, batch 1024, one fwd + bwd + AdamW step through the drop-in path,
-    with the same attribution of outliers as the fused trainer's one-step test."""
+    with the same attribution of outliers as the fused trainer's one-step test.  A single
+    step runs its fused elementwise programs on the interpreter by default (each structure's
+    first use); the second case compiles them at their first use."""
     w = synth.WORKLOADS[synth.MLP_LARGE]
     dims, o = w["dims"], w["opt"]
     params, x, labels, onehot = synth.mlp_problem(w["seed"], dims, w["batch"])
     run = Composed(hb, dims, params, x, onehot, o, fused)
-    out = run.step()
+    ctx.set_ew_jit(jit)
+    try:
+        before = ctx.ew_jit_stats()
+        out = run.step()
+        new_params = run.params()  # runs the pending update programs under the same setting
+        after = ctx.ew_jit_stats()
+    finally:
+        ctx.set_ew_jit(1)
+    if jit == 2:
+        assert after["compiled_launches"] > before["compiled_launches"] and after["failures"] == before["failures"]
     ref = O.mlp_train(dims, params, x, onehot, ref_opt(o), steps=1)
     ref["hidden"] = oracle_hidden(params, x, dims)
     preds = A.argmax_rows(out["logits"])
     correct = int((preds == labels).sum())
-    check_one_adamw_step(dims, o, ref, out["loss"], out["logits"], out["hidden"], out["grads"], run.params(), preds,
+    check_one_adamw_step(dims, o, ref, out["loss"], out["logits"], out["hidden"], out["grads"], new_params, preds,
                          correct, what=f"composed 784-4096-4096-10 ({'fused' if fused else 'unchanged'})")
 
 
