@@ -12,6 +12,7 @@
 
 #include <algorithm>
 #include <cstdint>
+#include <cstdio>
 #include <cstring>
 #include <mutex>
 #include <string>
@@ -573,7 +574,9 @@ hipFunction_t jit_kernel(orca_hip_ctx* ctx, const EwProgram& p, bool vec) {
     (void)hipGetLastError();
     if (!e.module) {
       e.failed = true;
-      ++c.failures;
+      if (c.failures++ == 0)  // said once per context; the structure stays on the interpreter
+        std::fprintf(stderr, "orca_hip: compiling a fused elementwise program failed, interpreting it instead: %.800s\n",
+                     log.empty() ? "module load failed" : log.c_str());
     }
   }
   if (!e.module) {
