@@ -7,6 +7,8 @@ registers, across in-place updates of an input, and for whole composed
 training steps."""
 from __future__ import annotations
 
+import ctypes
+
 import numpy as np
 import pytest
 
@@ -260,3 +262,20 @@ def test_broadcast_beyond_2_31_elements(pair, jit):
     d = eager.sub(got, want, out_shape)
     ss = eager.sum_to_shape(eager.mul(d, d, out_shape), out_shape, (1,))
     assert eager.to_f32_vec(ss)[0] == 0.0
+
+
+@pytest.mark.parametrize("n", [1, 6, 4099])
+def test_unaligned_inputs_take_the_element_kernel(ctx, pair, jit, n):
+    """Inputs that are not 16-byte aligned (slices one float into an arena) run the
+    element-at-a-time kernel, interpreted and compiled; it equals the ops run one by one."""
+    lazy, eager = pair
+    rng = np.random.default_rng(n + 40)
+    a, b = special(rng, n), special(rng, n)
+    arena = lazy.arena(2 * n + 8)
+    _lib.call("orca_hip_h2d", ctx.handle, arena.ptr + 4, a.ctypes.data_as(ctypes.c_void_p), a.nbytes)
+    _lib.call("orca_hip_h2d", ctx.handle, arena.ptr + 4 * (n + 5), b.ctypes.data_as(ctypes.c_void_p), b.nbytes)
+    va, vb = lazy.view(arena, 1, n), lazy.view(arena, n + 5, n)
+    sh = (n,)
+    got = lazy.sqrt(lazy.add(lazy.mul(va, vb, sh), lazy.relu(va, sh), sh), sh)
+    want = eager.sqrt(eager.add(eager.mul(va, vb, sh), eager.relu(va, sh), sh), sh)
+    np.testing.assert_array_equal(lazy.to_f32_vec(got), eager.to_f32_vec(want))
