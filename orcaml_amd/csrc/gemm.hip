@@ -728,6 +728,274 @@ __global__ void __launch_bounds__(64 * SK_WAVES) gemm_skinny_kernel(SkinnyParams
 inline bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; }
 
 // Profiler names: "gemm_<op(A)><op(B)>", "_pipe" for the pipelined 128 x 128 kernel.
+// ---------------------------------------------------------------------------
+// Narrow products, which tile badly on the matrix cores: N <= 16 with a
+// row-major B (X W of a classifier head, X^T dY of its weight gradient) and
+// K <= 16 against B^T (dY W^T back through it).  They are memory-bound: each
+// streams its large operand once, with fp32 FMAs on the vector units.  The
+// small operand is staged through LDS with coalesced loads, padded with zeros
+// to NP = 4, 8 or 16 columns (padding terms are never stored), and every sum
+// has a fixed order, so results do not depend on timing.
+constexpr int NW_MAX = 16;     // largest narrow N (NN, TN) or K (NT)
+constexpr int NW_THREADS = 256;
+constexpr int NN_ROWS = 16;    // rows of C per NN block: 4 per wave
+constexpr int NN_CHUNK = 256;  // k per NN pass: lane l takes k0 + l + 64 j, j < 4
+constexpr int TN_CHUNK = 64;   // k rows of A per TN pass: 16 per wave
+constexpr int NW_MAX_SLICES = 64;
+
+inline int narrow_pad(size_t n) { return n <= 4 ? 4 : n <= 8 ? 8 : 16; }
+
+// C[M x N] = A[M x K] B[K x N], N <= NP.  Block (x, y): K slice x, rows 16 y ..
+// 16 y + 15, wave w owning rows 16 y + 4 w .. + 3.  Per 256-k chunk the block
+// stages B's rows in LDS (row stride NP + 4 floats: conflict-free float4 reads
+// for NP >= 8), lane l reads A at k0 + l + 64 j (coalesced) and accumulates
+// 4 x NP sums in k order; then the 64 lanes of each output are added in lane
+// order.  The next chunk's loads are in flight while a chunk is computed.
+// With one slice the result is C, else part[slice][M][N] (ldo = N), summed in
+// slice order by gemm_narrow_reduce_kernel.
+template <int NP>
+__global__ void __launch_bounds__(NW_THREADS) gemm_nn_narrow_kernel(const float* __restrict__ A, int64_t lda,
+                                                                     const float* __restrict__ B, int64_t ldb,
+                                                                     float* __restrict__ out, int64_t ldo, int M, int N,
+                                                                     int K, int kslice) {
+  constexpr int BS = NP == 4 ? 4 : NP + 4;
+  constexpr int RED = 4 * NP + 1;
+  constexpr int SMEM = NN_CHUNK * BS > 4 * 64 * RED ? NN_CHUNK * BS : 4 * 64 * RED;
+  constexpr int PER_T = NN_CHUNK * NP / NW_THREADS;  // staged B values per thread
+  __shared__ __align__(16) float smem[SMEM];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int k_beg = blockIdx.x * kslice, k_end = min(K, k_beg + kslice);
+  float* o = out + (int64_t)blockIdx.x * M * N;  // this slice's partials (C itself with one slice)
+  float bv[PER_T], a[4][4];
+  // B values first: the LDS writes wait for them and not for A
+  auto load = [&](int k0, int m0) {
+#pragma unroll
+    for (int i = 0; i < PER_T; ++i) {
+      const int e = tid + i * NW_THREADS, r = e / NP, n = e % NP, k = k0 + r;
+      bv[i] = k < k_end && n < N ? B[(int64_t)k * ldb + n] : 0.0f;
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int k = k0 + lane + 64 * j;
+        a[r][j] = m0 + r < M && k < k_end ? A[(int64_t)(m0 + r) * lda + k] : 0.0f;
+      }
+  };
+  for (int g = blockIdx.y; g * NN_ROWS < M; g += gridDim.y) {
+    const int m0 = g * NN_ROWS + 4 * w;  // this wave's first row
+    float acc[4][NP];
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+      for (int n = 0; n < NP; ++n) acc[r][n] = 0.0f;
+    load(k_beg, m0);
+    for (int k0 = k_beg; k0 < k_end; k0 += NN_CHUNK) {
+      __syncthreads();  // the previous chunk's (or row group's) LDS reads are done
+#pragma unroll
+      for (int i = 0; i < PER_T; ++i) {
+        const int e = tid + i * NW_THREADS;
+        smem[(e / NP) * BS + e % NP] = bv[i];
+      }
+      float ac[4][4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) ac[r][j] = a[r][j];
+      __syncthreads();
+      if (k0 + NN_CHUNK < k_end) load(k0 + NN_CHUNK, m0);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float* brow = smem + (lane + 64 * j) * BS;
+        float b[NP];
+#pragma unroll
+        for (int q = 0; q < NP / 4; ++q) {
+          const floatx4 v = *reinterpret_cast<const floatx4*>(brow + 4 * q);
+          b[4 * q] = v.x, b[4 * q + 1] = v.y, b[4 * q + 2] = v.z, b[4 * q + 3] = v.w;
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+          for (int n = 0; n < NP; ++n) acc[r][n] = fmaf(ac[r][j], b[n], acc[r][n]);
+      }
+    }
+    __syncthreads();  // all B reads done before the partials overwrite the staging area
+    float* red = smem + w * 64 * RED;
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+      for (int n = 0; n < NP; ++n) red[lane * RED + r * NP + n] = acc[r][n];
+    __syncthreads();
+    for (int q = lane; q < 4 * NP; q += 64) {
+      const int r = q / NP, n = q % NP;
+      if (m0 + r < M && n < N) {
+        float sum = red[q];
+        for (int t = 1; t < 64; ++t) sum = sum + red[t * RED + q];
+        o[(int64_t)(m0 + r) * ldo + n] = sum;
+      }
+    }
+  }
+}
+
+// C[M x N] = A[M x K] B^T with B stored [N][K], K <= KP.  Thread t of block
+// (x, y) owns column 256 x + t (its row of B in registers) for rows
+// rows_per_block y .. + rows_per_block - 1, whose A values are staged in LDS
+// per pass of 64 rows and read as broadcasts.  Each output is a dot product
+// over k in order; a wave's stores cover 64 consecutive columns of a row.
+template <int KP>
+__global__ void __launch_bounds__(NW_THREADS) gemm_nt_smallk_kernel(const float* __restrict__ A, int64_t lda,
+                                                                     const float* __restrict__ B, int64_t ldb,
+                                                                     float* __restrict__ C, int64_t ldc, int M, int N,
+                                                                     int K, int rows_per_block) {
+  constexpr int PASS = 64;
+  __shared__ __align__(16) float as[PASS * KP];
+  const int tid = threadIdx.x;
+  const int n = blockIdx.x * NW_THREADS + tid;
+  float b[KP];
+#pragma unroll
+  for (int k = 0; k < KP; ++k) b[k] = n < N && k < K ? B[(int64_t)n * ldb + k] : 0.0f;
+  const int m_beg = blockIdx.y * rows_per_block, m_end = min(M, m_beg + rows_per_block);
+  for (int p0 = m_beg; p0 < m_end; p0 += PASS) {
+    const int cnt = min(PASS, m_end - p0);
+    float av[PASS * KP / NW_THREADS];
+#pragma unroll
+    for (int i = 0; i < PASS * KP / NW_THREADS; ++i) {
+      const int e = tid + i * NW_THREADS, t = e / KP, k = e % KP;
+      av[i] = t < cnt && k < K ? A[(int64_t)(p0 + t) * lda + k] : 0.0f;
+    }
+    __syncthreads();  // the previous pass's LDS reads are done
+#pragma unroll
+    for (int i = 0; i < PASS * KP / NW_THREADS; ++i) as[tid + i * NW_THREADS] = av[i];
+    __syncthreads();
+    if (n >= N) continue;
+    float* dst = C + (int64_t)p0 * ldc + n;
+#pragma unroll 4
+    for (int t = 0; t < cnt; ++t) {
+      float a[KP];
+#pragma unroll
+      for (int q = 0; q < KP / 4; ++q) {
+        const floatx4 v = *reinterpret_cast<const floatx4*>(as + t * KP + 4 * q);
+        a[4 * q] = v.x, a[4 * q + 1] = v.y, a[4 * q + 2] = v.z, a[4 * q + 3] = v.w;
+      }
+      float c = 0.0f;
+#pragma unroll
+      for (int k = 0; k < KP; ++k) c = fmaf(a[k], b[k], c);
+      dst[(int64_t)t * ldc] = c;
+    }
+  }
+}
+
+// C[M x N] = A^T B with A stored [K][M], B [K][N], N <= NP.  Block (x, y):
+// columns 256 x .. + 255 (4 per lane, a float4 of an A row when aligned) and
+// K slice y.  Per 64-row chunk the block stages B's rows in LDS and wave w
+// takes chunk rows 16 w .. 16 w + 15; the next chunk's loads are in flight
+// while a chunk is computed.  The lane's sums run in k order, then the 4
+// waves are added in wave order.  With one slice the result is C, else
+// part[slice][M][N] (ldo = N).
+template <int NP>
+__global__ void __launch_bounds__(NW_THREADS) gemm_tn_narrow_kernel(const float* __restrict__ A, int64_t lda,
+                                                                     const float* __restrict__ B, int64_t ldb,
+                                                                     float* __restrict__ out, int64_t ldo, int M, int N,
+                                                                     int K, int kslice, int vec_a) {
+  constexpr int RED = 4 * NP + 1;
+  constexpr int PER_WAVE = TN_CHUNK / 4;
+  constexpr int PER_T = TN_CHUNK * NP / NW_THREADS;  // staged B values per thread
+  __shared__ __align__(16) float bs[TN_CHUNK * NP];
+  __shared__ float red[4 * 64 * RED];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int m0 = blockIdx.x * 256 + 4 * lane;
+  const int k_beg = blockIdx.y * kslice, k_end = min(K, k_beg + kslice);
+  const bool vec = vec_a && m0 + 3 < M;
+  float acc[4][NP];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int n = 0; n < NP; ++n) acc[i][n] = 0.0f;
+  float bv[PER_T], a[PER_WAVE][4];
+  auto load = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < PER_T; ++i) {
+      const int e = tid + i * NW_THREADS, r = e / NP, n = e % NP, k = k0 + r;
+      bv[i] = k < k_end && n < N ? B[(int64_t)k * ldb + n] : 0.0f;
+    }
+#pragma unroll
+    for (int r = 0; r < PER_WAVE; ++r) {
+      const int k = k0 + PER_WAVE * w + r;
+      const float* row = A + (int64_t)k * lda + m0;
+      if (k < k_end && vec) {
+        const floatx4 v = *reinterpret_cast<const floatx4*>(row);
+        a[r][0] = v.x, a[r][1] = v.y, a[r][2] = v.z, a[r][3] = v.w;
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) a[r][i] = k < k_end && m0 + i < M ? row[i] : 0.0f;
+      }
+    }
+  };
+  if (k_beg < k_end) load(k_beg);
+  for (int k0 = k_beg; k0 < k_end; k0 += TN_CHUNK) {
+    __syncthreads();  // the previous chunk's B reads are done
+#pragma unroll
+    for (int i = 0; i < PER_T; ++i) bs[tid + i * NW_THREADS] = bv[i];
+    float ac[PER_WAVE][4];
+#pragma unroll
+    for (int r = 0; r < PER_WAVE; ++r)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) ac[r][i] = a[r][i];
+    __syncthreads();
+    if (k0 + TN_CHUNK < k_end) load(k0 + TN_CHUNK);
+#pragma unroll
+    for (int r = 0; r < PER_WAVE; ++r) {
+      const float* brow = bs + (PER_WAVE * w + r) * NP;
+      float b[NP];
+#pragma unroll
+      for (int q = 0; q < NP / 4; ++q) {
+        const floatx4 v = *reinterpret_cast<const floatx4*>(brow + 4 * q);
+        b[4 * q] = v.x, b[4 * q + 1] = v.y, b[4 * q + 2] = v.z, b[4 * q + 3] = v.w;
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int n = 0; n < NP; ++n) acc[i][n] = fmaf(ac[r][i], b[n], acc[i][n]);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int n = 0; n < NP; ++n) red[(w * 64 + lane) * RED + i * NP + n] = acc[i][n];
+  __syncthreads();
+  // 256 threads store the block's 256 x N outputs: thread t takes entries t, t + 256, ...
+  float* o = out + (int64_t)blockIdx.y * M * N;
+  const int mb = blockIdx.x * 256;
+  for (int q = tid; q < 256 * NP; q += NW_THREADS) {
+    const int col = q / NP, n = q % NP, m = mb + col;
+    if (m < M && n < N) {
+      const int l = col / 4, src = (col % 4) * NP + n;
+      const float sum = ((red[l * RED + src] + red[(64 + l) * RED + src]) + red[(128 + l) * RED + src]) +
+                        red[(192 + l) * RED + src];
+      o[(int64_t)m * ldo + n] = sum;
+    }
+  }
+}
+
+// C[m][n] = sum over slices s (in order) of part[s][m][n].
+__global__ void __launch_bounds__(NW_THREADS) gemm_narrow_reduce_kernel(const float* __restrict__ part, int slices,
+                                                                         float* __restrict__ C, int64_t ldc, int M,
+                                                                         int N) {
+  const int64_t total = (int64_t)M * N;
+  for (int64_t e = (int64_t)blockIdx.x * NW_THREADS + threadIdx.x; e < total; e += (int64_t)gridDim.x * NW_THREADS) {
+    float sum = part[e];
+    for (int s0 = 1; s0 < slices; s0 += 8) {  // 8 loads in flight, added in slice order
+      float v[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] = s0 + i < slices ? part[(int64_t)(s0 + i) * total + e] : 0.0f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        if (s0 + i < slices) sum = sum + v[i];
+    }
+    C[(e / N) * ldc + e % N] = sum;
+  }
+}
+
 const char* kernel_name(bool ta, bool tb, bool pipelined) {
   static const char* names[2][4] = {{"gemm_nn", "gemm_nt", "gemm_tn", "gemm_tt"},
                                     {"gemm_nn_pipe", "gemm_nt_pipe", "gemm_tn_pipe", "gemm_tt_pipe"}};
@@ -742,13 +1010,37 @@ namespace {
 struct GemmPlan {
   bool fast;
   bool skinny;  // 32 x 32 tiles on gemm_skinny_kernel, no K split
+  int narrow;   // 0, or a narrow product: 1 NN (N <= 16), 2 NT (K <= 16), 3 TN (N <= 16)
   size_t BM, BN, mt, nt;
-  int splits, k_chunk;
+  int splits, k_chunk;  // for a narrow TN product: K slices and rows per slice
 };
 
 GemmPlan plan_gemm(orca_hip_ctx* ctx, bool trans_a, bool trans_b, size_t M, size_t N, size_t K, const float* A,
-                   size_t lda, size_t sa, const float* B, size_t ldb, size_t sb, size_t batch) {
+                   size_t lda, size_t sa, const float* B, size_t ldb, size_t sb, size_t batch,
+                   int epi_kind = ORCA_HIP_EPI_NONE) {
   GemmPlan g{};
+  // Narrow products (no epilogue, one batch entry) take the vector-unit kernels.
+  if (ctx->gemm_narrow && batch == 1 && epi_kind == ORCA_HIP_EPI_NONE && K > 0) {
+    if (!trans_a && !trans_b && N <= NW_MAX) g.narrow = 1;
+    else if (!trans_a && trans_b && K <= NW_MAX) g.narrow = 2;
+    else if (trans_a && !trans_b && N <= NW_MAX) g.narrow = 3;
+  }
+  if (g.narrow) {
+    // K slices (narrow NN and TN) so that the grid holds about two blocks per CU
+    g.splits = 1;
+    g.k_chunk = (int)K;
+    if (g.narrow != 2) {
+      const size_t chunk = g.narrow == 1 ? NN_CHUNK : TN_CHUNK;
+      const size_t other = g.narrow == 1 ? (M + NN_ROWS - 1) / NN_ROWS : (M + 255) / 256;
+      const size_t want = std::max<size_t>(1, (2 * (size_t)ctx->num_cus + other - 1) / other);
+      const size_t chunks = (K + chunk - 1) / chunk;
+      const size_t slices = std::min<size_t>(std::min(want, chunks), NW_MAX_SLICES);
+      const size_t per = (chunks + slices - 1) / slices * chunk;
+      g.k_chunk = (int)per;
+      g.splits = (int)((K + per - 1) / per);
+    }
+    return g;
+  }
   const bool vec_a = aligned16(A) && lda % 4 == 0 && (batch == 1 || sa % 4 == 0);
   const bool vec_b = aligned16(B) && ldb % 4 == 0 && (batch == 1 || sb % 4 == 0);
   // Products with M, N, K multiples of 4 and 16-byte aligned operands take the
@@ -816,16 +1108,91 @@ GemmPlan plan_gemm(orca_hip_ctx* ctx, bool trans_a, bool trans_b, size_t M, size
 // Workspace floats of a planned product: split-K partials, then per-split column sums.
 size_t plan_workspace_floats(const GemmPlan& g, size_t M, size_t N, size_t batch, bool colsum) {
   if (g.splits <= 1) return 0;
+  if (g.narrow) return (size_t)g.splits * M * N;  // TN slice partials (its column sum is a separate pass)
   return batch * (size_t)g.splits * M * N + (colsum ? (size_t)g.splits * N : 0);
+}
+
+}  // namespace
+
+namespace {
+
+// A narrow product (plan.narrow): one launch, plus the slice reduction of a
+// sliced product and, when asked for, the exact column sum of B.
+template <int NP>
+void launch_narrow(orca_hip_ctx* ctx, const GemmPlan& plan, size_t M, size_t N, size_t K, const float* A,
+                   size_t lda, const float* B, size_t ldb, float* out, int64_t ldo, int vec) {
+  if (plan.narrow == 1) {
+    const unsigned gy = (unsigned)std::min<size_t>((M + NN_ROWS - 1) / NN_ROWS, 65535);
+    hipLaunchKernelGGL(gemm_nn_narrow_kernel<NP>, dim3((unsigned)plan.splits, gy), dim3(NW_THREADS), 0, ctx->stream,
+                       A, (int64_t)lda, B, (int64_t)ldb, out, ldo, (int)M, (int)N, (int)K, plan.k_chunk);
+  } else if (plan.narrow == 2) {
+    // about two blocks per CU, each walking rows_per_block rows with its columns of B in registers
+    const size_t gx = (N + NW_THREADS - 1) / NW_THREADS;
+    const size_t want = std::max<size_t>(1, (2 * (size_t)ctx->num_cus + gx - 1) / gx);
+    size_t rows = std::max<size_t>((M + want - 1) / want, (M + 65534) / 65535);
+    const size_t gy = (M + rows - 1) / rows;
+    if (gx > 0x7fffffff) fail(ORCA_HIP_ERR_INTERNAL, "gemm: too many columns");
+    hipLaunchKernelGGL(gemm_nt_smallk_kernel<NP>, dim3((unsigned)gx, (unsigned)gy), dim3(NW_THREADS), 0, ctx->stream,
+                       A, (int64_t)lda, B, (int64_t)ldb, out, ldo, (int)M, (int)N, (int)K, (int)rows);
+  } else {
+    hipLaunchKernelGGL(gemm_tn_narrow_kernel<NP>, dim3((unsigned)((M + 255) / 256), (unsigned)plan.splits),
+                       dim3(NW_THREADS), 0, ctx->stream, A, (int64_t)lda, B, (int64_t)ldb, out, ldo, (int)M, (int)N,
+                       (int)K, plan.k_chunk, vec);
+  }
+  ORCA_HIP_CHECK(hipGetLastError());
+}
+
+void gemm_narrow(orca_hip_ctx* ctx, const GemmPlan& plan, size_t M, size_t N, size_t K, const float* A, size_t lda,
+                 const float* B, size_t ldb, float* C, size_t ldc, const GemmEpi& epi) {
+  static const char* names[4] = {"", "gemm_nn_narrow", "gemm_nt_smallk", "gemm_tn_narrow"};
+  std::string pname;
+  if (ctx->prof.enabled)
+    pname = std::string(names[plan.narrow]) + " " + std::to_string(M) + "x" + std::to_string(N) + "x" +
+            std::to_string(K);
+  const int slices = plan.splits;
+  std::unique_ptr<Scratch> scratch;
+  float* out = C;
+  int64_t ldo = (int64_t)ldc;
+  if (slices > 1) {
+    const size_t need = (size_t)slices * M * N;
+    if (epi.ws) {
+      if (epi.ws_floats < need) fail(ORCA_HIP_ERR_INTERNAL, "gemm: workspace too small for the planned slices");
+      out = epi.ws;
+    } else {
+      scratch.reset(new Scratch(ctx, sizeof(float) * need));
+      out = scratch->as<float>();
+    }
+    ldo = (int64_t)N;
+  }
+  {
+    ProfScope ps(ctx, pname.c_str(), 2.0 * (double)M * N * K,
+                 4.0 * (double)(M * K + K * N + (slices > 1 ? slices : 1) * M * N));
+    const int vec = aligned16(A) && lda % 4 == 0;  // float4 rows of A (narrow TN)
+    const int np = narrow_pad(plan.narrow == 2 ? K : N);
+    if (np == 4) launch_narrow<4>(ctx, plan, M, N, K, A, lda, B, ldb, out, ldo, vec);
+    else if (np == 8) launch_narrow<8>(ctx, plan, M, N, K, A, lda, B, ldb, out, ldo, vec);
+    else launch_narrow<16>(ctx, plan, M, N, K, A, lda, B, ldb, out, ldo, vec);
+  }
+  if (slices > 1) {
+    ProfScope ps(ctx, "gemm_narrow_reduce", 0.0, 4.0 * (double)M * N * (slices + 1));
+    const unsigned g = grid_for(M * N, NW_THREADS, ctx->num_cus * 4);
+    hipLaunchKernelGGL(gemm_narrow_reduce_kernel, dim3(g), dim3(NW_THREADS), 0, ctx->stream, out, slices, C,
+                       (int64_t)ldc, (int)M, (int)N);
+    ORCA_HIP_CHECK(hipGetLastError());
+  }
+  if (epi.colsum) {  // only a row-major B has one: the bias gradient, in ascending row order
+    if (plan.narrow == 2) fail(ORCA_HIP_ERR_INTERNAL, "gemm colsum epilogue requires row-major B");
+    launch_colsum(ctx, B, K, N, ldb, epi.colsum);
+  }
 }
 
 }  // namespace
 
 size_t gemm_workspace_floats(orca_hip_ctx* ctx, bool trans_a, bool trans_b, size_t M, size_t N, size_t K,
                              const float* A, size_t lda, size_t sa, const float* B, size_t ldb, size_t sb,
-                             size_t batch, bool colsum) {
+                             size_t batch, bool colsum, int epi_kind) {
   if (M == 0 || N == 0 || batch == 0 || K == 0) return 0;
-  const GemmPlan g = plan_gemm(ctx, trans_a, trans_b, M, N, K, A, lda, sa, B, ldb, sb, batch);
+  const GemmPlan g = plan_gemm(ctx, trans_a, trans_b, M, N, K, A, lda, sa, B, ldb, sb, batch, epi_kind);
   return plan_workspace_floats(g, M, N, batch, colsum && batch == 1 && !trans_b);
 }
 
@@ -847,7 +1214,11 @@ void gemm(orca_hip_ctx* ctx, bool trans_a, bool trans_b, size_t M, size_t N, siz
     if (epi.colsum) launch_fill(ctx, epi.colsum, 0.0f, N);
     return;
   }
-  const GemmPlan plan = plan_gemm(ctx, trans_a, trans_b, M, N, K, A, lda, sa, B, ldb, sb, batch);
+  const GemmPlan plan = plan_gemm(ctx, trans_a, trans_b, M, N, K, A, lda, sa, B, ldb, sb, batch, epi.kind);
+  if (plan.narrow) {
+    gemm_narrow(ctx, plan, M, N, K, A, lda, B, ldb, C, ldc, epi);
+    return;
+  }
   if (plan.skinny) {
     SkinnyParams q{};
     q.A = A;

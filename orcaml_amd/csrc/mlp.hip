@@ -352,12 +352,13 @@ int orca_hip_mlp_create(orca_hip_ctx* ctx, const size_t* dims, size_t n_layers, 
       const size_t K = dims[l], N = dims[l + 1];
       const float* a = l == 0 ? m->x : m->H[l - 1];
       const float* g = l + 1 == n_layers ? m->dlogits : m->dz[0];
+      const int f_epi = l + 1 < n_layers ? ORCA_HIP_EPI_BIAS_RELU : ORCA_HIP_EPI_BIAS;
       ws = std::max(ws, gemm_workspace_floats(ctx, false, false, batch, N, K, a, K, 0, m->P + m->off[2 * l], N, 0, 1,
-                                              false));
+                                              false, f_epi));
       ws = std::max(ws, gemm_workspace_floats(ctx, true, false, K, N, batch, a, K, 0, g, N, 0, 1, true));
       if (l > 0)
         ws = std::max(ws, gemm_workspace_floats(ctx, false, true, batch, K, N, g, N, 0, m->P + m->off[2 * l], N, 0,
-                                                1, false));
+                                                1, false, ORCA_HIP_EPI_RELU_MASK));
     }
     if (ws) {
       m->gemm_ws = m->dev(ws);

@@ -245,15 +245,20 @@ __global__ void reduce_kernel(const float* __restrict__ in, float* __restrict__ 
 // CR_COLS-column slab through LDS (one 128-byte line per row, transposed so that each column's
 // rows are contiguous, double-buffered, two slabs' loads in flight), and lane c of wave 0
 // combines column c's values in row order: the same sequence of operations as reduce_kernel,
-// so the result is bit-identical.
+// so the result is bit-identical.  A matrix of at most 16 columns (a classifier head's
+// bias gradient) takes slabs of 16 columns x 1024 rows instead of 32 x 128: the chain of
+// additions is the same, with 8x fewer slab round trips in front of it.
 constexpr int CR_THREADS = 256;
 constexpr int CR_COLS = 32;
 constexpr int CR_ROWS = 128;
-constexpr int CR_LD = CR_ROWS + 4;  // LDS floats per staged column (16-byte aligned, offset banks)
+constexpr int CR_NARROW_COLS = 16;
+constexpr int CR_NARROW_ROWS = 1024;
 
-template <bool IS_MAX>
+template <bool IS_MAX, int CR_COLS_T = CR_COLS, int CR_ROWS_T = CR_ROWS>
 __global__ void __launch_bounds__(CR_THREADS)
     colreduce_kernel(const float* __restrict__ in, float* __restrict__ out, size_t cols, int64_t rows, size_t st) {
+  constexpr int CR_COLS = CR_COLS_T, CR_ROWS = CR_ROWS_T;
+  constexpr int CR_LD = CR_ROWS + 4;               // LDS floats per staged column (16-byte aligned, offset banks)
   constexpr int GROUPS = CR_THREADS / CR_COLS;     // row quads loaded side by side
   constexpr int QUADS = CR_ROWS / (4 * GROUPS);    // row quads per thread per slab
   __shared__ __align__(16) float buf[2][CR_COLS * CR_LD];
@@ -482,9 +487,14 @@ void launch_colsum(orca_hip_ctx* ctx, const float* src, size_t rows, size_t cols
     return;
   }
   ProfScope ps(ctx, "colsum_rows", 0.0, 4.0 * (double)rows * cols + 4.0 * cols);
-  const unsigned g = (unsigned)((cols + CR_COLS - 1) / CR_COLS);
-  hipLaunchKernelGGL(colreduce_kernel<false>, dim3(g), dim3(CR_THREADS), 0, ctx->stream, src, colsum, cols,
-                     (int64_t)rows, ld);
+  if (cols <= CR_NARROW_COLS) {
+    hipLaunchKernelGGL((colreduce_kernel<false, CR_NARROW_COLS, CR_NARROW_ROWS>), dim3(1), dim3(CR_THREADS), 0,
+                       ctx->stream, src, colsum, cols, (int64_t)rows, ld);
+  } else {
+    const unsigned g = (unsigned)((cols + CR_COLS - 1) / CR_COLS);
+    hipLaunchKernelGGL(colreduce_kernel<false>, dim3(g), dim3(CR_THREADS), 0, ctx->stream, src, colsum, cols,
+                       (int64_t)rows, ld);
+  }
   ORCA_HIP_CHECK(hipGetLastError());
 }
 
@@ -735,7 +745,14 @@ static int reduce_entry(orca_hip_ctx* ctx, bool is_max, const void* s, const siz
         if (a.n_red == 1 && a.n_kept == 1 && a.kept_strides[0] == 1 && a.red_count >= CR_ROWS) {
           const unsigned gc = (unsigned)((n_threads + CR_COLS - 1) / CR_COLS);
           const size_t st = (size_t)a.red_strides[0];
-          if (is_max)
+          if (n_threads <= CR_NARROW_COLS) {
+            if (is_max)
+              hipLaunchKernelGGL((colreduce_kernel<true, CR_NARROW_COLS, CR_NARROW_ROWS>), dim3(1), dim3(CR_THREADS),
+                                 0, ctx->stream, as_f(s), o, n_threads, a.red_count, st);
+            else
+              hipLaunchKernelGGL((colreduce_kernel<false, CR_NARROW_COLS, CR_NARROW_ROWS>), dim3(1), dim3(CR_THREADS),
+                                 0, ctx->stream, as_f(s), o, n_threads, a.red_count, st);
+          } else if (is_max)
             hipLaunchKernelGGL(colreduce_kernel<true>, dim3(gc), dim3(CR_THREADS), 0, ctx->stream, as_f(s), o,
                                n_threads, a.red_count, st);
           else

@@ -173,6 +173,8 @@ struct orca_hip_ctx {
   bool gemm_small_tiles = true;
   // ORCA_HIP_GEMM_SKINNY=0 keeps the K split for few-row products instead of the skinny kernel.
   bool gemm_skinny = true;
+  // ORCA_HIP_GEMM_NARROW=0 keeps products with N <= 16 (or K <= 16 against B^T) on the tiled kernels.
+  bool gemm_narrow = true;
   // Host waits on this context's work so far (stream or event synchronisations).
   std::atomic<uint64_t> host_syncs{0};
   orca_hip::StagingRing staging;
@@ -291,7 +293,7 @@ struct GemmEpi {
 // Workspace floats gemm() needs for this product (0 when K is not split).
 size_t gemm_workspace_floats(orca_hip_ctx* ctx, bool trans_a, bool trans_b, size_t M, size_t N, size_t K,
                              const float* A, size_t lda, size_t sa, const float* B, size_t ldb, size_t sb,
-                             size_t batch, bool colsum);
+                             size_t batch, bool colsum, int epi_kind = ORCA_HIP_EPI_NONE);
 // Batched GEMM: C[b] = op(A[b]) op(B[b]) with element strides sa/sb/sc between batch entries.
 void gemm(orca_hip_ctx* ctx, bool trans_a, bool trans_b, size_t M, size_t N, size_t K, const float* A,
           size_t lda, size_t sa, const float* B, size_t ldb, size_t sb, float* C, size_t ldc, size_t sc,

@@ -85,7 +85,9 @@ def test_unary_and_scalar_ops(hb, shape):
                                                 ((1024, 1), (1024, 10)), ((1,), (33, 65)), ((1, 1), (4096, 16)),
                                                 ((1, 100), (1000, 100)), ((70,), (3, 300, 70)),
                                                 ((1, 1, 33), (2, 129, 33)), ((1, 10), (1024, 10)),
-                                                ((1, 4100), (300, 4100)), ((1, 64), (127, 64)), ((1, 5), (128, 5))])
+                                                ((1, 4100), (300, 4100)), ((1, 64), (127, 64)), ((1, 5), (128, 5)),
+                                                # at most 16 columns: 1024-row slabs, ragged last slab
+                                                ((1, 16), (8192, 16)), ((1, 3), (2049, 3)), ((1, 10), (3000, 10))])
 def test_expand_and_sum_to_shape_bit_exact(hb, in_shape, out_shape):
     rng = np.random.default_rng(sum(out_shape))
     a = rng.standard_normal(in_shape).astype(np.float32)
@@ -136,7 +138,8 @@ def test_reductions_that_reduce_nothing_bit_exact(hb, shape):
                                   O.max_to_shape(x, shape))
 
 
-@pytest.mark.parametrize("shape,out_shape", [((1000, 70), (1, 70)), ((3, 300, 33), (33,)), ((129, 4096), (1, 4096))])
+@pytest.mark.parametrize("shape,out_shape", [((1000, 70), (1, 70)), ((3, 300, 33), (33,)), ((129, 4096), (1, 4096)),
+                                             ((5000, 10), (1, 10)), ((1030, 16), (1, 16)), ((128, 1), (1, 1))])
 def test_column_max_to_shape_bit_exact(hb, shape, out_shape):
     rng = np.random.default_rng(shape[-1])
     x = rng.integers(-3, 3, shape).astype(np.float32)  # many ties
