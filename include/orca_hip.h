@@ -279,6 +279,10 @@ int orca_hip_ew_jit_headers(const char** ew_ops_text);
 #define ORCA_HIP_EPI_BIAS 1      /* C = acc + bias[n] */
 #define ORCA_HIP_EPI_BIAS_RELU 2 /* C = relu(acc + bias[n])  (x > 0 ? x : 0) */
 #define ORCA_HIP_EPI_RELU_MASK 3 /* C = mask[m][n] > 0 ? acc : 0  (ReLU backward on the product) */
+#define ORCA_HIP_EPI_BIAS_RELU_PRE 4 /* pre[m][n] = acc + bias[n] and C = relu(pre)  (pre has C's ldc):
+                                        a Linear + ReLU whose pre-activation is kept for ReLU backward */
+#define ORCA_HIP_EPI_RELU_MASK_PRE 5 /* pre[m][n] = acc and C = mask[m][n] > 0 ? acc : 0: ReLU backward on a
+                                        product that is kept as well (a gradient the tape holds) */
 
 typedef struct {
   int kind;            /* ORCA_HIP_EPI_* */
@@ -286,6 +290,7 @@ typedef struct {
   const float* mask;   /* [M][ldmask] for EPI_RELU_MASK: the ReLU output (or pre-activation) */
   size_t ldmask;
   float* colsum;       /* optional [N]: column sums of op(B) over K (bias gradient of dW = X^T dY) */
+  float* pre;          /* [M][ldc] for EPI_BIAS_RELU_PRE (acc + bias) and EPI_RELU_MASK_PRE (acc) */
 } orca_hip_epilogue;
 
 /* C[M,N] = op(A)[M,K] . op(B)[K,N] in f32 on the fp32 MFMA units.

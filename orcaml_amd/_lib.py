@@ -32,7 +32,7 @@ F32, F64, F16, BF16, I32, I64, U8, BOOL = range(8)
 VIEW_CONTIGUOUS = 0
 VIEW_TRANSPOSED = 1
 
-EPI_NONE, EPI_BIAS, EPI_BIAS_RELU, EPI_RELU_MASK = range(4)
+EPI_NONE, EPI_BIAS, EPI_BIAS_RELU, EPI_RELU_MASK, EPI_BIAS_RELU_PRE, EPI_RELU_MASK_PRE = range(6)
 
 
 class OrcaHipError(ValueError):
@@ -52,6 +52,7 @@ class Epilogue(ctypes.Structure):
         ("mask", ctypes.c_void_p),
         ("ldmask", ctypes.c_size_t),
         ("colsum", ctypes.c_void_p),
+        ("pre", ctypes.c_void_p),
     ]
 
 

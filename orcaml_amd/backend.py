@@ -34,6 +34,16 @@ one pass over memory instead of one per op.  Pending values that something
 outside the chain still references (a tape node's saved primal, an optimizer's
 moment) are written by the same launch.  Each instruction is the op's own f32
 operation, so every value has the bits the ops run one by one would give.
+
+Products are lazy too: a 2-D f32 `matmul` returns a storage that runs the GEMM
+at its first use.  When that use is a pending chain that is exactly a GEMM
+epilogue over a product nothing else references -- Linear's `x @ W +
+b.expand(..)` with or without the ReLU after it (orca-autograd/src/backend.rs:
+1625-1646 keeps the pre-activation, so both are written), or ReluBackward's
+`relu_backward(g @ W^T, z)` (the product, a gradient the tape keeps, is written
+too) -- the product runs once with that epilogue (orca_hip_gemm) instead of a
+product and a program.  The epilogue computes the
+same f32 operations on the same product, so the bits are those of the ops.
 """
 from __future__ import annotations
 
@@ -97,7 +107,7 @@ def _broadcast_map(in_shape, out_shape):
 
 class HipStorage:
     __slots__ = ("_buf", "n", "transposed_shape", "_fill", "colsum_waiters", "ident", "_expr", "_ew_ops",
-                 "_ew_leaves", "__weakref__")
+                 "_ew_leaves", "_prod", "__weakref__")
 
     def __init__(self, buf: Buffer | None, n: int, transposed_shape=None):
         self._buf = buf
@@ -116,6 +126,8 @@ class HipStorage:
         self._expr = None
         self._ew_ops = 0
         self._ew_leaves = 1
+        # A pending product (with _fill set): (lhs, rhs, M, K, N, lhs transposed, rhs transposed).
+        self._prod = None
 
     def __len__(self) -> int:
         return self.n
@@ -167,7 +179,7 @@ def _numel(shape) -> int:
 class HipBackend:
     """Drop-in for `GpuBackend` (orca-backend-gpu/src/backend.rs:45-50)."""
 
-    def __init__(self, ctx: Context | None = None, deferred: bool = True, lazy: bool = True):
+    def __init__(self, ctx: Context | None = None, deferred: bool = True, lazy: bool = True, fold: bool = True):
         self.ctx = ctx if ctx is not None else Context(0)
         # The identity-reduction memo and the deferred column sum (module
         # docstring); off, every sum_to_shape runs its kernel at once.
@@ -175,8 +187,11 @@ class HipBackend:
         # Lazy elementwise ops run as fused programs (module docstring); off,
         # every elementwise op runs its own kernel at once.
         self.lazy = lazy
-        # weak references to storages created with a pending elementwise op (some since
-        # computed or gone; pruned when the list grows, emptied by _mutating)
+        # Pending products whose consumer is a GEMM epilogue run with it (module
+        # docstring; needs lazy); off, every product runs by itself.
+        self.fold = fold
+        # weak references to storages created with a pending elementwise op or product (some
+        # since computed or gone; pruned when the list grows, emptied by _mutating)
         self._pending = []
         self._programs = {}  # compiled elementwise programs by chain structure
 
@@ -271,6 +286,18 @@ class HipBackend:
                           ctypes.byref(out))
                 target._buf, target._fill = cs, None
                 return self._wrap(out, M * N)
+        if (self.lazy and dtype == _lib.F32 and len(lhs_shape) == 2 and len(rhs_shape) == 2
+                and lhs_shape[1] == rhs_shape[0]):
+            M, K, N = int(lhs_shape[0]), int(lhs_shape[1]), int(rhs_shape[1])
+            if lhs.n == M * K and rhs.n == K * N and M * N > 0 and K > 0:
+                out = HipStorage(None, M * N)
+                out._prod = (lhs, rhs, M, K, N, lhs.transposed_shape is not None, rhs.transposed_shape is not None)
+                out._fill = self._run_product
+                pending = self._pending
+                pending.append(_wref(out))
+                if len(pending) > 4096:
+                    pending[:] = [r for r in pending if (x := r()) is not None and x.pending]
+                return out
         out = ctypes.c_void_p()
         dl, rl = _dims(lhs_shape)
         dr, rr = _dims(rhs_shape)
@@ -280,6 +307,18 @@ class HipBackend:
                   ctypes.byref(out))
         n = _numel(lhs_shape[:-1]) * int(rhs_shape[-1])
         return self._wrap(out, n)
+
+    def _run_product(self, st: HipStorage) -> None:
+        """The _fill of a pending product: runs it by itself (orca_hip_matmul)."""
+        lhs, rhs, M, K, N, lt, rt = st._prod
+        st._prod = None
+        out = ctypes.c_void_p()
+        dl, rl = _dims((M, K))
+        dr, rr = _dims((K, N))
+        _lib.call("orca_hip_matmul", self.ctx.handle, lhs.ptr, rhs.ptr, dl, rl, dr, rr, _lib.F32,
+                  _lib.VIEW_TRANSPOSED if lt else _lib.VIEW_CONTIGUOUS,
+                  _lib.VIEW_TRANSPOSED if rt else _lib.VIEW_CONTIGUOUS, ctypes.byref(out))
+        st._buf = Buffer(self.ctx, out.value, 4 * M * N)
 
     def transpose(self, s: HipStorage, shape, dim0: int, dim1: int, dtype=_lib.F32):
         rank = len(shape)
@@ -325,7 +364,7 @@ class HipBackend:
         pending = self._pending
         pending.append(_wref(out))
         if len(pending) > 4096:
-            pending[:] = [r for r in pending if (x := r()) is not None and x._expr is not None]
+            pending[:] = [r for r in pending if (x := r()) is not None and x.pending]
         return out
 
     def _lazy_ok(self, dtype, *operands) -> bool:
@@ -375,6 +414,9 @@ class HipBackend:
             if sys.getrefcount(order[k]) > inner.get(id(order[k]), 0) + 2:
                 out_idx.append(k)
         out_idx.append(len(order) - 1)  # the root
+        if self.fold and type(leaves[0]) is HipStorage and leaves[0]._prod is not None:
+            if self._fold(order, leaves, sig, out_idx):
+                return
         key = (tuple(sig), tuple(out_idx), len(leaves))
         prog = self._programs.get(key)
         if prog is None:
@@ -398,6 +440,69 @@ class HipBackend:
         for k, b in zip(out_idx, bufs):
             X = order[k]
             X._buf, X._expr, X._ew_ops, X._ew_leaves = b, None, 0, 1
+
+    # Chains that are a GEMM epilogue over their first input, a pending product P (leaf -1):
+    # add(P, expand(b)) with b broadcast along rows, optionally relu of it, and
+    # relu_backward(P, z).
+    _FOLD_BIAS = ((EW_COPY, -2), (EW_ADD, -1, 0))
+    _FOLD_BIAS_RELU = ((EW_COPY, -2), (EW_ADD, -1, 0), (EW_RELU, 1))
+    _FOLD_MASK = ((EW_RELU_BW, -1, -2),)
+    # ... and its identity sum_to_shape (0 + x, Linear's expand-both broadcast in backward).
+    # A product never holds -0 (every sum starts from +0 and adds in round-to-nearest, where
+    # +0 + -0 = +0) and the mask writes +0, so 0 + x is x bit for bit (a NaN stays the same
+    # quiet NaN): both values share one buffer.
+    _FOLD_MASK_IDENT = ((EW_RELU_BW, -1, -2), (EW_SUM_VISIT, 0))
+
+    def _fold(self, order, leaves, sig, out_idx) -> bool:
+        """Runs the chain as its product's epilogue when it is one of the three forms above.
+        The `leaves` list, the one operand tuple that holds the product, `prod` and
+        getrefcount's argument account for 4 references to it; a product referenced beyond
+        them (a gradient the tape holds) is written as well by the mask epilogue, and is not
+        folded into the bias ones."""
+        prod = leaves[0]
+        if prod._fill is None:
+            return False
+        shared = sys.getrefcount(prod) > 4
+        lhs, rhs, M, K, N, lt, rt = prod._prod
+        sig = tuple(sig)
+        pre = None
+        if (sig == self._FOLD_MASK and out_idx == [0]) or (sig == self._FOLD_MASK_IDENT and out_idx in ([0, 1], [1])):
+            z = leaves[1]
+            if type(z) is not HipStorage or z.transposed_shape is not None or z.n != M * N:
+                return False
+            kind, bias, mask = _lib.EPI_RELU_MASK_PRE if shared else _lib.EPI_RELU_MASK, None, z
+        elif shared:
+            return False
+        elif (sig == self._FOLD_BIAS and out_idx == [1]) or (sig == self._FOLD_BIAS_RELU and out_idx in ([1, 2], [2])):
+            b = leaves[1]
+            if type(b) is not _Broadcast or b.div != 1 or b.mod != N or b.src.n != N or b.src.transposed_shape:
+                return False
+            if len(sig) == 3 and N <= 16:
+                return False  # the plain product of so narrow an N takes another kernel (other bits)
+            kind = _lib.EPI_BIAS if len(sig) == 2 else (_lib.EPI_BIAS_RELU_PRE if out_idx == [1, 2] else
+                                                        _lib.EPI_BIAS_RELU)
+            bias, mask = b.src, None
+        else:
+            return False
+        c = self.ctx.alloc(4 * M * N)
+        e = _lib.Epilogue(kind, bias.ptr if bias is not None else None, mask.ptr if mask is not None else None,
+                          N if mask is not None else 0, None)
+        if kind in (_lib.EPI_BIAS_RELU_PRE, _lib.EPI_RELU_MASK_PRE):
+            pre = self.ctx.alloc(4 * M * N)
+            e.pre = pre.ptr
+        _lib.call("orca_hip_gemm", self.ctx.handle, int(lt), int(rt), M, N, K, lhs.ptr, M if lt else K, rhs.ptr,
+                  K if rt else N, c.ptr, N, ctypes.byref(e))
+        prod._prod = prod._fill = None
+        if kind == _lib.EPI_RELU_MASK_PRE:
+            prod._buf, pre = pre, None  # the product itself, for its other holders
+        if sig == self._FOLD_MASK_IDENT:
+            outs = [c] * len(out_idx)  # the masked product and its identity sum: one buffer
+        else:
+            outs = [c] if pre is None else [pre, c]  # out_idx order: the add (pre-activation) before the relu
+        for k, buf in zip(out_idx, outs):
+            X = order[k]
+            X._buf, X._expr, X._ew_ops, X._ew_leaves = buf, None, 0, 1
+        return True
 
     @staticmethod
     def _compile(sig, out_idx, n_leaves):
@@ -583,8 +688,8 @@ class HipBackend:
         pending, self._pending = self._pending, []
         for r in pending:
             node = r()
-            if node is not None and node._expr is not None:
-                node.buf  # runs its pending elementwise chain
+            if node is not None and node.pending:
+                node.buf  # runs its pending elementwise chain or product
         for s in storages:
             if s.colsum_waiters:
                 for ref in s.colsum_waiters:

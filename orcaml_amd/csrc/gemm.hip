@@ -54,6 +54,7 @@ struct GemmParams {
   const float* bias;
   const float* mask;
   int64_t ldmask;
+  float* pre;     // EPI_BIAS_RELU_PRE: acc + bias; EPI_RELU_MASK_PRE: acc (with ldc)
   float* colsum;  // [splits][N]
   int vec_a, vec_b;
 };
@@ -141,7 +142,7 @@ __device__ __forceinline__ void read_frag(const float* __restrict__ s, int base,
 template <int EPI, bool FULL, int MT, int NT>
 __device__ __forceinline__ void store_acc(const floatx16 (&acc)[MT][NT], float* __restrict__ C, int64_t ldc, int row0,
                                           int col0, int M, int N, const float* __restrict__ bias,
-                                          const float* __restrict__ mask, int64_t ldmask) {
+                                          const float* __restrict__ mask, int64_t ldmask, float* __restrict__ pre) {
   const int lane = threadIdx.x & 63, h = lane >> 5, i = lane & 31;
   auto row_of = [&](int mt, int r) { return row0 + mt * 32 + (r >> 2) * 8 + h * 4 + (r & 3); };
   auto col_of = [&](int nt) { return col0 + nt * 32 + i; };
@@ -149,18 +150,20 @@ __device__ __forceinline__ void store_acc(const floatx16 (&acc)[MT][NT], float* 
   float bv[NT];
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt)
-    bv[nt] = (EPI == ORCA_HIP_EPI_BIAS || EPI == ORCA_HIP_EPI_BIAS_RELU) && (FULL || col_of(nt) < N) ? bias[col_of(nt)]
-                                                                                                   : 0.0f;
-  float mk[MT][NT][EPI == ORCA_HIP_EPI_RELU_MASK ? 16 : 1];
-  if (EPI == ORCA_HIP_EPI_RELU_MASK) {
+    bv[nt] = (EPI == ORCA_HIP_EPI_BIAS || EPI == ORCA_HIP_EPI_BIAS_RELU || EPI == ORCA_HIP_EPI_BIAS_RELU_PRE) &&
+                     (FULL || col_of(nt) < N)
+                 ? bias[col_of(nt)]
+                 : 0.0f;
+  constexpr bool MASK = EPI == ORCA_HIP_EPI_RELU_MASK || EPI == ORCA_HIP_EPI_RELU_MASK_PRE;
+  float mk[MT][NT][MASK ? 16 : 1];
+  if (MASK) {
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
         for (int r = 0; r < 16; ++r)
-          mk[mt][nt][r & (EPI == ORCA_HIP_EPI_RELU_MASK ? 15 : 0)] =
-              in(mt, nt, r) ? mask[(int64_t)row_of(mt, r) * ldmask + col_of(nt)] : 0.0f;
+          mk[mt][nt][r & (MASK ? 15 : 0)] = in(mt, nt, r) ? mask[(int64_t)row_of(mt, r) * ldmask + col_of(nt)] : 0.0f;
   }
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
@@ -175,7 +178,14 @@ __device__ __forceinline__ void store_acc(const floatx16 (&acc)[MT][NT], float* 
           v = v + bv[nt];
           v = v > 0.0f ? v : 0.0f;
         } else if (EPI == ORCA_HIP_EPI_RELU_MASK) {
-          v = mk[mt][nt][r & (EPI == ORCA_HIP_EPI_RELU_MASK ? 15 : 0)] > 0.0f ? v : 0.0f;
+          v = mk[mt][nt][r & (MASK ? 15 : 0)] > 0.0f ? v : 0.0f;
+        } else if (EPI == ORCA_HIP_EPI_RELU_MASK_PRE) {
+          if (in(mt, nt, r)) pre[(int64_t)row_of(mt, r) * ldc + col_of(nt)] = v;
+          v = mk[mt][nt][r & (MASK ? 15 : 0)] > 0.0f ? v : 0.0f;
+        } else if (EPI == ORCA_HIP_EPI_BIAS_RELU_PRE) {
+          v = v + bv[nt];
+          if (in(mt, nt, r)) pre[(int64_t)row_of(mt, r) * ldc + col_of(nt)] = v;
+          v = v > 0.0f ? v : 0.0f;
         }
         if (in(mt, nt, r)) C[(int64_t)row_of(mt, r) * ldc + col_of(nt)] = v;
       }
@@ -188,14 +198,16 @@ __device__ __forceinline__ void write_tile(const floatx16 (&acc)[MT][NT], float*
 #define ORCA_STORE_ACC(E)                                                                          \
   do {                                                                                             \
     if (full)                                                                                      \
-      store_acc<E, true>(acc, C, ldc, row0, col0, p.M, p.N, p.bias, p.mask, p.ldmask);             \
+      store_acc<E, true>(acc, C, ldc, row0, col0, p.M, p.N, p.bias, p.mask, p.ldmask, p.pre);      \
     else                                                                                           \
-      store_acc<E, false>(acc, C, ldc, row0, col0, p.M, p.N, p.bias, p.mask, p.ldmask);            \
+      store_acc<E, false>(acc, C, ldc, row0, col0, p.M, p.N, p.bias, p.mask, p.ldmask, p.pre);     \
   } while (0)
   switch (epi) {
     case ORCA_HIP_EPI_BIAS: ORCA_STORE_ACC(ORCA_HIP_EPI_BIAS); break;
     case ORCA_HIP_EPI_BIAS_RELU: ORCA_STORE_ACC(ORCA_HIP_EPI_BIAS_RELU); break;
     case ORCA_HIP_EPI_RELU_MASK: ORCA_STORE_ACC(ORCA_HIP_EPI_RELU_MASK); break;
+    case ORCA_HIP_EPI_BIAS_RELU_PRE: ORCA_STORE_ACC(ORCA_HIP_EPI_BIAS_RELU_PRE); break;
+    case ORCA_HIP_EPI_RELU_MASK_PRE: ORCA_STORE_ACC(ORCA_HIP_EPI_RELU_MASK_PRE); break;
     default: ORCA_STORE_ACC(ORCA_HIP_EPI_NONE); break;
   }
 #undef ORCA_STORE_ACC
@@ -530,6 +542,7 @@ struct SplitReduceParams {
   const float* bias;
   const float* mask;
   int64_t ldmask;
+  float* pre;            // EPI_BIAS_RELU_PRE: acc + bias; EPI_RELU_MASK_PRE: acc (with ldc)
   const float* cs_part;  // per-split column sums [splits][N] of a folded bias gradient, or null
   float* cs_out;         // their in-order sum [N]
 };
@@ -549,6 +562,13 @@ __global__ void splitk_reduce_kernel(SplitReduceParams p, size_t total) {
       v = v + p.bias[col];
       v = v > 0.0f ? v : 0.0f;
     } else if (p.epi == ORCA_HIP_EPI_RELU_MASK) {
+      v = p.mask[(int64_t)row * p.ldmask + col] > 0.0f ? v : 0.0f;
+    } else if (p.epi == ORCA_HIP_EPI_BIAS_RELU_PRE) {
+      v = v + p.bias[col];
+      p.pre[b * p.sc + (int64_t)row * p.ldc + col] = v;
+      v = v > 0.0f ? v : 0.0f;
+    } else if (p.epi == ORCA_HIP_EPI_RELU_MASK_PRE) {
+      p.pre[b * p.sc + (int64_t)row * p.ldc + col] = v;
       v = p.mask[(int64_t)row * p.ldmask + col] > 0.0f ? v : 0.0f;
     }
     p.C[b * p.sc + (int64_t)row * p.ldc + col] = v;
@@ -579,16 +599,20 @@ __global__ void splitk_reduce_vec_kernel(SplitReduceParams p, uint32_t total4) {
     floatx4 v = *reinterpret_cast<const floatx4*>(w);
 #pragma unroll 4
     for (int s = 1; s < p.splits; ++s) v = v + *reinterpret_cast<const floatx4*>(w + s * mn);
-    if (p.epi == ORCA_HIP_EPI_BIAS || p.epi == ORCA_HIP_EPI_BIAS_RELU) {
+    if (p.epi == ORCA_HIP_EPI_BIAS || p.epi == ORCA_HIP_EPI_BIAS_RELU || p.epi == ORCA_HIP_EPI_BIAS_RELU_PRE) {
       const floatx4 bv = {p.bias[col], p.bias[col + 1], p.bias[col + 2], p.bias[col + 3]};
       v = v + bv;
-      if (p.epi == ORCA_HIP_EPI_BIAS_RELU) {
+      if (p.epi == ORCA_HIP_EPI_BIAS_RELU_PRE)
+        *reinterpret_cast<floatx4*>(p.pre + b * p.sc + (int64_t)row * p.ldc + col) = v;
+      if (p.epi != ORCA_HIP_EPI_BIAS) {
         v.x = v.x > 0.0f ? v.x : 0.0f;
         v.y = v.y > 0.0f ? v.y : 0.0f;
         v.z = v.z > 0.0f ? v.z : 0.0f;
         v.w = v.w > 0.0f ? v.w : 0.0f;
       }
-    } else if (p.epi == ORCA_HIP_EPI_RELU_MASK) {
+    } else if (p.epi == ORCA_HIP_EPI_RELU_MASK || p.epi == ORCA_HIP_EPI_RELU_MASK_PRE) {
+      if (p.epi == ORCA_HIP_EPI_RELU_MASK_PRE)
+        *reinterpret_cast<floatx4*>(p.pre + b * p.sc + (int64_t)row * p.ldc + col) = v;
       const floatx4 m = *reinterpret_cast<const floatx4*>(p.mask + (int64_t)row * p.ldmask + col);
       v.x = m.x > 0.0f ? v.x : 0.0f;
       v.y = m.y > 0.0f ? v.y : 0.0f;
@@ -632,6 +656,7 @@ struct SkinnyParams {
   const float* bias;
   const float* mask;
   int64_t ldmask;
+  float* pre;  // EPI_BIAS_RELU_PRE: acc + bias; EPI_RELU_MASK_PRE: acc (with ldc)
 };
 
 template <bool TB>
@@ -720,6 +745,13 @@ __global__ void __launch_bounds__(64 * SK_WAVES) gemm_skinny_kernel(SkinnyParams
       x = x > 0.0f ? x : 0.0f;
     } else if (p.epi == ORCA_HIP_EPI_RELU_MASK) {
       x = p.mask[(int64_t)m * p.ldmask + n] > 0.0f ? x : 0.0f;
+    } else if (p.epi == ORCA_HIP_EPI_BIAS_RELU_PRE) {
+      x = x + p.bias[n];
+      p.pre[(int64_t)m * p.ldc + n] = x;
+      x = x > 0.0f ? x : 0.0f;
+    } else if (p.epi == ORCA_HIP_EPI_RELU_MASK_PRE) {
+      p.pre[(int64_t)m * p.ldc + n] = x;
+      x = p.mask[(int64_t)m * p.ldmask + n] > 0.0f ? x : 0.0f;
     }
     p.C[(int64_t)m * p.ldc + n] = x;
   }
@@ -757,7 +789,7 @@ template <int NP>
 __global__ void __launch_bounds__(NW_THREADS) gemm_nn_narrow_kernel(const float* __restrict__ A, int64_t lda,
                                                                      const float* __restrict__ B, int64_t ldb,
                                                                      float* __restrict__ out, int64_t ldo, int M, int N,
-                                                                     int K, int kslice) {
+                                                                     int K, int kslice, const float* __restrict__ bias) {
   constexpr int BS = NP == 4 ? 4 : NP + 4;
   constexpr int RED = 4 * NP + 1;
   constexpr int SMEM = NN_CHUNK * BS > 4 * 64 * RED ? NN_CHUNK * BS : 4 * 64 * RED;
@@ -831,6 +863,7 @@ __global__ void __launch_bounds__(NW_THREADS) gemm_nn_narrow_kernel(const float*
       if (m0 + r < M && n < N) {
         float sum = red[q];
         for (int t = 1; t < 64; ++t) sum = sum + red[t * RED + q];
+        if (bias) sum = sum + bias[n];  // the bias epilogue (one slice only)
         o[(int64_t)(m0 + r) * ldo + n] = sum;
       }
     }
@@ -846,7 +879,9 @@ template <int KP>
 __global__ void __launch_bounds__(NW_THREADS) gemm_nt_smallk_kernel(const float* __restrict__ A, int64_t lda,
                                                                      const float* __restrict__ B, int64_t ldb,
                                                                      float* __restrict__ C, int64_t ldc, int M, int N,
-                                                                     int K, int rows_per_block) {
+                                                                     int K, int rows_per_block,
+                                                                     const float* __restrict__ mask, int64_t ldmask,
+                                                                     float* __restrict__ pre) {
   constexpr int PASS = 64;
   __shared__ __align__(16) float as[PASS * KP];
   const int tid = threadIdx.x;
@@ -880,6 +915,8 @@ __global__ void __launch_bounds__(NW_THREADS) gemm_nt_smallk_kernel(const float*
       float c = 0.0f;
 #pragma unroll
       for (int k = 0; k < KP; ++k) c = fmaf(a[k], b[k], c);
+      if (pre) pre[(int64_t)(p0 + t) * ldc + n] = c;  // the product itself, kept beside the masked one
+      if (mask) c = mask[(int64_t)(p0 + t) * ldmask + n] > 0.0f ? c : 0.0f;  // the ReLU-mask epilogue
       dst[(int64_t)t * ldc] = c;
     }
   }
@@ -977,10 +1014,10 @@ __global__ void __launch_bounds__(NW_THREADS) gemm_tn_narrow_kernel(const float*
   }
 }
 
-// C[m][n] = sum over slices s (in order) of part[s][m][n].
+// C[m][n] = sum over slices s (in order) of part[s][m][n] (+ bias[n] when given).
 __global__ void __launch_bounds__(NW_THREADS) gemm_narrow_reduce_kernel(const float* __restrict__ part, int slices,
                                                                          float* __restrict__ C, int64_t ldc, int M,
-                                                                         int N) {
+                                                                         int N, const float* __restrict__ bias) {
   const int64_t total = (int64_t)M * N;
   for (int64_t e = (int64_t)blockIdx.x * NW_THREADS + threadIdx.x; e < total; e += (int64_t)gridDim.x * NW_THREADS) {
     float sum = part[e];
@@ -992,6 +1029,7 @@ __global__ void __launch_bounds__(NW_THREADS) gemm_narrow_reduce_kernel(const fl
       for (int i = 0; i < 8; ++i)
         if (s0 + i < slices) sum = sum + v[i];
     }
+    if (bias) sum = sum + bias[e % N];  // the bias epilogue
     C[(e / N) * ldc + e % N] = sum;
   }
 }
@@ -1019,11 +1057,14 @@ GemmPlan plan_gemm(orca_hip_ctx* ctx, bool trans_a, bool trans_b, size_t M, size
                    size_t lda, size_t sa, const float* B, size_t ldb, size_t sb, size_t batch,
                    int epi_kind = ORCA_HIP_EPI_NONE) {
   GemmPlan g{};
-  // Narrow products (no epilogue, one batch entry) take the vector-unit kernels.
-  if (ctx->gemm_narrow && batch == 1 && epi_kind == ORCA_HIP_EPI_NONE && K > 0) {
-    if (!trans_a && !trans_b && N <= NW_MAX) g.narrow = 1;
-    else if (!trans_a && trans_b && K <= NW_MAX) g.narrow = 2;
-    else if (trans_a && !trans_b && N <= NW_MAX) g.narrow = 3;
+  // Narrow products (one batch entry; a bias on X W, a ReLU mask on dY W^T) take the vector-unit kernels.
+  if (ctx->gemm_narrow && batch == 1 && K > 0) {
+    const bool none = epi_kind == ORCA_HIP_EPI_NONE;
+    if (!trans_a && !trans_b && N <= NW_MAX && (none || epi_kind == ORCA_HIP_EPI_BIAS)) g.narrow = 1;
+    else if (!trans_a && trans_b && K <= NW_MAX &&
+             (none || epi_kind == ORCA_HIP_EPI_RELU_MASK || epi_kind == ORCA_HIP_EPI_RELU_MASK_PRE))
+      g.narrow = 2;
+    else if (trans_a && !trans_b && N <= NW_MAX && none) g.narrow = 3;
   }
   if (g.narrow) {
     // K slices (narrow NN and TN) so that the grid holds about two blocks per CU
@@ -1120,11 +1161,12 @@ namespace {
 // sliced product and, when asked for, the exact column sum of B.
 template <int NP>
 void launch_narrow(orca_hip_ctx* ctx, const GemmPlan& plan, size_t M, size_t N, size_t K, const float* A,
-                   size_t lda, const float* B, size_t ldb, float* out, int64_t ldo, int vec) {
+                   size_t lda, const float* B, size_t ldb, float* out, int64_t ldo, int vec, const GemmEpi& epi) {
   if (plan.narrow == 1) {
     const unsigned gy = (unsigned)std::min<size_t>((M + NN_ROWS - 1) / NN_ROWS, 65535);
     hipLaunchKernelGGL(gemm_nn_narrow_kernel<NP>, dim3((unsigned)plan.splits, gy), dim3(NW_THREADS), 0, ctx->stream,
-                       A, (int64_t)lda, B, (int64_t)ldb, out, ldo, (int)M, (int)N, (int)K, plan.k_chunk);
+                       A, (int64_t)lda, B, (int64_t)ldb, out, ldo, (int)M, (int)N, (int)K, plan.k_chunk,
+                       plan.splits == 1 && epi.kind == ORCA_HIP_EPI_BIAS ? epi.bias : nullptr);
   } else if (plan.narrow == 2) {
     // about two blocks per CU, each walking rows_per_block rows with its columns of B in registers
     const size_t gx = (N + NW_THREADS - 1) / NW_THREADS;
@@ -1133,7 +1175,9 @@ void launch_narrow(orca_hip_ctx* ctx, const GemmPlan& plan, size_t M, size_t N, 
     const size_t gy = (M + rows - 1) / rows;
     if (gx > 0x7fffffff) fail(ORCA_HIP_ERR_INTERNAL, "gemm: too many columns");
     hipLaunchKernelGGL(gemm_nt_smallk_kernel<NP>, dim3((unsigned)gx, (unsigned)gy), dim3(NW_THREADS), 0, ctx->stream,
-                       A, (int64_t)lda, B, (int64_t)ldb, out, ldo, (int)M, (int)N, (int)K, (int)rows);
+                       A, (int64_t)lda, B, (int64_t)ldb, out, ldo, (int)M, (int)N, (int)K, (int)rows,
+                       epi.kind == ORCA_HIP_EPI_RELU_MASK || epi.kind == ORCA_HIP_EPI_RELU_MASK_PRE ? epi.mask : nullptr,
+                       (int64_t)epi.ldmask, epi.kind == ORCA_HIP_EPI_RELU_MASK_PRE ? epi.pre : nullptr);
   } else {
     hipLaunchKernelGGL(gemm_tn_narrow_kernel<NP>, dim3((unsigned)((M + 255) / 256), (unsigned)plan.splits),
                        dim3(NW_THREADS), 0, ctx->stream, A, (int64_t)lda, B, (int64_t)ldb, out, ldo, (int)M, (int)N,
@@ -1169,15 +1213,15 @@ void gemm_narrow(orca_hip_ctx* ctx, const GemmPlan& plan, size_t M, size_t N, si
                  4.0 * (double)(M * K + K * N + (slices > 1 ? slices : 1) * M * N));
     const int vec = aligned16(A) && lda % 4 == 0;  // float4 rows of A (narrow TN)
     const int np = narrow_pad(plan.narrow == 2 ? K : N);
-    if (np == 4) launch_narrow<4>(ctx, plan, M, N, K, A, lda, B, ldb, out, ldo, vec);
-    else if (np == 8) launch_narrow<8>(ctx, plan, M, N, K, A, lda, B, ldb, out, ldo, vec);
-    else launch_narrow<16>(ctx, plan, M, N, K, A, lda, B, ldb, out, ldo, vec);
+    if (np == 4) launch_narrow<4>(ctx, plan, M, N, K, A, lda, B, ldb, out, ldo, vec, epi);
+    else if (np == 8) launch_narrow<8>(ctx, plan, M, N, K, A, lda, B, ldb, out, ldo, vec, epi);
+    else launch_narrow<16>(ctx, plan, M, N, K, A, lda, B, ldb, out, ldo, vec, epi);
   }
   if (slices > 1) {
     ProfScope ps(ctx, "gemm_narrow_reduce", 0.0, 4.0 * (double)M * N * (slices + 1));
     const unsigned g = grid_for(M * N, NW_THREADS, ctx->num_cus * 4);
     hipLaunchKernelGGL(gemm_narrow_reduce_kernel, dim3(g), dim3(NW_THREADS), 0, ctx->stream, out, slices, C,
-                       (int64_t)ldc, (int)M, (int)N);
+                       (int64_t)ldc, (int)M, (int)N, epi.kind == ORCA_HIP_EPI_BIAS ? epi.bias : nullptr);
     ORCA_HIP_CHECK(hipGetLastError());
   }
   if (epi.colsum) {  // only a row-major B has one: the bias gradient, in ascending row order
@@ -1204,9 +1248,13 @@ void gemm(orca_hip_ctx* ctx, bool trans_a, bool trans_b, size_t M, size_t N, siz
     fail(ORCA_HIP_ERR_INTERNAL, "gemm dimensions exceed the kernel's index range");
   if (K == 0) {  // empty product: C = epilogue(0)
     for (size_t b = 0; b < batch; ++b) {
-      if (epi.kind == ORCA_HIP_EPI_NONE || epi.kind == ORCA_HIP_EPI_RELU_MASK) {
-        if (ldc == N) launch_fill(ctx, C + b * sc, 0.0f, M * N);
-        else for (size_t r = 0; r < M; ++r) launch_fill(ctx, C + b * sc + r * ldc, 0.0f, N);
+      if (epi.kind == ORCA_HIP_EPI_NONE || epi.kind == ORCA_HIP_EPI_RELU_MASK ||
+          epi.kind == ORCA_HIP_EPI_RELU_MASK_PRE) {
+        for (float* out : {C, epi.kind == ORCA_HIP_EPI_RELU_MASK_PRE ? epi.pre : nullptr}) {
+          if (!out) continue;
+          if (ldc == N) launch_fill(ctx, out + b * sc, 0.0f, M * N);
+          else for (size_t r = 0; r < M; ++r) launch_fill(ctx, out + b * sc + r * ldc, 0.0f, N);
+        }
       } else {
         fail(ORCA_HIP_ERR_INTERNAL, "gemm with K = 0 and a bias epilogue is not supported");
       }
@@ -1236,6 +1284,7 @@ void gemm(orca_hip_ctx* ctx, bool trans_a, bool trans_b, size_t M, size_t N, siz
     q.bias = epi.bias;
     q.mask = epi.mask;
     q.ldmask = (int64_t)epi.ldmask;
+    q.pre = epi.pre;
     {
       std::string pname;
       if (ctx->prof.enabled)
@@ -1281,6 +1330,7 @@ void gemm(orca_hip_ctx* ctx, bool trans_a, bool trans_b, size_t M, size_t N, siz
   p.bias = epi.bias;
   p.mask = epi.mask;
   p.ldmask = (int64_t)epi.ldmask;
+  p.pre = epi.pre;
   const bool fold_colsum = epi.colsum != nullptr && batch == 1 && !trans_b && (splits == 1 || !epi.exact_colsum);
   // Split-K partials (and per-split column sums) go to the caller's workspace
   // when it provides one, else to blocks from the context cache.
@@ -1359,11 +1409,13 @@ void gemm(orca_hip_ctx* ctx, bool trans_a, bool trans_b, size_t M, size_t N, siz
     r.bias = epi.bias;
     r.mask = epi.mask;
     r.ldmask = (int64_t)epi.ldmask;
+    r.pre = epi.pre;
     size_t total = batch * M * N;
     ProfScope ps(ctx, "gemm_splitk_reduce", 0.0, 4.0 * (double)total * (splits + 1));
     const bool vec = N % 4 == 0 && ldc % 4 == 0 && (batch == 1 || sc % 4 == 0) && aligned16(C) && aligned16(r.ws) &&
-                     (epi.kind != ORCA_HIP_EPI_RELU_MASK || (aligned16(epi.mask) && epi.ldmask % 4 == 0)) &&
-                     total / 4 < (size_t)INT32_MAX;
+                     ((epi.kind != ORCA_HIP_EPI_RELU_MASK && epi.kind != ORCA_HIP_EPI_RELU_MASK_PRE) ||
+                      (aligned16(epi.mask) && epi.ldmask % 4 == 0)) &&
+                     (!epi.pre || aligned16(epi.pre)) && total / 4 < (size_t)INT32_MAX;
     if (vec) {
       if (fold_colsum) {
         r.cs_part = p.colsum;
@@ -1413,15 +1465,20 @@ int orca_hip_gemm(orca_hip_ctx* ctx, int trans_a, int trans_b, size_t M, size_t 
       e.mask = epi->mask;
       e.ldmask = epi->ldmask;
       e.colsum = epi->colsum;
-      if (e.kind < ORCA_HIP_EPI_NONE || e.kind > ORCA_HIP_EPI_RELU_MASK)
+      const bool has_bias = e.kind == ORCA_HIP_EPI_BIAS || e.kind == ORCA_HIP_EPI_BIAS_RELU ||
+                            e.kind == ORCA_HIP_EPI_BIAS_RELU_PRE;
+      const bool has_mask = e.kind == ORCA_HIP_EPI_RELU_MASK || e.kind == ORCA_HIP_EPI_RELU_MASK_PRE;
+      if (e.kind < ORCA_HIP_EPI_NONE || e.kind > ORCA_HIP_EPI_RELU_MASK_PRE)
         fail(ORCA_HIP_ERR_INTERNAL, "unknown gemm epilogue " + std::to_string(e.kind));
-      if ((e.kind == ORCA_HIP_EPI_BIAS || e.kind == ORCA_HIP_EPI_BIAS_RELU) && !e.bias)
-        fail(ORCA_HIP_ERR_INTERNAL, "bias epilogue without a bias pointer");
-      if (e.kind == ORCA_HIP_EPI_RELU_MASK && (!e.mask || e.ldmask < N))
-        fail(ORCA_HIP_ERR_INTERNAL, "mask epilogue without a valid mask");
-      if (e.kind == ORCA_HIP_EPI_BIAS || e.kind == ORCA_HIP_EPI_BIAS_RELU)
-        check_extent(ctx, e.bias, N * sizeof(float), "gemm (bias)");
-      if (e.kind == ORCA_HIP_EPI_RELU_MASK) check_extent(ctx, e.mask, matrix_bytes(M, N, e.ldmask), "gemm (mask)");
+      if (has_bias && !e.bias) fail(ORCA_HIP_ERR_INTERNAL, "bias epilogue without a bias pointer");
+      if (has_mask && (!e.mask || e.ldmask < N)) fail(ORCA_HIP_ERR_INTERNAL, "mask epilogue without a valid mask");
+      if (e.kind == ORCA_HIP_EPI_BIAS_RELU_PRE || e.kind == ORCA_HIP_EPI_RELU_MASK_PRE) {
+        if (!epi->pre) fail(ORCA_HIP_ERR_INTERNAL, "pre-activation epilogue without a pre pointer");
+        e.pre = epi->pre;
+        check_extent(ctx, e.pre, matrix_bytes(M, N, ldc), "gemm (pre)");
+      }
+      if (has_bias) check_extent(ctx, e.bias, N * sizeof(float), "gemm (bias)");
+      if (has_mask) check_extent(ctx, e.mask, matrix_bytes(M, N, e.ldmask), "gemm (mask)");
       check_extent(ctx, e.colsum, N * sizeof(float), "gemm (colsum)");
     }
     gemm(ctx, trans_a != 0, trans_b != 0, M, N, K, A, lda, 0, B, ldb, 0, C, ldc, 0, 1, e);

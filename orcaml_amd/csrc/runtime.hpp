@@ -282,6 +282,7 @@ struct GemmEpi {
   const float* mask = nullptr;
   size_t ldmask = 0;
   float* colsum = nullptr;
+  float* pre = nullptr;  // EPI_BIAS_RELU_PRE: acc + bias; EPI_RELU_MASK_PRE: acc (C's ldc)
   // Column sums in ascending row order (bit-identical to sum_to_shape) even
   // when K is split: the split product then takes them in a separate pass.
   bool exact_colsum = false;

@@ -99,13 +99,26 @@ def test_narrow_unaligned_operands(ctx, ta, tb):
     np.testing.assert_array_equal(run_gemm(ctx, ta, tb, a_st, b_st), want)
 
 
-def test_narrow_epilogues_stay_on_tiles(ctx):
-    """A bias or ReLU-mask epilogue keeps a narrow product on the tiled kernels
-    (the epilogues live there), with the same integers."""
+def test_narrow_epilogues_match_composed_ops(ctx):
+    """A bias on a narrow X W and a ReLU mask on a narrow dY W^T run inside the narrow kernels
+    (sliced or not), bit-identical to the composed ops on their own product; bias + ReLU keeps
+    a narrow product on the tiled kernels."""
     rng = np.random.default_rng(9)
-    M, N, K = 256, 10, 512
-    A, B = int_matrix(rng, (M, K)), int_matrix(rng, (K, N))
-    bias = int_matrix(rng, (N,))
-    got, names = kernel_names(ctx, lambda: run_gemm(ctx, False, False, A, B, _lib.EPI_BIAS, bias=bias))
-    assert not any("narrow" in n for n in names), names
-    np.testing.assert_array_equal(got, (A.astype(np.int64) @ B.astype(np.int64) + bias).astype(np.float32))
+    for M, N, K in ((256, 10, 512), (1024, 10, 4096), (7, 3, 5)):  # one slice, 8 slices, one tiny block
+        A, B = rng.standard_normal((M, K)).astype(np.float32), rng.standard_normal((K, N)).astype(np.float32)
+        bias = rng.standard_normal(N).astype(np.float32)
+        prod = run_gemm(ctx, False, False, A, B)
+        got, names = kernel_names(ctx, lambda: run_gemm(ctx, False, False, A, B, _lib.EPI_BIAS, bias=bias))
+        assert f"gemm_nn_narrow {M}x{N}x{K}" in names, names
+        np.testing.assert_array_equal(got, O.add(prod, O.expand(bias.reshape(1, N), (M, N))))
+        _, names = kernel_names(ctx, lambda: run_gemm(ctx, False, False, A, B, _lib.EPI_BIAS_RELU, bias=bias))
+        assert not any("narrow" in n for n in names), names
+    for M, N, K in ((1024, 4096, 10), (33, 1001, 3)):
+        A, B = rng.standard_normal((M, K)).astype(np.float32), rng.standard_normal((K, N)).astype(np.float32)
+        Bt = np.ascontiguousarray(B.T)
+        mask = rng.standard_normal((M, N)).astype(np.float32)
+        mask[::5, ::3] = 0.0
+        prod = run_gemm(ctx, False, True, A, Bt)
+        got, names = kernel_names(ctx, lambda: run_gemm(ctx, False, True, A, Bt, _lib.EPI_RELU_MASK, mask=mask))
+        assert f"gemm_nt_smallk {M}x{N}x{K}" in names, names
+        np.testing.assert_array_equal(got, O.relu_backward(prod, mask))
