@@ -217,6 +217,7 @@ int orca_hip_has_nan_or_inf(orca_hip_ctx* ctx, const void* s, size_t n, int dtyp
 #define ORCA_HIP_EW_SUM_VISIT 16   /* 0 + a   (sum_to_shape onto the same shape) */
 #define ORCA_HIP_EW_MAX_VISIT 17   /* a > -FLT_MAX ? a : -FLT_MAX   (max_to_shape onto the same shape) */
 #define ORCA_HIP_EW_COPY 18        /* a   (Backend::expand: the broadcast is the input's index map) */
+#define ORCA_HIP_EW_ADD_SCALAR 19  /* a + scalar   (add of an expanded one-element constant) */
 #define ORCA_HIP_EW_MAX_INPUTS 8
 #define ORCA_HIP_EW_MAX_OUTPUTS 8
 #define ORCA_HIP_EW_MAX_OPS 64
@@ -227,7 +228,7 @@ typedef struct {
   uint8_t dst;      /* register written */
   uint8_t a, b, c;  /* registers read (b, c when the op takes them) */
   uint8_t pad[3];
-  float scalar;     /* ORCA_HIP_EW_MUL_SCALAR's factor */
+  float scalar;     /* ORCA_HIP_EW_MUL_SCALAR's factor, ORCA_HIP_EW_ADD_SCALAR's addend */
 } orca_hip_ew_instr;
 
 /* An input of a program: element e of the n reads ptr[(e / div) % mod], so a

@@ -62,7 +62,7 @@ from .device import Buffer, Context
 # Elementwise program opcodes (include/orca_hip.h ORCA_HIP_EW_*) and interpreter limits.
 EW_ADD, EW_SUB, EW_MUL, EW_DIV, EW_MUL_SCALAR, EW_RELU, EW_RELU_BW, EW_EXP, EW_LOG, EW_SQRT = range(10)
 EW_SIGMOID, EW_EXP_BW, EW_LOG_BW, EW_SQRT_BW, EW_SIGMOID_BW, EW_DIV_BW_RHS, EW_SUM_VISIT, EW_MAX_VISIT = range(10, 18)
-EW_COPY = 18
+EW_COPY, EW_ADD_SCALAR = 18, 19
 EW_MAX_INPUTS, EW_MAX_OUTPUTS, EW_MAX_OPS, EW_MAX_REGS = 8, 8, 64, 16
 _INSTR = struct.Struct("<BBBBBxxxf")  # orca_hip_ew_instr
 _SCALAR = struct.Struct("<f")  # its scalar field, at byte 8
@@ -107,7 +107,7 @@ def _broadcast_map(in_shape, out_shape):
 
 class HipStorage:
     __slots__ = ("_buf", "n", "transposed_shape", "_fill", "colsum_waiters", "ident", "_expr", "_ew_ops",
-                 "_ew_leaves", "_prod", "__weakref__")
+                 "_ew_leaves", "_prod", "_const", "__weakref__")
 
     def __init__(self, buf: Buffer | None, n: int, transposed_shape=None):
         self._buf = buf
@@ -128,6 +128,9 @@ class HipStorage:
         self._ew_leaves = 1
         # A pending product (with _fill set): (lhs, rhs, M, K, N, lhs transposed, rhs transposed).
         self._prod = None
+        # The value of a one-element storage known on the host (a small upload, uploaded at
+        # its first use on the device); dropped by an in-place update.
+        self._const = None
 
     def __len__(self) -> int:
         return self.n
@@ -247,6 +250,8 @@ class HipBackend:
 
     def from_f32_slice(self, shape, data):
         data = np.ascontiguousarray(data, np.float32).reshape(-1)
+        if self.lazy and data.size == 1 and _numel(shape) == 1 and not math.isnan(data[0]):
+            return self._const_node(float(data[0]), 1)
         out = ctypes.c_void_p()
         d, r = _dims(shape)
         _lib.call("orca_hip_from_f32_slice", self.ctx.handle, d, r, data.ctypes.data_as(ctypes.c_void_p), data.size,
@@ -535,7 +540,7 @@ class HipBackend:
             reg[k] = dst
             regs += [regs[0]] * (3 - len(regs))
             instrs += _INSTR.pack(op, dst, regs[0], regs[1], regs[2], 0.0)
-            if op == EW_MUL_SCALAR:
+            if op in (EW_MUL_SCALAR, EW_ADD_SCALAR):
                 scalar_at.append(k)
         if n_regs > EW_MAX_REGS:
             return False
@@ -559,12 +564,20 @@ class HipBackend:
         return self._op2(name, a, b, shape, dtype)
 
     def add(self, a, b, shape, dtype=_lib.F32):
+        if self._lazy_ok(dtype, a, b):
+            r = self._fold_const(EW_ADD, a, b)
+            if r is not None:
+                return r
         return self._binary("add", EW_ADD, a, b, shape, dtype)
 
     def sub(self, a, b, shape, dtype=_lib.F32):
         return self._binary("sub", EW_SUB, a, b, shape, dtype)
 
     def mul(self, a, b, shape, dtype=_lib.F32):
+        if self._lazy_ok(dtype, a, b):
+            r = self._fold_const(EW_MUL, a, b)
+            if r is not None:
+                return r
         return self._binary("mul", EW_MUL, a, b, shape, dtype)
 
     def div(self, a, b, shape, dtype=_lib.F32):
@@ -572,7 +585,13 @@ class HipBackend:
 
     def mul_scalar(self, s, scalar: float, shape, dtype=_lib.F32):
         if self._lazy_ok(dtype, s):
-            return self._ew(EW_MUL_SCALAR, (s,), s.n, float(ctypes.c_float(scalar).value))
+            f = float(ctypes.c_float(scalar).value)
+            c = self._const_src(s)
+            if c is not None:
+                v = np.float32(c._const) * np.float32(f)
+                if not math.isnan(v):
+                    return self._const_node(float(v), s.n)
+            return self._ew(EW_MUL_SCALAR, (s,), s.n, f)
         s = self._plain(s)
         out = ctypes.c_void_p()
         d, r = _dims(shape)
@@ -624,7 +643,8 @@ class HipBackend:
 
     def accumulate_grad(self, a, b):
         if self._lazy_ok(_lib.F32, a, b):
-            return self._ew(EW_ADD, (a, b), a.n)
+            r = self._fold_const(EW_ADD, a, b)
+            return r if r is not None else self._ew(EW_ADD, (a, b), a.n)
         a, b = self._plain(a), self._plain(b)
         out = ctypes.c_void_p()
         _lib.call("orca_hip_accumulate_grad", self.ctx.handle, a.ptr, b.ptr, a.n, ctypes.byref(out))
@@ -633,6 +653,11 @@ class HipBackend:
     def expand(self, s, in_shape, out_shape, dtype=_lib.F32):
         if tuple(in_shape) == tuple(out_shape) and dtype == _lib.F32:
             return s  # identity broadcast: share the storage
+        c = self._const_src(s) if self.lazy and dtype == _lib.F32 else None
+        if c is not None and len(out_shape) >= len(in_shape):
+            n = _numel(out_shape)
+            if n > 0 and s.n == _numel(in_shape):
+                return self._ew(EW_COPY, (_Broadcast(c, n, 1, 1),), n)
         if self.lazy and dtype == _lib.F32 and len(out_shape) >= len(in_shape):
             m = _broadcast_map(tuple(int(d) for d in in_shape), tuple(int(d) for d in out_shape))
             n = _numel(out_shape)
@@ -682,6 +707,54 @@ class HipBackend:
         s.colsum_waiters = live or None
         return found
 
+    # ---- one-element constants ----
+    # A one-element upload (the backward seed, Tensor::scalar) stays on the host until the
+    # device needs it.  An expand of it is a single-value broadcast of the same storage, and
+    # add / mul / accumulate_grad with such a value take it as an instruction's scalar
+    # (x + c, x * c: the ops' own f32 operations; the constant is never NaN, so the operand
+    # order does not matter), mul_scalar of it is computed on the host in f32.
+    def _const_node(self, value: float, n: int) -> HipStorage:
+        c = HipStorage(None, 1)
+        c._const = value
+        c._fill = lambda st, v=value: self._upload_const(st, v)
+        return c if n == 1 else self._ew(EW_COPY, (_Broadcast(c, n, 1, 1),), n)
+
+    def _upload_const(self, st: HipStorage, value: float) -> None:
+        data = np.array([value], np.float32)
+        out = ctypes.c_void_p()
+        d, r = _dims((1,))
+        _lib.call("orca_hip_from_f32_slice", self.ctx.handle, d, r, data.ctypes.data_as(ctypes.c_void_p), 1,
+                  ctypes.byref(out))
+        st._buf = Buffer(self.ctx, out.value, 4)
+
+    @staticmethod
+    def _const_src(s):
+        """The one-element constant storage whose value s holds everywhere, or None."""
+        if type(s) is not HipStorage:
+            return None
+        if s._const is not None:
+            return s
+        e = s._expr
+        if e is not None and e[1] == EW_COPY:
+            b = e[2][0]
+            if type(b) is _Broadcast and b.mod == 1 and type(b.src) is HipStorage and b.src._const is not None:
+                return b.src
+        return None
+
+    def _fold_const(self, op, a, b):
+        """add / mul (op EW_ADD / EW_MUL) with a constant operand as a scalar instruction, or of
+        two constants on the host; None when neither operand is a constant."""
+        ca, cb = self._const_src(a), self._const_src(b)
+        if ca is None and cb is None:
+            return None
+        n = a.n
+        if ca is not None and cb is not None:
+            x, y = np.float32(ca._const), np.float32(cb._const)
+            v = x + y if op == EW_ADD else x * y
+            return None if math.isnan(v) else self._const_node(float(v), n)
+        x, c = (a, cb._const) if cb is not None else (b, ca._const)
+        return self._ew(EW_ADD_SCALAR if op == EW_ADD else EW_MUL_SCALAR, (x,), n, c)
+
     def _mutating(self, *storages) -> None:
         """Before an in-place update: values derived lazily from these storages are computed
         from their current contents, and their memoised identity reductions are dropped."""
@@ -698,6 +771,9 @@ class HipBackend:
                         t.buf  # runs a pending fill
             s.colsum_waiters = None
             s.ident = None
+            if s._const is not None:
+                s.buf  # a constant not yet on the device is uploaded before it changes there
+                s._const = None
 
     def reshape(self, s, in_shape, out_shape, dtype=_lib.F32):
         n_in = _numel(in_shape)

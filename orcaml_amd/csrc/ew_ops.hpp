@@ -29,6 +29,10 @@ struct OpScale {
   float s;
   __device__ float operator()(float x) const { return x * s; }
 };
+struct OpAddScalar {
+  float s;
+  __device__ float operator()(float x) const { return x + s; }
+};
 // One visit per output of sum_to_shape / max_to_shape (nothing reduced): the first step of
 // the reduction from its start value, so -0 becomes +0 and NaN / -inf become -FLT_MAX.
 struct OpSumVisit { __device__ float operator()(float x) const { return 0.0f + x; } };

@@ -109,6 +109,10 @@ __device__ __forceinline__ V ew_apply(const orca_hip_ew_instr& I, V a, V b, V c)
       const float s = I.scalar;
       return lanes([s](float x, float, float) { return OpScale{s}(x); }, a, b, c);
     }
+    case ORCA_HIP_EW_ADD_SCALAR: {
+      const float s = I.scalar;
+      return lanes([s](float x, float, float) { return OpAddScalar{s}(x); }, a, b, c);
+    }
     EW_OP1(ORCA_HIP_EW_RELU, OpRelu);
     EW_OP2(ORCA_HIP_EW_RELU_BW, OpReluBw);
     EW_OP1(ORCA_HIP_EW_EXP, OpExp);
@@ -235,7 +239,7 @@ void check_program(size_t n_inputs, const uint8_t* out_regs, size_t n_outputs, c
     const bool two = three || I.op == ORCA_HIP_EW_ADD || I.op == ORCA_HIP_EW_SUB || I.op == ORCA_HIP_EW_MUL ||
                      I.op == ORCA_HIP_EW_DIV || I.op == ORCA_HIP_EW_RELU_BW || I.op == ORCA_HIP_EW_EXP_BW ||
                      I.op == ORCA_HIP_EW_LOG_BW || I.op == ORCA_HIP_EW_SQRT_BW || I.op == ORCA_HIP_EW_SIGMOID_BW;
-    if (I.op > ORCA_HIP_EW_COPY || I.dst >= n_regs || I.b >= n_regs || I.c >= n_regs || !readable(I.a) ||
+    if (I.op > ORCA_HIP_EW_ADD_SCALAR || I.dst >= n_regs || I.b >= n_regs || I.c >= n_regs || !readable(I.a) ||
         (two && !readable(I.b)) || (three && !readable(I.c)))
       fail(ORCA_HIP_ERR_INTERNAL, "ew_program: instruction " + std::to_string(k) + " is invalid");
     written |= 1u << I.dst;
@@ -313,7 +317,7 @@ const char kJitPrelude[] =
     "  return floatx4{f(a.x, b.x, c.x), f(a.y, b.y, c.y), f(a.z, b.z, c.z), f(a.w, b.w, c.w)};\n"
     "}\n";
 
-// Functor and arity of an opcode (ORCA_HIP_EW_MUL_SCALAR and ORCA_HIP_EW_COPY are written inline).
+// Functor and arity of an opcode (the scalar ops and ORCA_HIP_EW_COPY are written inline).
 struct JitOp {
   int arity;
   const char* functor;
@@ -325,6 +329,7 @@ JitOp jit_op(uint8_t op) {
     case ORCA_HIP_EW_MUL: return {2, "OpMul{}"};
     case ORCA_HIP_EW_DIV: return {2, "OpDiv{}"};
     case ORCA_HIP_EW_MUL_SCALAR: return {1, nullptr};
+    case ORCA_HIP_EW_ADD_SCALAR: return {1, nullptr};
     case ORCA_HIP_EW_RELU: return {1, "OpRelu{}"};
     case ORCA_HIP_EW_RELU_BW: return {2, "OpReluBw{}"};
     case ORCA_HIP_EW_EXP: return {1, "OpExp{}"};
@@ -389,6 +394,8 @@ std::string jit_body(size_t n_in, const uint8_t* modes, size_t n_out, const uint
     std::string expr;
     if (I.op == ORCA_HIP_EW_MUL_SCALAR)
       expr = "L1(OpScale{p.sc[" + std::to_string(k) + "]}, " + name[I.a] + ")";
+    else if (I.op == ORCA_HIP_EW_ADD_SCALAR)
+      expr = "L1(OpAddScalar{p.sc[" + std::to_string(k) + "]}, " + name[I.a] + ")";
     else if (!op.functor)
       expr = name[I.a];
     else if (op.arity == 1)

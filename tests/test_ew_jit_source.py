@@ -51,6 +51,7 @@ ALL_OPS = [
     (B.EW_SIGMOID, 6, 15, 15, 15, 0.0), (B.EW_EXP_BW, 7, 6, 0, 0, 0.0), (B.EW_LOG_BW, 8, 7, 1, 0, 0.0),
     (B.EW_SQRT_BW, 9, 8, 2, 0, 0.0), (B.EW_SIGMOID_BW, 10, 9, 3, 0, 0.0), (B.EW_DIV_BW_RHS, 11, 10, 4, 5, 0.0),
     (B.EW_SUM_VISIT, 12, 11, 11, 11, 0.0), (B.EW_MAX_VISIT, 13, 12, 12, 12, 0.0), (B.EW_COPY, 14, 13, 13, 13, 0.0),
+    (B.EW_ADD_SCALAR, 15, 14, 14, 14, 0.25),
 ]
 
 
@@ -76,6 +77,7 @@ def test_source_has_one_value_per_instruction_and_one_store_per_output():
     assert stores[2][1] == "x0"       # register 0 is never overwritten: the input itself
     # the scalar is a kernel argument, not a constant: programs that differ only in scalars share a kernel
     assert "OpScale{p.sc[4]}" in src and "0.5" not in src
+    assert "OpAddScalar{p.sc[19]}" in src and "0.25" not in src
     # each input is read with the access its (div, mod) selects
     assert "reinterpret_cast<const floatx4*>(p.in[0])[q]" in loop
     assert "bc4(p.in[1][0])" in loop
@@ -130,7 +132,7 @@ def test_functor_header_is_the_one_the_build_compiled():
     ([(B.EW_ADD, 2, 0, 3, 0, 0.0)], [2], 4, "reads register 3 before any write"),
     ([(B.EW_RELU, 2, 0, 0, 0, 0.0)], [3], 4, "outputs register 3, never written"),
     ([(B.EW_DIV_BW_RHS, 2, 0, 1, 3, 0.0)], [2], 4, "third operand not written"),
-    ([(19, 2, 0, 1, 0, 0.0)], [2], 3, "unknown opcode"),
+    ([(20, 2, 0, 1, 0, 0.0)], [2], 3, "unknown opcode"),
     ([(B.EW_ADD, 5, 0, 1, 0, 0.0)], [5], 4, "destination past the registers"),
 ])
 def test_malformed_programs_are_refused(instrs, out_regs, n_regs, what):

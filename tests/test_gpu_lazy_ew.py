@@ -144,6 +144,25 @@ def test_pending_value_survives_in_place_update_of_its_input(pair):
     np.testing.assert_array_equal(lazy.to_f32_vec(twice), p0 * np.float32(2.0))
 
 
+def test_constant_updated_in_place_is_read_from_the_device_afterwards(pair):
+    """A one-element upload folded into a pending chain as an instruction's scalar keeps its
+    value there; once an in-place update changes it, later ops read the new value."""
+    lazy, eager = pair
+    rng = np.random.default_rng(12)
+    n = 4096
+    x0 = rng.standard_normal(n).astype(np.float32)
+    x = up(lazy, x0)
+    c = lazy.from_f32_slice((1,), np.array([0.75], np.float32))
+    g = lazy.from_f32_slice((1,), np.array([0.5], np.float32))
+    before = lazy.add(x, lazy.expand(c, (1,), (n,)), (n,))
+    assert before.pending
+    lazy.sgd_step_(c, g, 1, 0.5)  # c = 0.75 - 0.5 * 0.5
+    after = lazy.mul(lazy.expand(c, (1,), (n,)), x, (n,))
+    np.testing.assert_array_equal(lazy.to_f32_vec(before), O.add(x0, np.full(n, 0.75, np.float32)))
+    np.testing.assert_array_equal(lazy.to_f32_vec(after), O.mul(np.full(n, 0.5, np.float32), x0))
+    np.testing.assert_array_equal(lazy.to_f32_vec(c), np.array([0.5], np.float32))
+
+
 def test_one_launch_for_a_chain(pair, ctx):
     lazy, _ = pair
     rng = np.random.default_rng(3)

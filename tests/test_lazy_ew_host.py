@@ -28,6 +28,7 @@ _OPS = {
     B.EW_LOG_BW: lambda a, b, c, s: O.log_backward(a, b), B.EW_SQRT_BW: lambda a, b, c, s: O.sqrt_backward(a, b),
     B.EW_SIGMOID_BW: lambda a, b, c, s: O.sigmoid_backward(a, b),
     B.EW_DIV_BW_RHS: lambda a, b, c, s: O.div_backward_rhs(a, b, c), B.EW_COPY: lambda a, b, c, s: a.copy(),
+    B.EW_ADD_SCALAR: lambda a, b, c, s: O.add(a, np.full_like(a, s)),
 }
 
 
@@ -205,6 +206,38 @@ def test_broadcast_inputs_match_expand(fake, in_shape, out_shape):
     got = hb.expand(d, in_shape, out_shape)
     assert got.pending
     np.testing.assert_array_equal(down(hb, hb.add(got, got, (want.size,))), O.add(want, want))
+
+
+def test_one_element_constants_become_instruction_scalars(fake):
+    """A one-element upload (the backward seed, Tensor::scalar) stays on the host: mul_scalar of
+    it is computed there, and add / mul with its expand take it as an instruction's scalar,
+    with either operand order, so the program reads only the other input and the constant is
+    never uploaded.  Every value equals the ops run one by one."""
+    dev, hb = fake
+    rng = np.random.default_rng(8)
+    n = 50
+    f = np.float32
+    x0 = np.abs(rng.standard_normal(n)).astype(np.float32)
+    x = up(hb, x0)
+    eps = hb.from_f32_slice((1,), np.array([1e-8], np.float32))
+    seed = hb.from_f32_slice((1,), np.array([1.0], np.float32))
+    assert eps.pending and eps._const == f(1e-8) and seed._const == 1.0
+    g = hb.mul_scalar(seed, 1.0 / 7.0, (1,))
+    assert g._const == f(1.0) * f(1.0 / 7.0)
+    ge = hb.expand(g, (1,), (n,))
+    denom = hb.add(hb.sqrt(x, (n,)), hb.expand(eps, (1,), (n,)), (n,))
+    z = hb.accumulate_grad(hb.mul(ge, denom, (n,)), hb.expand(eps, (1,), (n,)))
+    got = down(hb, z)
+    want_denom = O.add(O.sqrt(x0), O.expand(np.array([1e-8], np.float32), (n,)))
+    want_g = O.expand(O.mul_scalar(np.array([1.0], np.float32), f(1.0 / 7.0)), (n,))
+    want = O.accumulate_grad(O.mul(want_g, want_denom), O.expand(np.array([1e-8], np.float32), (n,)))
+    np.testing.assert_array_equal(got, want)
+    assert dev.programs[-1][0] == 1  # one input: x
+    assert eps._buf is None and seed._buf is None and g._buf is None  # never uploaded
+    # a constant the device needs (here the input of exp) is uploaded at that use
+    e = down(hb, hb.exp(hb.expand(eps, (1,), (n,)), (n,)))
+    np.testing.assert_array_equal(e, O.exp(O.expand(np.array([1e-8], np.float32), (n,))))
+    assert eps._buf is not None
 
 
 def test_broadcast_map_rejects_split_blocks():
