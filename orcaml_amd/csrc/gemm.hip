@@ -774,6 +774,7 @@ constexpr int NN_ROWS = 16;    // rows of C per NN block: 4 per wave
 constexpr int NN_CHUNK = 256;  // k per NN pass: lane l takes k0 + l + 64 j, j < 4
 constexpr int TN_CHUNK = 64;   // k rows of A per TN pass: 16 per wave
 constexpr int NW_MAX_SLICES = 64;
+constexpr int NT_ROW_GROUP = 16;  // rows of an NT block whose mask values are loaded together
 
 inline int narrow_pad(size_t n) { return n <= 4 ? 4 : n <= 8 ? 8 : 16; }
 
@@ -904,20 +905,32 @@ __global__ void __launch_bounds__(NW_THREADS) gemm_nt_smallk_kernel(const float*
     __syncthreads();
     if (n >= N) continue;
     float* dst = C + (int64_t)p0 * ldc + n;
-#pragma unroll 4
-    for (int t = 0; t < cnt; ++t) {
-      float a[KP];
+    // Rows in groups of 16, the group's mask values loaded before its first row is
+    // computed (a load per row ahead of each store would chain the rows on memory).
+    for (int t0 = 0; t0 < cnt; t0 += NT_ROW_GROUP) {
+      float mk[NT_ROW_GROUP];
+      if (mask) {
 #pragma unroll
-      for (int q = 0; q < KP / 4; ++q) {
-        const floatx4 v = *reinterpret_cast<const floatx4*>(as + t * KP + 4 * q);
-        a[4 * q] = v.x, a[4 * q + 1] = v.y, a[4 * q + 2] = v.z, a[4 * q + 3] = v.w;
+        for (int j = 0; j < NT_ROW_GROUP; ++j)
+          mk[j] = t0 + j < cnt ? mask[(int64_t)(p0 + t0 + j) * ldmask + n] : 0.0f;
       }
-      float c = 0.0f;
 #pragma unroll
-      for (int k = 0; k < KP; ++k) c = fmaf(a[k], b[k], c);
-      if (pre) pre[(int64_t)(p0 + t) * ldc + n] = c;  // the product itself, kept beside the masked one
-      if (mask) c = mask[(int64_t)(p0 + t) * ldmask + n] > 0.0f ? c : 0.0f;  // the ReLU-mask epilogue
-      dst[(int64_t)t * ldc] = c;
+      for (int j = 0; j < NT_ROW_GROUP; ++j) {
+        const int t = t0 + j;
+        if (t >= cnt) break;
+        float a[KP];
+#pragma unroll
+        for (int q = 0; q < KP / 4; ++q) {
+          const floatx4 v = *reinterpret_cast<const floatx4*>(as + t * KP + 4 * q);
+          a[4 * q] = v.x, a[4 * q + 1] = v.y, a[4 * q + 2] = v.z, a[4 * q + 3] = v.w;
+        }
+        float c = 0.0f;
+#pragma unroll
+        for (int k = 0; k < KP; ++k) c = fmaf(a[k], b[k], c);
+        if (pre) pre[(int64_t)(p0 + t) * ldc + n] = c;  // the product itself, kept beside the masked one
+        if (mask) c = mk[j] > 0.0f ? c : 0.0f;          // the ReLU-mask epilogue
+        dst[(int64_t)t * ldc] = c;
+      }
     }
   }
 }
