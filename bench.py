@@ -179,10 +179,10 @@ def secondary(ctx) -> dict:
             A.CrossEntropyLoss(fused=fused)(model(xt), tt).backward()
             opt.step()
 
-        for _ in range(3):
+        for _ in range(10):  # the first steps compile the recurring program structures
             step()
         ctx.sync()
-        n = 10
+        n = 30
         t0 = time.perf_counter()
         for _ in range(n):
             step()
