@@ -458,6 +458,19 @@ class HipBackend:
     # quiet NaN): both values share one buffer.
     _FOLD_MASK_IDENT = ((EW_RELU_BW, -1, -2), (EW_SUM_VISIT, 0))
 
+    @staticmethod
+    def _narrow(kind, lt, rt, N, K) -> bool:
+        """Whether orca_hip_gemm runs the product on its narrow kernels with this epilogue: the
+        planner's rule (orcaml_amd/csrc/gemm.hip plan_gemm).  A fold is taken only where the
+        plain product and the one with the epilogue run on the same kernel (the same sums)."""
+        if not lt and not rt and N <= 16:
+            return kind in (_lib.EPI_NONE, _lib.EPI_BIAS)
+        if not lt and rt and K <= 16:
+            return kind in (_lib.EPI_NONE, _lib.EPI_RELU_MASK, _lib.EPI_RELU_MASK_PRE)
+        if lt and not rt and N <= 16:
+            return kind == _lib.EPI_NONE
+        return False
+
     def _fold(self, order, leaves, sig, out_idx) -> bool:
         """Runs the chain as its product's epilogue when it is one of the three forms above.
         The `leaves` list, the one operand tuple that holds the product, `prod` and
@@ -482,13 +495,13 @@ class HipBackend:
             b = leaves[1]
             if type(b) is not _Broadcast or b.div != 1 or b.mod != N or b.src.n != N or b.src.transposed_shape:
                 return False
-            if len(sig) == 3 and N <= 16:
-                return False  # the plain product of so narrow an N takes another kernel (other bits)
             kind = _lib.EPI_BIAS if len(sig) == 2 else (_lib.EPI_BIAS_RELU_PRE if out_idx == [1, 2] else
                                                         _lib.EPI_BIAS_RELU)
             bias, mask = b.src, None
         else:
             return False
+        if self._narrow(kind, lt, rt, N, K) != self._narrow(_lib.EPI_NONE, lt, rt, N, K):
+            return False  # the plain product runs on another kernel (other sums, other bits)
         c = self.ctx.alloc(4 * M * N)
         e = _lib.Epilogue(kind, bias.ptr if bias is not None else None, mask.ptr if mask is not None else None,
                           N if mask is not None else 0, None)

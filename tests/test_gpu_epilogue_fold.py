@@ -219,6 +219,49 @@ def test_identity_sum_keeps_nan_bits(ctx):
     assert got[6] == 0  # -0 -> +0
 
 
+@pytest.mark.parametrize("form,lt,rt,M,K,N,folds", [
+    ("bias", False, False, 96, 200, 10, True),      # narrow X W takes the bias itself
+    ("bias", False, True, 96, 10, 300, False),      # narrow dY W^T has no bias epilogue: not folded
+    ("bias", True, False, 300, 96, 10, False),      # nor narrow X^T dY
+    ("relu", False, False, 96, 200, 10, False),     # bias + ReLU never runs narrow
+    ("relu", False, True, 96, 10, 300, False),
+    ("relu", False, False, 96, 200, 40, True),
+    ("mask", False, True, 96, 10, 300, True),       # narrow dY W^T takes the mask itself
+    ("mask", False, False, 96, 200, 10, False),     # narrow X W has no mask epilogue: not folded
+    ("mask", True, False, 300, 96, 10, False),
+    ("mask", True, False, 300, 96, 40, True),
+])
+def test_fold_only_where_the_product_keeps_its_kernel(ctx, form, lt, rt, M, K, N, folds):
+    """A chain over a pending product folds only where the product with the epilogue runs on
+    the same kernel as the plain product, so folding never changes a bit."""
+    rng = np.random.default_rng(M + K + N + 2 * lt + rt)
+    a = rng.standard_normal((K, M) if lt else (M, K)).astype(np.float32)
+    w = rng.standard_normal((N, K) if rt else (K, N)).astype(np.float32)
+    b = rng.standard_normal((1, N)).astype(np.float32)
+    z = rng.standard_normal((M, N)).astype(np.float32)
+    out = []
+    for fold in (True, False):
+        hb = HipBackend(ctx, fold=fold)
+        da, dw = hb.from_f32_slice(a.shape, a), hb.from_f32_slice(w.shape, w)
+        lhs = hb.transpose(da, a.shape, 0, 1) if lt else da
+        rhs = hb.transpose(dw, w.shape, 0, 1) if rt else dw
+        prod = hb.matmul(lhs, rhs, (M, K), (K, N))
+        if form == "mask":
+            r = hb.relu_backward(prod, hb.from_f32_slice((M, N), z), (M, N))
+        else:
+            r = hb.add(prod, hb.expand(hb.from_f32_slice((1, N), b), (1, N), (M, N)), (M, N))
+            if form == "relu":
+                r = hb.relu(r, (M, N))
+        del prod
+        before = ctx.ew_jit_stats()
+        out.append(hb.to_f32_vec(r))
+        after = ctx.ew_jit_stats()
+        launched = after["interpreted"] + after["compiled_launches"] - before["interpreted"] - before["compiled_launches"]
+        if fold:
+            assert (launched == 0) == folds, launched
+    np.testing.assert_array_equal(out[0], out[1])
+
+
 def test_pending_product_runs_before_its_input_is_updated(ctx):
     """An in-place optimizer update of a product's input first runs the pending product on
     the old values."""
