@@ -78,6 +78,9 @@ int orca_hip_device(const orca_hip_ctx* ctx, int* ordinal);
  * block is reused by later work on the same stream without a hipMalloc. */
 int orca_hip_alloc(orca_hip_ctx* ctx, size_t bytes, void** out);
 int orca_hip_free(orca_hip_ctx* ctx, void* ptr);
+/* orca_hip_free of each of ptrs[0..n) in order (no counterpart in the reference: for a
+ * binding that releases dropped storages in batches, one call instead of one per storage). */
+int orca_hip_free_many(orca_hip_ctx* ctx, void* const* ptrs, size_t n);
 /* Returns cached blocks to the device (synchronises first). */
 int orca_hip_empty_cache(orca_hip_ctx* ctx);
 /* live bytes, cached bytes, and the number of hipMalloc calls so far. */

@@ -85,6 +85,7 @@ SIGNATURES = {
     "orca_hip_device": [_P, ctypes.POINTER(_I)],
     "orca_hip_alloc": [_P, _SZ, _PP],
     "orca_hip_free": [_P, _P],
+    "orca_hip_free_many": [_P, _P, _SZ],
     "orca_hip_empty_cache": [_P],
     "orca_hip_mem_stats": [_P, _SZP, _SZP, _SZP],
     "orca_hip_h2d": [_P, _P, _P, _SZ],

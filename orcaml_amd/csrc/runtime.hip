@@ -144,6 +144,14 @@ int orca_hip_free(orca_hip_ctx* ctx, void* ptr) {
   });
 }
 
+int orca_hip_free_many(orca_hip_ctx* ctx, void* const* ptrs, size_t n) {
+  return guard([&] {
+    check_ctx(ctx);
+    if (n && !ptrs) fail(ORCA_HIP_ERR_INTERNAL, "free_many: null pointer array");
+    for (size_t i = 0; i < n; ++i) ctx->alloc.release(ptrs[i]);
+  });
+}
+
 int orca_hip_empty_cache(orca_hip_ctx* ctx) {
   return guard([&] {
     bind(ctx);

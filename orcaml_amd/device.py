@@ -14,14 +14,32 @@ class Context:
     (orca_hip_ctx_create).  Plays the role of the process-global backend
     behind global_backend_gpu() (orca-python/src/lib.rs:23-33)."""
 
+    # Dropped buffers are released in batches of this many (orca_hip_free_many): one call
+    # instead of one per storage.  The allocator reuses a block once it is released.
+    RELEASE_BATCH = 64
+
     def __init__(self, device: int = 0):
         h = ctypes.c_void_p()
         _lib.call("orca_hip_ctx_create", device, ctypes.byref(h))
         self.handle = h
         self.device = device
+        self._dropped = []  # device pointers of dropped buffers not yet released
+
+    def release(self, ptr: int) -> None:
+        """Releases a buffer's block (batched; see RELEASE_BATCH)."""
+        dropped = self._dropped
+        dropped.append(ptr)
+        if len(dropped) >= self.RELEASE_BATCH:
+            self.release_dropped()
+
+    def release_dropped(self) -> None:
+        dropped, self._dropped = self._dropped, []
+        if dropped and self.handle:
+            _lib.call("orca_hip_free_many", self.handle, (ctypes.c_void_p * len(dropped))(*dropped), len(dropped))
 
     def close(self) -> None:
         if self.handle:
+            self.release_dropped()
             _lib.call("orca_hip_ctx_destroy", self.handle)
             self.handle = None
 
@@ -51,6 +69,7 @@ class Context:
         _lib.call("orca_hip_d2d", self.handle, dst.ptr, src.ptr, nbytes)
 
     def sync(self) -> None:
+        self.release_dropped()
         _lib.call("orca_hip_sync", self.handle)
 
     def set_ew_jit(self, mode: int) -> None:
@@ -71,11 +90,13 @@ class Context:
         return n.value
 
     def mem_stats(self) -> dict:
+        self.release_dropped()
         live, cached, mallocs = ctypes.c_size_t(), ctypes.c_size_t(), ctypes.c_size_t()
         _lib.call("orca_hip_mem_stats", self.handle, ctypes.byref(live), ctypes.byref(cached), ctypes.byref(mallocs))
         return dict(live=live.value, cached=cached.value, device_allocs=mallocs.value)
 
     def empty_cache(self) -> None:
+        self.release_dropped()
         _lib.call("orca_hip_empty_cache", self.handle)
 
     # ---- timing ----
@@ -108,13 +129,17 @@ class Buffer:
         self.nbytes = nbytes
 
     def free(self) -> None:
+        """Releases the block now."""
         if self.ptr and self.ctx.handle:
             _lib.call("orca_hip_free", self.ctx.handle, self.ptr)
         self.ptr = None
 
     def __del__(self):
+        # a dropped buffer's block is released with the context's next batch
         try:
-            self.free()
+            if self.ptr and self.ctx.handle:
+                self.ctx.release(self.ptr)
+            self.ptr = None
         except Exception:
             pass
 
