@@ -287,6 +287,7 @@ struct HeadBwdParams {
   float* dH;        // [B][K] or null
   float* dW;        // [K][C]
   float* db;        // [C] or null
+  float* dh_colsum; // [K] column sums of dH (the bias gradient of the layer below) or null
   HeadFinish fin;   // block 0 also finishes the forward's loss when fin.loss or fin.correct is set
   int B, K;
   int mask;
@@ -301,7 +302,10 @@ struct HeadBwdParams {
 // A thread keeps W's 4 x C slice for its columns, writes
 // dH = (dlogits W^T) * [H > 0] for its rows and accumulates its 4 x C
 // products of dW in row order; the row lanes are then added by a wave fold
-// and the 8 waves in wave order.  Adjacent panels share 128-byte lines of H
+// and the 8 waves in wave order.  With dh_colsum the block also adds up its
+// 16 columns of dH over all rows the same way (each thread its rows in
+// order, then the fold and the waves): the bias gradient of the layer below,
+// which its weight-gradient product then need not compute.  Adjacent panels share 128-byte lines of H
 // and dH, so they run on one XCD.
 template <int C>
 __global__ void __launch_bounds__(BWD_THREADS) head_backward_kernel(HeadBwdParams p) {
@@ -340,6 +344,7 @@ __global__ void __launch_bounds__(BWD_THREADS) head_backward_kernel(HeadBwdParam
   float adb[C];
 #pragma unroll
   for (int c = 0; c < C; ++c) adb[c] = 0.0f;
+  float adz[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 
   const int ngroups = (p.B + BWD_GROUP - 1) / BWD_GROUP;
   for (int gi = 0; gi < ngroups; ++gi) {
@@ -417,6 +422,10 @@ __global__ void __launch_bounds__(BWD_THREADS) head_backward_kernel(HeadBwdParam
           dz[e] = (!p.mask || hv[e] > 0.0f) ? s : 0.0f;
         }
         *reinterpret_cast<floatx4*>(p.dH + (int64_t)row * p.K + k) = floatx4{dz[0], dz[1], dz[2], dz[3]};
+        if (p.dh_colsum) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) adz[e] = adz[e] + dz[e];
+        }
       }
 #pragma unroll
       for (int e = 0; e < 4; ++e)
@@ -440,6 +449,18 @@ __global__ void __launch_bounds__(BWD_THREADS) head_backward_kernel(HeadBwdParam
 #pragma unroll
     for (int w2 = 1; w2 < NW; ++w2) v = v + part[(w2 * 4 + qq) * NV + j];
     if (k0 + 4 * qq + j / C < p.K) p.dW[(int64_t)k0 * C + tid] = v;
+  }
+  if (p.dh_colsum) {
+    __syncthreads();  // part is read above
+    fold_to_lds<4, 32, 4>(adz, part, 4, wave * 4 + q);
+    __syncthreads();
+    if (tid < 16) {  // column k0 + tid = k0 + 4 qq + e
+      const int qq = tid / 4, e = tid % 4;
+      float v = part[qq * 4 + e];
+#pragma unroll
+      for (int w2 = 1; w2 < NW; ++w2) v = v + part[(w2 * 4 + qq) * 4 + e];
+      if (k0 + tid < p.K) p.dh_colsum[k0 + tid] = v;
+    }
   }
   if (do_db) {
     __syncthreads();
@@ -516,7 +537,7 @@ void head_finish(orca_hip_ctx* ctx, const HeadWorkspace& ws, size_t B, float* lo
 
 void head_backward(orca_hip_ctx* ctx, const float* H, size_t B, size_t K, const float* W, size_t C,
                    const float* dlogits, bool mask, float* dH, float* dW, float* db, const HeadWorkspace* finish,
-                   float* loss, int64_t* correct) {
+                   float* loss, int64_t* correct, float* dh_colsum) {
   if (!head_supported(B, K, C)) fail(ORCA_HIP_ERR_SHAPE, "head_backward: unsupported shape");
   if (!aligned16(H) || !aligned16(W) || (dH && !aligned16(dH)))
     fail(ORCA_HIP_ERR_INTERNAL, "head_backward: H, W and dH must be 16-byte aligned");
@@ -528,6 +549,8 @@ void head_backward(orca_hip_ctx* ctx, const float* H, size_t B, size_t K, const 
   p.dH = dH;
   p.dW = dW;
   p.db = db;
+  if (dh_colsum && !dH) fail(ORCA_HIP_ERR_INTERNAL, "head_backward: dH column sums without dH");
+  p.dh_colsum = dh_colsum;
   if (finish) p.fin = HeadFinish{finish->row_loss, finish->row_correct, loss, correct, 1.0f / (float)B};
   p.B = (int)B;
   p.K = (int)K;

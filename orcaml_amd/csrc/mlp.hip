@@ -61,6 +61,10 @@ struct orca_hip_mlp {
   std::vector<void*> owned;
   bool have_batch = false;
   bool fused_head = false;
+  // With the fused head, its backward kernel also sums dZ of the layer below over the
+  // rows (that layer's bias gradient), so that layer's dW product runs without the
+  // folded column sum (ORCA_HIP_HEAD_DB=0 keeps the fold).
+  bool head_db = false;
   orca_hip::HeadWorkspace head;
   // Second stream (default priority) for the update of layers >= 1, which
   // overlaps the first layer's weight-gradient GEMM; fork / join events.
@@ -142,7 +146,8 @@ void step_body(orca_hip_mlp* m, const AdamWScalars* kdev) {
     float* dz = l > 0 ? m->dz[ping] : nullptr;
     // The backward kernel also adds the forward's row terms into the loss.
     head_backward(ctx, l == 0 ? m->x : m->H[l - 1], B, m->dims[l], m->P + m->off[2 * l], C, m->dlogits, l > 0, dz,
-                  m->G + m->off[2 * l], m->G + m->off[2 * l + 1], &m->head, m->loss, m->correct);
+                  m->G + m->off[2 * l], m->G + m->off[2 * l + 1], &m->head, m->loss, m->correct,
+                  dz && m->head_db ? m->G + m->off[2 * (l - 1) + 1] : nullptr);
     if (dz) {
       g = dz;
       ping ^= 1;
@@ -179,7 +184,8 @@ void step_body(orca_hip_mlp* m, const AdamWScalars* kdev) {
     GemmEpi ew;
     ew.ws = m->gemm_ws;
     ew.ws_floats = m->gemm_ws_floats;
-    ew.colsum = m->G + m->off[2 * l + 1];  // bias gradient
+    // bias gradient (the head's backward kernel already summed the layer below it)
+    ew.colsum = m->head_db && l + 2 == L ? nullptr : m->G + m->off[2 * l + 1];
     gemm(ctx, true, false, K, N, B, a, K, 0, g, N, 0, m->G + m->off[2 * l], N, 0, 1, ew);
     // Layers >= 1 have all their gradients after dW of layer 1; with a second
     // arena nothing of this step writes the P that layer 1's dZ reads.
@@ -342,6 +348,8 @@ int orca_hip_mlp_create(orca_hip_ctx* ctx, const size_t* dims, size_t n_layers, 
     }
     const char* fh = std::getenv("ORCA_HIP_FUSED_HEAD");
     m->fused_head = head_supported(batch, dims[n_layers - 1], C) && !(fh && fh[0] == '0');
+    const char* hd = std::getenv("ORCA_HIP_HEAD_DB");
+    m->head_db = m->fused_head && n_layers > 1 && !(hd && hd[0] == '0');
     m->head.row_loss = m->dev(batch);
     m->head.row_correct = reinterpret_cast<int*>(m->dev(batch));
     if (opt->kind == 1) m->kdev = reinterpret_cast<AdamWScalars*>(m->dev(sizeof(AdamWScalars) / sizeof(float)));

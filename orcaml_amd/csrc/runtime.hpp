@@ -322,7 +322,7 @@ void head_finish(orca_hip_ctx* ctx, const HeadWorkspace& ws, size_t B, float* lo
 // dW, db, dH; when `finish` is set, also what head_finish computes.
 void head_backward(orca_hip_ctx* ctx, const float* H, size_t B, size_t K, const float* W, size_t C,
                    const float* dlogits, bool mask, float* dH, float* dW, float* db, const HeadWorkspace* finish,
-                   float* loss, int64_t* correct);
+                   float* loss, int64_t* correct, float* dh_colsum = nullptr);
 
 // AdamW's per-step f32 scalars: the f64 expressions of python/orca/optim/adamw.py:64-94
 // rounded to f32 as PyO3 passes them.
