@@ -106,6 +106,11 @@ struct orca_hip_mlp {
 namespace orca_hip {
 namespace {
 
+// The fork / mid / join events order the two streams on this device only: no
+// system-scope fence at record (the kernels' own release and acquire are at
+// device scope).  Measured: 0.9163 -> 0.9102 ms per step (median of 6 x 100).
+constexpr unsigned kStreamEventFlags = hipEventDisableTiming | hipEventDisableSystemFence;
+
 // Smallest update (parameters of layers >= 1) worth a second stream.
 constexpr size_t kMinOverlapParams = size_t(1) << 22;
 
@@ -343,8 +348,8 @@ int orca_hip_mlp_create(orca_hip_ctx* ctx, const size_t* dims, size_t n_layers, 
     const size_t overlapped = n_layers > 1 ? o - m->off[2] : 0;
     if (overlapped >= kMinOverlapParams && !(ov && ov[0] == '0')) {
       ORCA_HIP_CHECK(hipStreamCreateWithFlags(&m->side, hipStreamNonBlocking));
-      ORCA_HIP_CHECK(hipEventCreateWithFlags(&m->fork, hipEventDisableTiming));
-      ORCA_HIP_CHECK(hipEventCreateWithFlags(&m->join, hipEventDisableTiming));
+      ORCA_HIP_CHECK(hipEventCreateWithFlags(&m->fork, kStreamEventFlags));
+      ORCA_HIP_CHECK(hipEventCreateWithFlags(&m->join, kStreamEventFlags));
     }
     const char* fh = std::getenv("ORCA_HIP_FUSED_HEAD");
     m->fused_head = head_supported(batch, dims[n_layers - 1], C) && !(fh && fh[0] == '0');
@@ -385,7 +390,7 @@ int orca_hip_mlp_create(orca_hip_ctx* ctx, const size_t* dims, size_t n_layers, 
     if (m->side && opt->kind == 1 && !m->use_graph && !(da && da[0] == '0')) {
       m->P_next = m->dev(o);
       launch_fill(ctx, m->P_next, 0.0f, o);
-      ORCA_HIP_CHECK(hipEventCreateWithFlags(&m->mid, hipEventDisableTiming));
+      ORCA_HIP_CHECK(hipEventCreateWithFlags(&m->mid, kStreamEventFlags));
       const char* sf = std::getenv("ORCA_HIP_SIDE_FRAC");
       const double frac = sf ? std::atof(sf) / 100.0 : 0.7;
       const size_t span = o - m->off[2];
