@@ -176,8 +176,10 @@ hipEvent_t Profiler::get_event() {
     pool.pop_back();
     return e;
   }
+  // Timing only: no system-scope fence at record, so the stop event of a kernel
+  // does not add a cache write-back to its measured duration or to the next launch.
   hipEvent_t e;
-  ORCA_HIP_CHECK(hipEventCreate(&e));
+  ORCA_HIP_CHECK(hipEventCreateWithFlags(&e, hipEventDisableSystemFence));
   return e;
 }
 

@@ -21,6 +21,7 @@ typedef StubEvent* hipEvent_t;
 enum hipMemcpyKind { hipMemcpyHostToHost = 0, hipMemcpyHostToDevice = 1, hipMemcpyDeviceToHost = 2, hipMemcpyDeviceToDevice = 3 };
 #define hipHostMallocDefault 0
 #define hipEventDisableTiming 2
+#define hipEventDisableSystemFence 0x20000000
 
 namespace hip_stub {
 inline int& event_delay() { static int v = 0; return v; }        // queries an event stays pending
