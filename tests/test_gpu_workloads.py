@@ -69,6 +69,36 @@ def test_mlp784_1024_b256_hundred_adamw_steps_teacher_forced(ctx):
     assert tr.step_count() == state["t"] == 100
 
 
+def test_side_stream_update_at_ragged_widths_teacher_forced(ctx):
+    """100-2100-2002-10 at batch 129: more than 2^22 parameters above layer 0, so the update of
+    layers 1-2 runs on the second stream beside the dZ and dW products, reading one parameter
+    arena and writing the other, split at a ragged offset; partial GEMM tiles everywhere.
+    Three steps, each from the GPU's own state (parameters, moments, t): loss and gradients to
+    the path's tolerance (modulo counted ReLU mask flips), new parameters and moments
+    bit-identical to the oracle's AdamW on the GPU's gradients."""
+    dims, batch = (100, 2100, 2002, 10), 129
+    o = dict(kind="adamw", lr=1e-3, weight_decay=0.01)
+    w = dict(dims=dims, batch=batch, opt=o)
+    assert sum(a * b + b for a, b in zip(dims[1:-1], dims[2:])) > 1 << 22
+    params, x, labels, onehot = synth.mlp_problem(11, dims, batch)
+    tr = make_trainer(ctx, w, params)
+    tr.set_batch(x, onehot=onehot)
+    zeros = [np.zeros_like(p) for p in params]
+    state = dict(params=params, m=zeros, v=zeros, t=0)
+    for step in range(3):
+        tr.step()
+        loss, _ = tr.metrics()
+        ref = O.mlp_train(dims, state["params"], x, onehot, ref_opt(w), steps=1, m=state["m"], v=state["v"],
+                          t=state["t"], want_grads=True)
+        ref["hidden"] = oracle_hidden(state["params"], x, dims)
+        hidden = [tr.activation(l) for l in range(len(dims) - 2)]
+        got_g, got_p, got_m, got_v = tr.grads(), tr.params(), tr.moments(0), tr.moments(1)
+        check_teacher_forced_adamw_step(dims, o, state, ref, loss, hidden, got_g, got_p, got_m, got_v,
+                                        what=f"step {step}")
+        state = dict(params=got_p, m=got_m, v=got_v, t=state["t"] + 1)
+    tr.close()
+
+
 def _fraction_outside(got, want):
     bad = sum(int((np.abs(g.astype(np.float64) - w) > 1e-5 + 1e-4 * np.abs(w.astype(np.float64))).sum())
               for g, w in zip(got, want))
