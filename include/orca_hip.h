@@ -57,6 +57,7 @@ extern "C" {
 
 typedef struct orca_hip_ctx orca_hip_ctx;
 typedef struct orca_hip_mlp orca_hip_mlp;
+typedef struct orca_hip_event orca_hip_event;
 
 /* ======================= context, memory, host I/O ======================= */
 
@@ -96,6 +97,22 @@ int orca_hip_sync(orca_hip_ctx* ctx);
  * No counterpart in the reference: it lets a caller check that a span of calls,
  * such as a backward pass and an optimizer step, never waited for the device. */
 int orca_hip_sync_count(const orca_hip_ctx* ctx, uint64_t* count);
+
+/* A second stream per context, and events that order the two.  No counterpart in
+ * the reference, whose backend runs on one queue: a binding uses them to run an
+ * optimizer update of parameters whose gradients are complete beside the backward's
+ * remaining products.  orca_hip_use_side_stream(ctx, b) with b != 0 sends the context's
+ * later launches to the side stream, (ctx, 0) back to the context stream.  Host reads and
+ * orca_hip_sync first make the context stream wait for the side stream's work.
+ * orca_hip_event_record marks the current stream's work so far; orca_hip_event_wait
+ * makes the current stream wait for such a mark (no host wait); orca_hip_event_release
+ * hands the event back for reuse (waits already enqueued are unaffected).  An optimizer pass
+ * launched on the side stream takes at most b blocks per CU when b > 0 (room for a
+ * product that fills the CUs beside it) and its full grid when b < 0. */
+int orca_hip_use_side_stream(orca_hip_ctx* ctx, int blocks_per_cu);
+int orca_hip_event_record(orca_hip_ctx* ctx, orca_hip_event** out);
+int orca_hip_event_wait(orca_hip_ctx* ctx, orca_hip_event* ev);
+int orca_hip_event_release(orca_hip_ctx* ctx, orca_hip_event* ev);
 
 /* =========================== Backend trait ops =========================== */
 /* `shape`/`rank` are the logical shape (Shape, orca-core/src/shape.rs:6).

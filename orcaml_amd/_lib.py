@@ -93,6 +93,10 @@ SIGNATURES = {
     "orca_hip_d2d": [_P, _P, _P, _SZ],
     "orca_hip_fill": [_P, _P, _F, _SZ],
     "orca_hip_sync": [_P],
+    "orca_hip_use_side_stream": [_P, ctypes.c_int],
+    "orca_hip_event_record": [_P, ctypes.POINTER(ctypes.c_void_p)],
+    "orca_hip_event_wait": [_P, _P],
+    "orca_hip_event_release": [_P, _P],
     "orca_hip_sync_count": [_P, ctypes.POINTER(ctypes.c_uint64)],
     "orca_hip_zeros": [_P, _SZP, _SZ, _I, _PP],
     "orca_hip_from_f32_slice": [_P, _SZP, _SZ, _P, _SZ, _PP],

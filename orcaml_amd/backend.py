@@ -44,11 +44,24 @@ b.expand(..)` with or without the ReLU after it (orca-autograd/src/backend.rs:
 too) -- the product runs once with that epilogue (orca_hip_gemm) instead of a
 product and a program.  The epilogue computes the
 same f32 operations on the same product, so the bits are those of the ops.
+
+The fused optimizer passes (`adamw_multi_`, `sgd_multi_`, one launch over many
+parameters) may run part of the update on the context's second stream: a
+weight-gradient product (`matmul` of a transposed view) leaves a mark (an
+event) on its output, and the parameters whose gradients came from a product
+before the step's last one are updated on the side stream as soon as those
+gradients exist, beside the backward's remaining products.  The parameters it
+writes carry the side stream's mark: their first use waits for it on the
+context stream, and what that update reads stays referenced until then, so no
+block is reused early.  Same kernel, same bits.
 """
 from __future__ import annotations
 
+import collections
 import ctypes
+import itertools
 import math
+import os
 import struct
 import sys
 import weakref
@@ -105,9 +118,45 @@ def _broadcast_map(in_shape, out_shape):
     return math.prod(out_shape[i1:]), math.prod(out_shape[i0:i1])
 
 
+class _Mark:
+    """A point in one stream's work (an event), to order the context's two streams.  `keep`
+    holds what work before the mark reads: it stays referenced until the context stream has
+    been made to wait for the mark, so its blocks are not reused before that work is done."""
+
+    __slots__ = ("ctx", "ev", "seq", "keep", "settled")
+    _seq = itertools.count()
+
+    def __init__(self, ctx: Context):
+        self.ctx = ctx
+        self.ev = ctx.event_record()  # on the current stream
+        self.seq = next(_Mark._seq)
+        self.keep = None
+        self.settled = False
+
+    def wait(self) -> None:
+        """The current stream waits for the mark (no host wait)."""
+        self.ctx.event_wait(self.ev)
+
+    def settle(self) -> None:
+        """The context stream waits for the mark (once); the kept storages can go."""
+        if not self.settled:
+            self.settled = True
+            self.ctx.event_wait(self.ev)
+            self.keep = None
+
+    def __del__(self):
+        try:
+            if self.ctx.handle:
+                if self.keep is not None:
+                    self.settle()
+                self.ctx.event_release(self.ev)
+        except Exception:
+            pass
+
+
 class HipStorage:
     __slots__ = ("_buf", "n", "transposed_shape", "_fill", "colsum_waiters", "ident", "_expr", "_ew_ops",
-                 "_ew_leaves", "_prod", "_const", "__weakref__")
+                 "_ew_leaves", "_prod", "_const", "_ready", "_made", "__weakref__")
 
     def __init__(self, buf: Buffer | None, n: int, transposed_shape=None):
         self._buf = buf
@@ -131,6 +180,10 @@ class HipStorage:
         # The value of a one-element storage known on the host (a small upload, uploaded at
         # its first use on the device); dropped by an in-place update.
         self._const = None
+        # Written on the side stream: the mark its first use waits for on the context stream.
+        self._ready = None
+        # Made by a weight-gradient product: the mark just after that launch.
+        self._made = None
 
     def __len__(self) -> int:
         return self.n
@@ -141,6 +194,9 @@ class HipStorage:
 
     @property
     def buf(self) -> Buffer:
+        if self._ready is not None:
+            mark, self._ready = self._ready, None
+            mark.settle()
         if self._expr is not None:
             self._expr[0]._flush(self)
         if self._fill is not None:
@@ -179,11 +235,46 @@ def _numel(shape) -> int:
     return math.prod(int(d) for d in shape)
 
 
+def _split_rows(ptrs, frac):
+    """Splits optimizer segments (p_src, p_dst, g, m, v, n pointers) at `frac` of their elements,
+    on a 64-element boundary (256 bytes, so a split segment keeps its alignment)."""
+    total = sum(p[5] for p in ptrs)
+    cut = int(total * frac) // 64 * 64
+    a, b, acc = [], [], 0
+    for p in ptrs:
+        n = p[5]
+        if acc + n <= cut:
+            a.append(p)
+        elif acc >= cut:
+            b.append(p)
+        else:
+            k = (cut - acc) // 64 * 64
+            shift = tuple(None if q is None else q + 4 * k for q in p[:5])
+            a.append(p[:5] + (k,))
+            b.append(shift + (n - k,))
+        acc += n
+    return [p for p in a if p[5]], [p for p in b if p[5]]
+
+
 class HipBackend:
     """Drop-in for `GpuBackend` (orca-backend-gpu/src/backend.rs:45-50)."""
 
-    def __init__(self, ctx: Context | None = None, deferred: bool = True, lazy: bool = True, fold: bool = True):
+    def __init__(self, ctx: Context | None = None, deferred: bool = True, lazy: bool = True, fold: bool = True,
+                 overlap: bool | None = None):
         self.ctx = ctx if ctx is not None else Context(0)
+        # Part of a fused optimizer pass on the second stream (module docstring); off
+        # (or ORCA_HIP_OVERLAP=0), the whole pass runs on the context stream.
+        self.overlap = os.environ.get("ORCA_HIP_OVERLAP", "1") != "0" if overlap is None else overlap
+        # Backward products (a transposed operand) leave marks once a fused optimizer pass has
+        # asked for them (the last few kept: the pass splits its side-stream part at the one
+        # before the last weight gradient).
+        self._marking = False
+        self._recent = collections.deque(maxlen=8)
+        # The side-stream part: side_frac of it on side_bpc blocks per CU beside the product
+        # after the first weight gradients, the rest on the full grid once the product before
+        # the last weight gradient is done (which leaves CUs idle beside it).
+        self.side_frac = float(os.environ.get("ORCA_HIP_SIDE_FRAC", "70")) / 100.0
+        self.side_bpc = int(os.environ.get("ORCA_HIP_SIDE_BPC", "3")) or -1
         # The identity-reduction memo and the deferred column sum (module
         # docstring); off, every sum_to_shape runs its kernel at once.
         self.deferred = deferred
@@ -290,7 +381,12 @@ class HipBackend:
                 _lib.call("orca_hip_matmul_colsum", self.ctx.handle, lhs.ptr, rhs.ptr, M, K, N, lv, dtype, cs.ptr,
                           ctypes.byref(out))
                 target._buf, target._fill = cs, None
-                return self._wrap(out, M * N)
+                res = self._wrap(out, M * N)
+                if self._marking:
+                    mark = self._mark()
+                    if lv == _lib.VIEW_TRANSPOSED:  # a weight gradient X^T G and its bias gradient
+                        res._made = target._made = mark
+                return res
         if (self.lazy and dtype == _lib.F32 and len(lhs_shape) == 2 and len(rhs_shape) == 2
                 and lhs_shape[1] == rhs_shape[0]):
             M, K, N = int(lhs_shape[0]), int(lhs_shape[1]), int(rhs_shape[1])
@@ -324,6 +420,10 @@ class HipBackend:
                   _lib.VIEW_TRANSPOSED if lt else _lib.VIEW_CONTIGUOUS,
                   _lib.VIEW_TRANSPOSED if rt else _lib.VIEW_CONTIGUOUS, ctypes.byref(out))
         st._buf = Buffer(self.ctx, out.value, 4 * M * N)
+        if self._marking and (lt or rt):  # a backward product
+            mark = self._mark()
+            if lt:  # a weight gradient X^T G
+                st._made = mark
 
     def transpose(self, s: HipStorage, shape, dim0: int, dim1: int, dtype=_lib.F32):
         rank = len(shape)
@@ -502,14 +602,19 @@ class HipBackend:
             return False
         if self._narrow(kind, lt, rt, N, K) != self._narrow(_lib.EPI_NONE, lt, rt, N, K):
             return False  # the plain product runs on another kernel (other sums, other bits)
+        # The operands first: pending work they need is launched before a wait on a mark that a
+        # bias or mask written on the second stream brings in.
+        lp, rp = lhs.ptr, rhs.ptr
         c = self.ctx.alloc(4 * M * N)
         e = _lib.Epilogue(kind, bias.ptr if bias is not None else None, mask.ptr if mask is not None else None,
                           N if mask is not None else 0, None)
         if kind in (_lib.EPI_BIAS_RELU_PRE, _lib.EPI_RELU_MASK_PRE):
             pre = self.ctx.alloc(4 * M * N)
             e.pre = pre.ptr
-        _lib.call("orca_hip_gemm", self.ctx.handle, int(lt), int(rt), M, N, K, lhs.ptr, M if lt else K, rhs.ptr,
+        _lib.call("orca_hip_gemm", self.ctx.handle, int(lt), int(rt), M, N, K, lp, M if lt else K, rp,
                   K if rt else N, c.ptr, N, ctypes.byref(e))
+        if self._marking and (lt or rt):  # a backward product
+            self._mark()
         prod._prod = prod._fill = None
         if kind == _lib.EPI_RELU_MASK_PRE:
             prod._buf, pre = pre, None  # the product itself, for its other holders
@@ -871,17 +976,77 @@ class HipBackend:
         (p_src, p_dst, g, m, v, n) storages; p_dst, m and v are written."""
         rows = [(self._plain(ps), pd, self._plain(g), m, v, n) for ps, pd, g, m, v, n in segs]
         self._mutating(*[r[k] for r in rows for k in (1, 3, 4)])
-        table = (_lib.OptSegment * max(1, len(rows)))(
-            *[(ps.ptr, pd.ptr, g.ptr, m.ptr, v.ptr, n) for ps, pd, g, m, v, n in rows])
-        _lib.call("orca_hip_adamw_multi", self.ctx.handle, table, len(rows), lr, beta1, beta2, eps, weight_decay, t)
+
+        def launch(ptrs):
+            table = (_lib.OptSegment * max(1, len(ptrs)))(*ptrs)
+            _lib.call("orca_hip_adamw_multi", self.ctx.handle, table, len(ptrs), lr, beta1, beta2, eps, weight_decay,
+                      t)
+
+        self._optimizer_pass(rows, 2, 1, lambda r: (r[0].ptr, r[1].ptr, r[2].ptr, r[3].ptr, r[4].ptr, r[5]), launch)
+
+    def _mark(self) -> _Mark:
+        mark = _Mark(self.ctx)
+        self._recent.append(mark)
+        return mark
+
+    def _optimizer_pass(self, rows, gi: int, di: int, ptrs_of, launch) -> None:
+        """Runs launch(pointer rows) for an optimizer pass; rows[k][gi] is a gradient, rows[k][di]
+        the parameter written.  With overlap, the rows whose gradients come from a weight-gradient
+        product before the latest one among them run first, on the side stream, after that
+        product (beside the rest of the backward); the parameters they write are marked, and what
+        they read is kept until the context stream waits for the mark.  The other rows (gradients
+        of the latest product, or of no marked product) run on the context stream.  Gradients
+        still pending are computed first, the last row's last, as a backward pass makes them.
+        The side-stream part is split like the trainer's update: side_frac of it on a bounded grid
+        beside the product after those gradients, the rest on the full grid once the product
+        before the latest weight gradient is done."""
+        self._marking = self.overlap
+        if self.overlap:  # gradients still pending run now, the last parameter's last (backward order)
+            for r in reversed(rows):
+                if r[gi].pending:
+                    r[gi].buf
+        marks = [r[gi]._made for r in rows] if self.overlap else []
+        known = [m for m in marks if m is not None]
+        last = max((m.seq for m in known), default=None)
+        early = [m for m in known if m.seq != last]
+        side = [r for r, m in zip(rows, marks) if m is not None and m.seq != last] if early else []
+        here = [r for r, m in zip(rows, marks) if m is None or m.seq == last] if early else rows
+        if side:
+            after = max(early, key=lambda m: m.seq)  # the same stream's earlier marks come before it
+            mid = max((m for m in self._recent if after.seq < m.seq < last), key=lambda m: m.seq, default=None)
+            ptrs = [ptrs_of(r) for r in side]  # pending values settled on the context stream first
+            parts = [(after, self.side_bpc, ptrs)]
+            if mid is not None and self.side_frac < 1.0:
+                a, b = _split_rows(ptrs, self.side_frac)
+                parts = [(after, self.side_bpc, a), (mid, -1, b)]
+            done = None
+            for mark, bpc, part in parts:
+                if not part:
+                    continue
+                self.ctx.use_side_stream(bpc)
+                try:
+                    mark.wait()
+                    launch(part)
+                    done = _Mark(self.ctx)  # the side stream's work so far
+                finally:
+                    self.ctx.use_side_stream(0)
+            if done is not None:
+                done.keep = [tuple(x for k, x in enumerate(r) if k != di) for r in side]
+                for r in side:
+                    r[di]._ready = done
+        if here:
+            launch([ptrs_of(r) for r in here])
 
     def sgd_multi_(self, segs, lr: float) -> None:
         """One SGD pass over many parameters (orca_hip_sgd_multi): segs holds (p_src, p_dst, g, n)."""
         rows = [(self._plain(ps), pd, self._plain(g), n) for ps, pd, g, n in segs]
         self._mutating(*[r[1] for r in rows])
-        table = (_lib.OptSegment * max(1, len(rows)))(
-            *[(ps.ptr, pd.ptr, g.ptr, None, None, n) for ps, pd, g, n in rows])
-        _lib.call("orca_hip_sgd_multi", self.ctx.handle, table, len(rows), lr)
+
+        def launch(ptrs):
+            table = (_lib.OptSegment * max(1, len(ptrs)))(*ptrs)
+            _lib.call("orca_hip_sgd_multi", self.ctx.handle, table, len(ptrs), lr)
+
+        self._optimizer_pass(rows, 2, 1, lambda r: (r[0].ptr, r[1].ptr, r[2].ptr, None, None, r[3]), launch)
 
     def sgd_step_(self, p: HipStorage, g: HipStorage, n: int, lr: float) -> None:
         """In place on p (orca_hip_sgd_step)."""

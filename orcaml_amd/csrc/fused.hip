@@ -442,9 +442,7 @@ __device__ __forceinline__ int opt_segment(const OptSegs& s, uint64_t q) {
 }
 
 template <bool ADAMW>
-__global__ void __launch_bounds__(256) opt_multi_kernel(OptSegs s, AdamWScalars k, float lr) {
-  const uint64_t q = (uint64_t)blockIdx.x * 256 + threadIdx.x;
-  if (q >= s.start4[s.count]) return;
+__device__ __forceinline__ void opt_multi_group(const OptSegs& s, const AdamWScalars& k, float lr, uint64_t q) {
   const int i = opt_segment(s, q);
   const uint64_t e0 = 4 * (q - s.start4[i]);
   const uint64_t n = s.n[i];
@@ -483,6 +481,14 @@ __global__ void __launch_bounds__(256) opt_multi_kernel(OptSegs s, AdamWScalars 
       s.pd[i][e] = s.ps[i][e] - s.g[i][e] * lr;
     }
   }
+}
+
+// One float4 group per thread on the full grid; a bounded grid (a pass beside
+// other work) strides over the groups.
+template <bool ADAMW>
+__global__ void __launch_bounds__(256) opt_multi_kernel(OptSegs s, AdamWScalars k, float lr) {
+  const uint64_t total = s.start4[s.count], stride = (uint64_t)gridDim.x * 256;
+  for (uint64_t q = (uint64_t)blockIdx.x * 256 + threadIdx.x; q < total; q += stride) opt_multi_group<ADAMW>(s, k, lr, q);
 }
 
 __global__ void __launch_bounds__(256) sgd_vec_kernel(float4* __restrict__ p, const float4* __restrict__ g, size_t n4, float lr) {
@@ -676,9 +682,15 @@ void opt_multi(orca_hip_ctx* ctx, const orca_hip_opt_segment* segs, size_t n_seg
     }
     t.start4[t.count] = total4;
     if (total4 == 0) continue;
-    const uint64_t blocks = (total4 + 255) / 256;
+    // On the side stream the pass may run beside a product that fills the CUs: a
+    // bounded grid leaves it room to launch its own blocks.
+    const uint64_t full = (total4 + 255) / 256;
+    const uint64_t blocks =
+        ctx->main && ctx->side_bpc > 0 ? std::min<uint64_t>(full, (uint64_t)ctx->side_bpc * ctx->num_cus) : full;
     if (blocks > 0x7fffffffu) fail(ORCA_HIP_ERR_INTERNAL, "optimizer: too many parameters for one launch");
-    ProfScope ps(ctx, adamw_ ? "adamw_multi" : "sgd_multi", 0.0, bytes);
+    ProfScope ps(ctx, ctx->main ? (adamw_ ? "adamw_multi_overlapped" : "sgd_multi_overlapped")
+                                : (adamw_ ? "adamw_multi" : "sgd_multi"),
+                 0.0, bytes);
     if (adamw_)
       hipLaunchKernelGGL(opt_multi_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, ctx->stream, t, k, lr);
     else

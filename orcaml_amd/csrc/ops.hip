@@ -624,6 +624,7 @@ int orca_hip_to_f32_vec(orca_hip_ctx* ctx, const void* s, size_t n, float* host_
     bind(ctx);
     if (!n) return;
     check_extent(ctx, s, n * sizeof(float), "to_f32_vec");
+    join_side(ctx);
     ORCA_HIP_CHECK(hipMemcpyAsync(host_out, s, n * sizeof(float), hipMemcpyDeviceToHost, ctx->stream));
     host_sync(ctx);
   });
@@ -649,6 +650,7 @@ int orca_hip_to_bytes(orca_hip_ctx* ctx, const void* s, size_t n_bytes, uint8_t*
     bind(ctx);
     if (!n_bytes) return;
     check_extent(ctx, s, n_bytes, "to_bytes");
+    join_side(ctx);
     ORCA_HIP_CHECK(hipMemcpyAsync(host_out, s, n_bytes, hipMemcpyDeviceToHost, ctx->stream));
     host_sync(ctx);
   });

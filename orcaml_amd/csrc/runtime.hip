@@ -111,13 +111,81 @@ int orca_hip_ctx_destroy(orca_hip_ctx* ctx) {
   return guard([&] {
     if (!ctx) return;
     bind(ctx);
+    if (ctx->main) ctx->stream = ctx->main;
+    if (ctx->side) (void)hipStreamSynchronize(ctx->side);
     (void)hipStreamSynchronize(ctx->stream);
     ew_jit_release(ctx);
     if (ctx->timer_start) (void)hipEventDestroy(ctx->timer_start);
     if (ctx->timer_stop) (void)hipEventDestroy(ctx->timer_stop);
-    hipStream_t s = ctx->stream;
+    if (ctx->side_last) (void)hipEventDestroy(ctx->side_last);
+    for (hipEvent_t ev : ctx->event_pool) (void)hipEventDestroy(ev);
+    hipStream_t s = ctx->stream, side = ctx->side;
     delete ctx;  // allocator and profiler release their resources
     if (s) (void)hipStreamDestroy(s);
+    if (side) (void)hipStreamDestroy(side);
+  });
+}
+
+// Events that order the two streams of one context: no system-scope fence at
+// record (the kernels' own release and acquire are at device scope).
+static constexpr unsigned kOrderEventFlags = hipEventDisableTiming | hipEventDisableSystemFence;
+
+int orca_hip_use_side_stream(orca_hip_ctx* ctx, int blocks_per_cu) {
+  return guard([&] {
+    bind(ctx);
+    if (blocks_per_cu) {
+      if (ctx->main) fail(ORCA_HIP_ERR_INTERNAL, "launches already go to the side stream");
+      if (!ctx->side) {
+        ORCA_HIP_CHECK(hipStreamCreateWithFlags(&ctx->side, hipStreamNonBlocking));
+        ORCA_HIP_CHECK(hipEventCreateWithFlags(&ctx->side_last, kOrderEventFlags));
+      }
+      ctx->main = ctx->stream;
+      ctx->stream = ctx->side;
+      ctx->side_bpc = blocks_per_cu > 0 ? blocks_per_cu : 0;
+    } else {
+      if (!ctx->main) fail(ORCA_HIP_ERR_INTERNAL, "launches do not go to the side stream");
+      ORCA_HIP_CHECK(hipEventRecord(ctx->side_last, ctx->side));
+      ctx->side_joined = false;
+      ctx->stream = ctx->main;
+      ctx->main = nullptr;
+    }
+  });
+}
+
+int orca_hip_event_record(orca_hip_ctx* ctx, orca_hip_event** out) {
+  return guard([&] {
+    bind(ctx);
+    if (!out) fail(ORCA_HIP_ERR_INTERNAL, "null output pointer");
+    hipEvent_t ev = nullptr;
+    if (!ctx->event_pool.empty()) {
+      ev = ctx->event_pool.back();
+      ctx->event_pool.pop_back();
+    } else {
+      ORCA_HIP_CHECK(hipEventCreateWithFlags(&ev, kOrderEventFlags));
+    }
+    const hipError_t e = hipEventRecord(ev, ctx->stream);
+    if (e != hipSuccess) {
+      (void)hipEventDestroy(ev);
+      ORCA_HIP_CHECK(e);
+    }
+    *out = reinterpret_cast<orca_hip_event*>(ev);
+  });
+}
+
+int orca_hip_event_wait(orca_hip_ctx* ctx, orca_hip_event* ev) {
+  return guard([&] {
+    bind(ctx);
+    if (!ev) fail(ORCA_HIP_ERR_INTERNAL, "null event");
+    ORCA_HIP_CHECK(hipStreamWaitEvent(ctx->stream, reinterpret_cast<hipEvent_t>(ev), 0));
+  });
+}
+
+// A wait already enqueued keeps the record it was enqueued after, so a released
+// event can be recorded again.
+int orca_hip_event_release(orca_hip_ctx* ctx, orca_hip_event* ev) {
+  return guard([&] {
+    check_ctx(ctx);
+    if (ev) ctx->event_pool.push_back(reinterpret_cast<hipEvent_t>(ev));
   });
 }
 
@@ -181,6 +249,7 @@ int orca_hip_d2h(orca_hip_ctx* ctx, void* dst, const void* src, size_t bytes) {
     bind(ctx);
     if (!bytes) return;
     check_extent(ctx, src, bytes, "d2h");
+    join_side(ctx);
     ORCA_HIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream));
     host_sync(ctx);
   });

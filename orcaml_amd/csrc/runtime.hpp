@@ -183,6 +183,18 @@ struct orca_hip_ctx {
   // program, 1 compiles a program structure at its second use, 2 at its first.
   orca_hip::EwJitCache* ew_jit = nullptr;
   int ew_jit_mode = 1;
+  // A second stream (default priority) for work that runs beside the context
+  // stream: while launches go to it (orca_hip_use_side_stream), `main` holds
+  // the context stream.  `side_last` marks the side stream's work so far;
+  // host reads and synchronisations first make the context stream wait for it.
+  hipStream_t side = nullptr;
+  hipStream_t main = nullptr;
+  hipEvent_t side_last = nullptr;
+  bool side_joined = true;
+  // Blocks per CU of an optimizer pass launched on the side stream (0: the full grid).
+  int side_bpc = 0;
+  // Released ordering events, reused by orca_hip_event_record.
+  std::vector<hipEvent_t> event_pool;
 };
 
 namespace orca_hip {
@@ -261,6 +273,8 @@ inline unsigned grid_for(size_t work_items, unsigned block, unsigned max_blocks)
 // Every host wait the library performs goes through these two, which count it
 // in ctx->host_syncs (reported by orca_hip_sync_count).
 void host_sync(orca_hip_ctx* ctx, hipStream_t stream = nullptr);
+// The context stream waits for the side stream's work so far (no host wait).
+void join_side(orca_hip_ctx* ctx);
 void host_wait_event(orca_hip_ctx* ctx, hipEvent_t ev);
 // Stream-ordered host-to-device copy that does not wait for the device: small
 // payloads travel as a kernel argument, larger ones through the staging ring.

@@ -223,8 +223,16 @@ ProfScope::~ProfScope() {
 }
 
 // ------------------------------------------------------------ host waits and uploads
+void join_side(orca_hip_ctx* ctx) {
+  if (ctx->side && !ctx->side_joined && !ctx->main) {
+    ORCA_HIP_CHECK(hipStreamWaitEvent(ctx->stream, ctx->side_last, 0));
+    ctx->side_joined = true;
+  }
+}
+
 void host_sync(orca_hip_ctx* ctx, hipStream_t stream) {
   ctx->host_syncs.fetch_add(1, std::memory_order_relaxed);
+  if (!stream || stream == ctx->stream) join_side(ctx);
   ORCA_HIP_CHECK(hipStreamSynchronize(stream ? stream : ctx->stream));
 }
 

@@ -72,6 +72,26 @@ class Context:
         self.release_dropped()
         _lib.call("orca_hip_sync", self.handle)
 
+    # ---- the second stream (orca_hip_use_side_stream) and events that order the two ----
+    def use_side_stream(self, blocks_per_cu: int) -> None:
+        """Later launches go to the second stream (blocks_per_cu != 0: an optimizer pass there
+        takes at most that many blocks per CU if > 0, its full grid if < 0) or back (0)."""
+        _lib.call("orca_hip_use_side_stream", self.handle, int(blocks_per_cu))
+
+    def event_record(self) -> int:
+        """An event marking the current stream's work so far (orca_hip_event_record)."""
+        ev = ctypes.c_void_p()
+        _lib.call("orca_hip_event_record", self.handle, ctypes.byref(ev))
+        return ev.value
+
+    def event_wait(self, ev: int) -> None:
+        """The current stream waits for `ev` (no host wait)."""
+        _lib.call("orca_hip_event_wait", self.handle, ev)
+
+    def event_release(self, ev: int) -> None:
+        """Hands an event back for reuse (waits already enqueued are unaffected)."""
+        _lib.call("orca_hip_event_release", self.handle, ev)
+
     def set_ew_jit(self, mode: int) -> None:
         """How fused elementwise programs run (orca_hip_ew_set_jit): 0 interpreted, 1 compiled
         at a structure's second use (the default), 2 at its first."""

@@ -26,6 +26,7 @@ enum hipMemcpyKind { hipMemcpyHostToHost = 0, hipMemcpyHostToDevice = 1, hipMemc
 namespace hip_stub {
 inline int& event_delay() { static int v = 0; return v; }        // queries an event stays pending
 inline long& device_mallocs() { static long v = 0; return v; }
+inline long& stream_waits() { static long v = 0; return v; }
 inline long& device_frees() { static long v = 0; return v; }
 inline long& stream_syncs() { static long v = 0; return v; }
 inline long& event_syncs() { static long v = 0; return v; }
@@ -82,6 +83,10 @@ inline hipError_t hipEventRecord(hipEvent_t e, hipStream_t) {
   e->recorded = true;
   e->queries_left = hip_stub::event_delay();
   return hipSuccess;
+}
+inline hipError_t hipStreamWaitEvent(hipStream_t, hipEvent_t e, unsigned) {
+  ++hip_stub::stream_waits();
+  return e && e->recorded ? hipSuccess : hipErrorInvalidValue;
 }
 inline hipError_t hipEventQuery(hipEvent_t e) {
   if (e->queries_left > 0) {

@@ -110,3 +110,39 @@ def test_composed_mlp784_1024_b256_teacher_forced(hb, fused):
                      v=[v.reshape(s.shape) for v, s in zip(new_v, params)], t=state["t"] + 1)
     print(f"composed 784-1024-1024-10 ({'fused' if fused else 'unchanged'}) teacher-forced: {total} mask flips")
     assert run.opt.t == 12
+
+
+@pytest.mark.parametrize("wl", [synth.MLP_LARGE, synth.MLP_SMALL])
+def test_fused_update_on_second_stream_changes_no_bit(ctx, wl):
+    """The fused optimizer pass (AdamW at 784-4096-4096-10 / B 1024, SGD at 784-128-128-10 /
+    B 64) updates the parameters whose gradients an earlier weight-gradient product made on the
+    context's second stream, beside the backward's remaining products.  Four steps of the
+    drop-in path with the fused loss and optimizer, with and without that, from the same start,
+    and no host read in between: parameters and moments bit-identical, and the second stream
+    took part from the second step on."""
+    from orcaml_amd.backend import HipBackend
+
+    w = synth.WORKLOADS[wl]
+    o = w["opt"]
+    params, x, labels, onehot = synth.mlp_problem(w["seed"], w["dims"], w["batch"])
+    out = {}
+    for overlap in (True, False):
+        ad = A.Autodiff(HipBackend(ctx, overlap=overlap))
+        model = A.build_mlp(ad, params)
+        if o["kind"] == "adamw":
+            opt = A.AdamW(model.parameters(), lr=o["lr"], weight_decay=o["weight_decay"], fused=True)
+        else:
+            opt = A.SGD(model.parameters(), lr=o["lr"], fused=True)
+        loss_fn = A.CrossEntropyLoss(fused=True)
+        xt, tt = A.Tensor.from_numpy(ad, x), A.Tensor.from_numpy(ad, onehot)
+        for _ in range(4):
+            opt.zero_grad()
+            loss_fn(model(xt), tt).backward()
+            opt.step()
+        marked = sum(p.tensor.storage.primal._ready is not None for p in model.parameters())
+        assert (marked > 0) == overlap, marked
+        out[overlap] = [p.tensor.numpy() for p in model.parameters()]
+        if o["kind"] == "adamw":
+            out[overlap] += [m.numpy() for m in opt.m] + [v.numpy() for v in opt.v]
+    for i, (a, b) in enumerate(zip(out[True], out[False])):
+        np.testing.assert_array_equal(a, b, err_msg=f"array {i}")
