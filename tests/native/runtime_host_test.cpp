@@ -136,6 +136,31 @@ static void waits_and_profiler(orca_hip_ctx& ctx) {
   ctx.prof.enabled = false;
 }
 
+// A host wait on the context stream first makes it wait for the side stream's
+// work (once per recording), and not while launches go to the side stream.
+static void side_stream_join(orca_hip_ctx& ctx) {
+  hipStream_t side = reinterpret_cast<hipStream_t>(&ctx);  // any non-null handle: the stand-in ignores it
+  CHECK(hipEventCreate(&ctx.side_last) == hipSuccess);
+  CHECK(hipEventRecord(ctx.side_last, side) == hipSuccess);
+  ctx.side = side;
+  ctx.side_joined = false;
+  const long waits = hip_stub::stream_waits();
+  host_sync(&ctx);
+  CHECK(hip_stub::stream_waits() == waits + 1 && ctx.side_joined);
+  host_sync(&ctx);
+  CHECK(hip_stub::stream_waits() == waits + 1);
+  ctx.side_joined = false;
+  ctx.main = side;  // launches on the side stream (the stand-in handle): no join
+  join_side(&ctx);
+  CHECK(hip_stub::stream_waits() == waits + 1 && !ctx.side_joined);
+  ctx.main = nullptr;
+  join_side(&ctx);
+  CHECK(hip_stub::stream_waits() == waits + 2 && ctx.side_joined);
+  CHECK(hipEventDestroy(ctx.side_last) == hipSuccess);
+  ctx.side_last = nullptr;
+  ctx.side = nullptr;
+}
+
 int main() {
   {
     orca_hip_ctx ctx;
@@ -145,6 +170,7 @@ int main() {
     out_of_memory_retry(ctx);
     staging_ring(ctx);
     waits_and_profiler(ctx);
+    side_stream_join(ctx);
     ctx.alloc.empty(nullptr);
   }  // the context's destructor frees every block, event and the pinned ring
   CHECK(hip_stub::device_mallocs() == hip_stub::device_frees());
