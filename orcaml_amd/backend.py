@@ -273,8 +273,8 @@ class HipBackend:
         # The side-stream part: side_frac of it on side_bpc blocks per CU beside the product
         # after the first weight gradients, the rest on the full grid once the product before
         # the last weight gradient is done (which leaves CUs idle beside it).
-        self.side_frac = float(os.environ.get("ORCA_HIP_SIDE_FRAC", "70")) / 100.0
-        self.side_bpc = int(os.environ.get("ORCA_HIP_SIDE_BPC", "3")) or -1
+        self.side_frac = float(os.environ.get("ORCA_HIP_OPT_SIDE_FRAC", "70")) / 100.0
+        self.side_bpc = int(os.environ.get("ORCA_HIP_OPT_SIDE_BPC", "3")) or -1
         # The identity-reduction memo and the deferred column sum (module
         # docstring); off, every sum_to_shape runs its kernel at once.
         self.deferred = deferred
