@@ -139,6 +139,8 @@ class _Mark:
 
     def settle(self) -> None:
         """The context stream waits for the mark (once); the kept storages can go."""
+        if self.ctx.on_side:
+            raise RuntimeError("a marked storage was used while launches go to the second stream")
         if not self.settled:
             self.settled = True
             self.ctx.event_wait(self.ev)

@@ -24,6 +24,7 @@ class Context:
         self.handle = h
         self.device = device
         self._dropped = []  # device pointers of dropped buffers not yet released
+        self.on_side = False  # launches go to the second stream (use_side_stream)
 
     def release(self, ptr: int) -> None:
         """Releases a buffer's block (batched; see RELEASE_BATCH)."""
@@ -77,6 +78,7 @@ class Context:
         """Later launches go to the second stream (blocks_per_cu != 0: an optimizer pass there
         takes at most that many blocks per CU if > 0, its full grid if < 0) or back (0)."""
         _lib.call("orca_hip_use_side_stream", self.handle, int(blocks_per_cu))
+        self.on_side = blocks_per_cu != 0
 
     def event_record(self) -> int:
         """An event marking the current stream's work so far (orca_hip_event_record)."""
