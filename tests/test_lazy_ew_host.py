@@ -268,3 +268,42 @@ def test_flushed_chains_leave_no_reference_cycles(fake):
         assert all(w() is None for w in watch)
     finally:
         gc.enable()
+
+
+@pytest.mark.parametrize("frac", [0.0, 0.3, 0.7, 0.999, 1.0])
+def test_side_update_split_keeps_every_element_once(frac):
+    """_split_rows (the fused optimizer's update on the second stream, split between a bounded
+    and a full grid): every element of every segment lands in exactly one part, in order; a
+    split segment is cut at a multiple of 64 elements with all its pointers advanced by the
+    same bytes (so the halves stay 256-byte aligned); absent moment pointers stay absent."""
+    sizes = [4096 * 4096, 4096, 40960, 10, 1, 64, 127]
+    ptrs, base = [], 1 << 20
+    for n in sizes:
+        ptrs.append((base, base + (1 << 32), base + (2 << 32), None if n == 10 else base + (3 << 32),
+                     None if n == 10 else base + (4 << 32), n))
+        base += 4 * n + 256
+    a, b = B._split_rows(ptrs, frac)
+    cut = int(sum(sizes) * frac) // 64 * 64
+    assert cut - 64 < sum(p[5] for p in a) <= cut or not b
+    covered = {}
+    for p in a + b:
+        for k in range(5):
+            if p[k] is not None:
+                covered.setdefault(k, []).append((p[k], p[k] + 4 * p[5]))
+    for k in range(5):
+        spans = sorted(covered[k])
+        want = sorted((q[k], q[k] + 4 * q[5]) for q in ptrs if q[k] is not None)
+        merged = []
+        for lo, hi in spans:
+            if merged and merged[-1][1] == lo:
+                merged[-1] = (merged[-1][0], hi)
+            else:
+                merged.append((lo, hi))
+        assert merged == want, k
+    for p in a + b:
+        assert p[5] > 0
+        src = next(q for q in ptrs if q[0] <= p[0] < q[0] + 4 * q[5])
+        off = p[0] - src[0]
+        assert off % 256 == 0
+        assert all((p[k] is None) == (src[k] is None) for k in range(5))
+        assert all(p[k] - src[k] == off for k in range(5) if p[k] is not None)
