@@ -915,7 +915,7 @@ class AdamW(Optimizer):
             active = {i for i, _, _ in grads}
 
             def run(segs):
-                ad.inner.adamw_multi_([(ps, pd, g, flat.moment("m", i), flat.moment("v", i), flat.sizes[i])
+                ad.inner.adamw_multi_([(ps, pd, g, self.m[i].storage.primal, self.v[i].storage.primal, flat.sizes[i])
                                        for i, ps, pd, g in segs if i in active],
                                       self.lr, self.beta1, self.beta2, self.eps, self.weight_decay, self.t)
 

@@ -984,19 +984,21 @@ class HipBackend:
             _lib.call("orca_hip_adamw_multi", self.ctx.handle, table, len(ptrs), lr, beta1, beta2, eps, weight_decay,
                       t)
 
-        self._optimizer_pass(rows, 2, 1, lambda r: (r[0].ptr, r[1].ptr, r[2].ptr, r[3].ptr, r[4].ptr, r[5]), launch)
+        self._optimizer_pass(rows, 2, (1, 3, 4), lambda r: (r[0].ptr, r[1].ptr, r[2].ptr, r[3].ptr, r[4].ptr, r[5]),
+                             launch)
 
     def _mark(self) -> _Mark:
         mark = _Mark(self.ctx)
         self._recent.append(mark)
         return mark
 
-    def _optimizer_pass(self, rows, gi: int, di: int, ptrs_of, launch) -> None:
-        """Runs launch(pointer rows) for an optimizer pass; rows[k][gi] is a gradient, rows[k][di]
-        the parameter written.  With overlap, the rows whose gradients come from a weight-gradient
-        product before the latest one among them run first, on the side stream, after that
-        product (beside the rest of the backward); the parameters they write are marked, and what
-        they read is kept until the context stream waits for the mark.  The other rows (gradients
+    def _optimizer_pass(self, rows, gi: int, written, ptrs_of, launch) -> None:
+        """Runs launch(pointer rows) for an optimizer pass; rows[k][gi] is a gradient, rows[k][w]
+        for w in `written` the storages written (parameter, moments).  With overlap, the rows whose
+        gradients come from a weight-gradient product before the latest one among them run first,
+        on the side stream, after that product (beside the rest of the backward); the storages
+        they write are marked, and what they only read is kept until the context stream waits
+        for the mark.  The other rows (gradients
         of the latest product, or of no marked product) run on the context stream.  Gradients
         still pending are computed first, the last row's last, as a backward pass makes them.
         The side-stream part is split like the trainer's update: side_frac of it on a bounded grid
@@ -1033,9 +1035,10 @@ class HipBackend:
                 finally:
                     self.ctx.use_side_stream(0)
             if done is not None:
-                done.keep = [tuple(x for k, x in enumerate(r) if k != di) for r in side]
+                done.keep = [tuple(x for k, x in enumerate(r) if k not in written) for r in side]
                 for r in side:
-                    r[di]._ready = done
+                    for k in written:
+                        r[k]._ready = done
         if here:
             launch([ptrs_of(r) for r in here])
 
@@ -1048,7 +1051,7 @@ class HipBackend:
             table = (_lib.OptSegment * max(1, len(ptrs)))(*ptrs)
             _lib.call("orca_hip_sgd_multi", self.ctx.handle, table, len(ptrs), lr)
 
-        self._optimizer_pass(rows, 2, 1, lambda r: (r[0].ptr, r[1].ptr, r[2].ptr, None, None, r[3]), launch)
+        self._optimizer_pass(rows, 2, (1,), lambda r: (r[0].ptr, r[1].ptr, r[2].ptr, None, None, r[3]), launch)
 
     def sgd_step_(self, p: HipStorage, g: HipStorage, n: int, lr: float) -> None:
         """In place on p (orca_hip_sgd_step)."""

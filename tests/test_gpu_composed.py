@@ -141,8 +141,12 @@ def test_fused_update_on_second_stream_changes_no_bit(ctx, wl):
             opt.step()
         marked = sum(p.tensor.storage.primal._ready is not None for p in model.parameters())
         assert (marked > 0) == overlap, marked
+        # a snapshot of the moments first: device copies on the context stream, taken right
+        # after the step, while the second stream may still be writing them
+        snap = opt.state_dict() if o["kind"] == "adamw" else {}
         out[overlap] = [p.tensor.numpy() for p in model.parameters()]
         if o["kind"] == "adamw":
             out[overlap] += [m.numpy() for m in opt.m] + [v.numpy() for v in opt.v]
+            out[overlap] += [snap[k].numpy() for k in sorted(k for k in snap if k != "t")]
     for i, (a, b) in enumerate(zip(out[True], out[False])):
         np.testing.assert_array_equal(a, b, err_msg=f"array {i}")
