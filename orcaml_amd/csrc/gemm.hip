@@ -27,6 +27,8 @@
 #include <string>
 #include <type_traits>
 
+#include <hip/hip_ext.h>
+
 #include "runtime.hpp"
 
 namespace orca_hip {
@@ -1253,9 +1255,12 @@ size_t gemm_workspace_floats(orca_hip_ctx* ctx, bool trans_a, bool trans_b, size
   return plan_workspace_floats(g, M, N, batch, colsum && batch == 1 && !trans_b);
 }
 
-void gemm(orca_hip_ctx* ctx, bool trans_a, bool trans_b, size_t M, size_t N, size_t K, const float* A, size_t lda,
-          size_t sa, const float* B, size_t ldb, size_t sb, float* C, size_t ldc, size_t sc, size_t batch,
-          const GemmEpi& epi) {
+namespace {
+// gemm() without epi.done; sets `bound` when the pipelined kernel was
+// launched with epi.done as its completion event.
+void gemm_launch(orca_hip_ctx* ctx, bool trans_a, bool trans_b, size_t M, size_t N, size_t K, const float* A,
+                 size_t lda, size_t sa, const float* B, size_t ldb, size_t sb, float* C, size_t ldc, size_t sc,
+                 size_t batch, const GemmEpi& epi, bool& bound) {
   if (M == 0 || N == 0 || batch == 0) return;
   if (M > INT32_MAX || N > INT32_MAX || K > INT32_MAX || batch > 65535)
     fail(ORCA_HIP_ERR_INTERNAL, "gemm dimensions exceed the kernel's index range");
@@ -1384,9 +1389,19 @@ void gemm(orca_hip_ctx* ctx, bool trans_a, bool trans_b, size_t M, size_t N, siz
     else if (trans_a && !trans_b) GEMM_LAUNCH(BM_, BN_, true, false); \
     else GEMM_LAUNCH(BM_, BN_, true, true);                          \
   } while (0)
-#define FAST_LAUNCH(TA_, TB_, CS_) \
-  hipLaunchKernelGGL((gemm_mfma_f32_fast_kernel<TA_, TB_, CS_>), grid, dim3(NTHREADS), 0, ctx->stream, p)
+#define FAST_LAUNCH(TA_, TB_, CS_)                                                                        \
+  do {                                                                                                     \
+    if (bind)                                                                                              \
+      hipExtLaunchKernelGGL((gemm_mfma_f32_fast_kernel<TA_, TB_, CS_>), grid, dim3(NTHREADS), 0, ctx->stream, \
+                            nullptr, epi.done, 0, p);                                                      \
+    else                                                                                                   \
+      hipLaunchKernelGGL((gemm_mfma_f32_fast_kernel<TA_, TB_, CS_>), grid, dim3(NTHREADS), 0, ctx->stream, p); \
+  } while (0)
+    // The pipelined kernel is the product's last launch unless a split
+    // reduce or a separate column sum follows it.
+    const bool bind = epi.done && splits == 1 && (!epi.colsum || fold_colsum);
     if (fast) {
+      bound = bind;
       // The column sum reads only B's LDS tile (row-major B), so it folds in
       // whatever A's layout is.
       const bool cs = p.colsum != nullptr;
@@ -1454,6 +1469,15 @@ void gemm(orca_hip_ctx* ctx, bool trans_a, bool trans_b, size_t M, size_t N, siz
     if (trans_b) fail(ORCA_HIP_ERR_INTERNAL, "gemm colsum epilogue requires row-major B");
     launch_colsum(ctx, B, K, N, ldb, epi.colsum);
   }
+}
+}  // namespace
+
+void gemm(orca_hip_ctx* ctx, bool trans_a, bool trans_b, size_t M, size_t N, size_t K, const float* A, size_t lda,
+          size_t sa, const float* B, size_t ldb, size_t sb, float* C, size_t ldc, size_t sc, size_t batch,
+          const GemmEpi& epi) {
+  bool bound = false;
+  gemm_launch(ctx, trans_a, trans_b, M, N, K, A, lda, sa, B, ldb, sb, C, ldc, sc, batch, epi, bound);
+  if (epi.done && !bound) ORCA_HIP_CHECK(hipEventRecord(epi.done, ctx->stream));
 }
 
 }  // namespace orca_hip

@@ -83,6 +83,8 @@ struct orca_hip_mlp {
   // keeping several float4 groups of each array in flight: 15.2 against 16.0 us on the flat
   // grid for 784-4096 (ORCA_HIP_U0_BPC; 0 = the flat grid).
   int u0_bpc = 8;
+  // fork / mid events bound to the completion of the GEMM before them
+  bool bind_events = true;
   size_t side_a = 0;
   // Persistent workspaces: a step makes no allocator call, so it can be
   // captured once into a HIP graph and replayed.
@@ -195,12 +197,15 @@ void step_body(orca_hip_mlp* m, const AdamWScalars* kdev) {
     ew.ws_floats = m->gemm_ws_floats;
     // bias gradient (the head's backward kernel already summed the layer below it)
     ew.colsum = m->head_db && l + 2 == L ? nullptr : m->G + m->off[2 * l + 1];
-    gemm(ctx, true, false, K, N, B, a, K, 0, g, N, 0, m->G + m->off[2 * l], N, 0, 1, ew);
     // Layers >= 1 have all their gradients after dW of layer 1; with a second
     // arena nothing of this step writes the P that layer 1's dZ reads.
     const bool early = l == 1 && m->P_next && m->side && split > 0;
+    // The fork and mid events complete with the product's kernel rather than
+    // as markers of their own between two launches.
+    if (early && m->bind_events) ew.done = m->fork;
+    gemm(ctx, true, false, K, N, B, a, K, 0, g, N, 0, m->G + m->off[2 * l], N, 0, 1, ew);
     if (early) {
-      ORCA_HIP_CHECK(hipEventRecord(m->fork, ctx->stream));
+      if (!ew.done) ORCA_HIP_CHECK(hipEventRecord(m->fork, ctx->stream));
       ORCA_HIP_CHECK(hipStreamWaitEvent(m->side, m->fork, 0));
       update(split, split + m->side_a, m->side, m->side_bpc);
       forked = true;
@@ -213,12 +218,13 @@ void step_body(orca_hip_mlp* m, const AdamWScalars* kdev) {
       ex.mask = m->H[l - 1];
       ex.ldmask = K;
       float* dz = m->dz[ping];
+      if (early && m->bind_events) ex.done = m->mid;
       gemm(ctx, false, true, B, K, N, g, N, 0, m->P + m->off[2 * l], N, 0, dz, K, 0, 1, ex);
       g = dz;
       ping ^= 1;
     }
     if (early) {
-      ORCA_HIP_CHECK(hipEventRecord(m->mid, ctx->stream));
+      if (!m->bind_events) ORCA_HIP_CHECK(hipEventRecord(m->mid, ctx->stream));
       ORCA_HIP_CHECK(hipStreamWaitEvent(m->side, m->mid, 0));
       update(split + m->side_a, m->arena, m->side);
       ORCA_HIP_CHECK(hipEventRecord(m->join, m->side));
@@ -392,6 +398,7 @@ int orca_hip_mlp_create(orca_hip_ctx* ctx, const size_t* dims, size_t n_layers, 
     const char* sb = std::getenv("ORCA_HIP_SIDE_BPC");
     if (sb) m->side_bpc = std::atoi(sb);
     if (const char* u0 = std::getenv("ORCA_HIP_U0_BPC")) m->u0_bpc = std::atoi(u0);
+    if (const char* be = std::getenv("ORCA_HIP_BIND_EVENTS")) m->bind_events = be[0] != '0';
     if (m->side && opt->kind == 1 && !m->use_graph && !(da && da[0] == '0')) {
       m->P_next = m->dev(o);
       launch_fill(ctx, m->P_next, 0.0f, o);

@@ -304,6 +304,11 @@ struct GemmEpi {
   // gemm_workspace_floats); without it they come from the context cache.
   float* ws = nullptr;
   size_t ws_floats = 0;
+  // Optional event that the product records on ctx->stream once its last
+  // launch has run: bound to that launch's completion when the pipelined
+  // kernel is the last one (no separate marker between it and the next
+  // launch), else recorded after it.
+  hipEvent_t done = nullptr;
 };
 // Workspace floats gemm() needs for this product (0 when K is not split).
 size_t gemm_workspace_floats(orca_hip_ctx* ctx, bool trans_a, bool trans_b, size_t M, size_t N, size_t K,

@@ -177,15 +177,19 @@ def test_mlp784_4096_b1024_one_adamw_step(ctx, batch):
                          what=f"784-4096-4096-10 b{batch} end-to-end")
 
 
-def test_mlp784_4096_b1024_second_arena_changes_no_bit(ctx, monkeypatch):
-    """784-4096-4096-10, batch 1024, three AdamW steps: with the second parameter arena (the
-    update of layers >= 1 beside layer 1's dZ product, P and P_next swapping every step) every
-    parameter, moment-driven update and gradient equals the single-arena schedule bit for bit."""
+@pytest.mark.parametrize("switch", ["ORCA_HIP_DOUBLE_ARENA", "ORCA_HIP_BIND_EVENTS"])
+def test_mlp784_4096_b1024_schedule_changes_no_bit(ctx, monkeypatch, switch):
+    """784-4096-4096-10, batch 1024, three AdamW steps, each schedule switch on and off: every
+    parameter, moment-driven update and gradient is the same bit for bit. ORCA_HIP_DOUBLE_ARENA:
+    the second parameter arena (the update of layers >= 1 beside layer 1's dZ product, P and
+    P_next swapping every step) against the single-arena schedule. ORCA_HIP_BIND_EVENTS: the
+    events that start the update on the second stream completing with the GEMM launches
+    before them, against event records of their own."""
     w = synth.WORKLOADS[synth.MLP_LARGE]
     params, x, labels, onehot = synth.mlp_problem(w["seed"], w["dims"], w["batch"])
     out = []
-    for double in ("1", "0"):
-        monkeypatch.setenv("ORCA_HIP_DOUBLE_ARENA", double)
+    for on in ("1", "0"):
+        monkeypatch.setenv(switch, on)
         tr = make_trainer(ctx, w, params)
         tr.set_batch(x, onehot=onehot)
         losses = []
