@@ -103,7 +103,11 @@ int orca_hip_sync_count(const orca_hip_ctx* ctx, uint64_t* count);
  * optimizer update of parameters whose gradients are complete beside the backward's
  * remaining products.  orca_hip_use_side_stream(ctx, b) with b != 0 sends the context's
  * later launches to the side stream, (ctx, 0) back to the context stream.  Host reads and
- * orca_hip_sync first make the context stream wait for the side stream's work.
+ * orca_hip_sync first make the context stream wait for the side stream's work.  While
+ * launches go to the side stream, every entry point that allocates device memory (its
+ * result, or a workspace) fails with ORCA_HIP_ERR_INTERNAL: the caching allocator orders
+ * the reuse of a block by the context stream alone, so only non-allocating launches (the
+ * orca_hip_adamw_multi / orca_hip_sgd_multi passes, event records and waits) may run there.
  * orca_hip_event_record marks the current stream's work so far; orca_hip_event_wait
  * makes the current stream wait for such a mark (no host wait); orca_hip_event_release
  * hands the event back for reuse (waits already enqueued are unaffected).  An optimizer pass

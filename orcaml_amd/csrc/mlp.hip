@@ -95,7 +95,7 @@ struct orca_hip_mlp {
   hipGraphExec_t exec = nullptr;
 
   float* dev(size_t n) {
-    void* p = ctx->alloc.allocate(n * sizeof(float) + 256, ctx->stream);
+    void* p = orca_hip::ctx_allocate(ctx, n * sizeof(float) + 256);
     owned.push_back(p);
     return static_cast<float*>(p);
   }

@@ -881,6 +881,7 @@ int orca_hip_has_nan_or_inf(orca_hip_ctx* ctx, const void* s, size_t n, int dtyp
     bind(ctx);
     check_f32(dtype, "has_nan_or_inf");
     if (!result) fail(ORCA_HIP_ERR_INTERNAL, "null output pointer");
+    join_side(ctx);  // the scan below reads what the side stream may have written
     Scratch flag(ctx, sizeof(int));
     hipLaunchKernelGGL(zero_int_kernel, dim3(1), dim3(1), 0, ctx->stream, flag.as<int>());
     if (n) {

@@ -201,7 +201,7 @@ int orca_hip_alloc(orca_hip_ctx* ctx, size_t bytes, void** out) {
   return guard([&] {
     bind(ctx);
     if (!out) fail(ORCA_HIP_ERR_INTERNAL, "null output pointer");
-    *out = ctx->alloc.allocate(bytes, ctx->stream);
+    *out = ctx_allocate(ctx, bytes);
   });
 }
 

@@ -219,10 +219,17 @@ class ProfScope {
   bool on_;
 };
 
+// A block from the context's caching allocator for work on the context stream.
+// The allocator orders the reuse of a released block by the context stream alone,
+// so this fails (InternalError) while launches go to the side stream
+// (orca_hip_use_side_stream): a block released after side-stream work could be
+// handed to context-stream work that the side stream has not finished with.
+void* ctx_allocate(orca_hip_ctx* ctx, size_t bytes);
+
 // RAII device buffer from the context allocator (freed stream-ordered).
 class Scratch {
  public:
-  Scratch(orca_hip_ctx* ctx, size_t bytes) : ctx_(ctx), p_(bytes ? ctx->alloc.allocate(bytes, ctx->stream) : nullptr) {}
+  Scratch(orca_hip_ctx* ctx, size_t bytes) : ctx_(ctx), p_(bytes ? ctx_allocate(ctx, bytes) : nullptr) {}
   ~Scratch() {
     if (p_) ctx_->alloc.release(p_);
   }

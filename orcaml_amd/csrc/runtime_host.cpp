@@ -332,8 +332,16 @@ void outputs_abort() {
   g_outputs.made.clear();
 }
 
+void* ctx_allocate(orca_hip_ctx* ctx, size_t bytes) {
+  if (ctx->main)
+    fail(ORCA_HIP_ERR_INTERNAL,
+         "Internal error: a device allocation was requested while launches go to the side stream "
+         "(only non-allocating launches may run there)");
+  return ctx->alloc.allocate(bytes, ctx->stream);
+}
+
 float* new_output(orca_hip_ctx* ctx, size_t n) {
-  void* p = ctx->alloc.allocate(n * sizeof(float), ctx->stream);
+  void* p = ctx_allocate(ctx, n * sizeof(float));
   g_outputs.made.emplace_back(ctx, p);
   return static_cast<float*>(p);
 }

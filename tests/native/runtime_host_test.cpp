@@ -153,6 +153,14 @@ static void side_stream_join(orca_hip_ctx& ctx) {
   ctx.main = side;  // launches on the side stream (the stand-in handle): no join
   join_side(&ctx);
   CHECK(hip_stub::stream_waits() == waits + 1 && !ctx.side_joined);
+  // and no allocation: the allocator orders block reuse by the context stream alone
+  const size_t live_before = live_bytes(ctx);
+  int rc = guard([&] { new_output(&ctx, 16); });
+  CHECK(rc == ORCA_HIP_ERR_INTERNAL && std::strstr(last_error_cstr(), "side stream") && live_bytes(ctx) == live_before);
+  rc = guard([&] { Scratch s(&ctx, 64); });
+  CHECK(rc == ORCA_HIP_ERR_INTERNAL && live_bytes(ctx) == live_before);
+  rc = guard([&] { ctx_allocate(&ctx, 64); });
+  CHECK(rc == ORCA_HIP_ERR_INTERNAL);
   ctx.main = nullptr;
   join_side(&ctx);
   CHECK(hip_stub::stream_waits() == waits + 2 && ctx.side_joined);

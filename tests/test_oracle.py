@@ -93,6 +93,34 @@ def test_adamw_first_step_closed_form():
     np.testing.assert_allclose(v1, 0.001 * g64 * g64, rtol=1e-5)
 
 
+def test_adamw_constant_gradient_closed_form_over_ten_steps():
+    """With a fixed gradient g and m = v = 0 at the start, m_t = (1 - b1^t) g and
+    v_t = (1 - b2^t) g^2 exactly, so the bias-corrected m_hat = g and v_hat = g^2 at every t
+    (python/orca/optim/adamw.py:82-94) and each step is p <- p * f32(1 - lr*wd) - lr * g / (|g| + eps).
+    t = 1 alone cannot tell the correction 1 - b^t from 1 - b*t or 1 - b^(t-1); steps 2..10 can."""
+    rng = np.random.default_rng(4)
+    n = 2048
+    p0 = rng.standard_normal(n).astype(np.float32)
+    g = rng.standard_normal(n).astype(np.float32)
+    g[:64] *= np.float32(1e-8)  # |g| comparable to eps: the eps term matters here
+    lr, wd, eps, b1, b2 = 1e-3, 0.01, 1e-8, 0.9, 0.999
+    decay = float(np.float32(1.0 - lr * wd))  # the f32 factor PyO3 hands the multiply
+    g64 = g.astype(np.float64)
+    p, m, v = p0, np.zeros(n, np.float32), np.zeros(n, np.float32)
+    want = p0.astype(np.float64)
+    for t in range(1, 11):
+        p, m, v = O.adamw_update(p, g, m, v, t, lr=lr, weight_decay=wd, betas=(b1, b2), eps=eps)
+        want = want * decay - lr * g64 / (np.abs(g64) + eps)
+        np.testing.assert_allclose(m, (1.0 - b1 ** t) * g64, rtol=4e-6 * t, atol=0)
+        np.testing.assert_allclose(v, (1.0 - b2 ** t) * g64 * g64, rtol=4e-6 * t, atol=0)
+        np.testing.assert_allclose(p, want, rtol=2e-7 * t, atol=lr * 1e-6 * t)  # update rounding: ulps of lr
+        if t >= 2:
+            # what the two wrong corrections would make of m_hat: far outside the tolerance above
+            for wrong in (1.0 - b1 * t, 1.0 - b1 ** (t - 1)):
+                m_hat_wrong = (1.0 - b1 ** t) / wrong if wrong else np.inf
+                assert abs(m_hat_wrong - 1.0) > 0.05
+
+
 def test_sgd_closed_form():
     rng = np.random.default_rng(3)
     p = rng.standard_normal(999).astype(np.float32)
