@@ -69,6 +69,25 @@ int orca_hip_ctx_create(int device, orca_hip_ctx** out);
 int orca_hip_ctx_destroy(orca_hip_ctx* ctx);
 /* Message of the calling thread's last failure ("" if none). */
 const char* orca_hip_last_error(void);
+/* The calling thread's last failure as the fields of its orca_core::OrcaError variant
+ * (orca-core/src/error.rs:5-31), so a binding can rebuild the variant itself:
+ * ShapeMismatch {op, expected, got}; UnsupportedDType {op, dtype}; DTypeMismatch {op,
+ * expected = dtype, got = dtype_got}; DeviceMismatch(device 0, device 1) with each device as
+ * kind (0 Cpu, 1 Cuda, 2 Gpu; orca-core/src/device.rs:5-12) and index; InternalError(message).
+ * Fields a failure does not know are "" or -1.  The strings stay valid until the thread's
+ * next failing call. */
+typedef struct {
+  int code;              /* ORCA_HIP_OK or ORCA_HIP_ERR_* */
+  const char* op;
+  const char* expected;
+  const char* got;
+  int dtype;             /* ORCA_HIP_F32 ... */
+  int dtype_got;
+  int device_kind[2];
+  int device_index[2];
+  const char* message;   /* the whole message, as orca_hip_last_error */
+} orca_hip_error_info;
+int orca_hip_last_error_info(orca_hip_error_info* out);
 /* Backend::device (orca-tensor/src/backend.rs:25): the HIP ordinal, reported
  * as Device::Gpu(ordinal) so orca-python routes "gpu"/"cuda" here
  * (orca-python/src/lib.rs:91-93). */
@@ -212,6 +231,218 @@ int orca_hip_max_to_shape_backward(orca_hip_ctx* ctx, const void* grad_out, cons
                                    const size_t* out_shape, size_t out_rank, int dtype, void** out);
 /* Backend::has_nan_or_inf (backend.rs:298); synchronises */
 int orca_hip_has_nan_or_inf(orca_hip_ctx* ctx, const void* s, size_t n, int dtype, int* result);
+
+/* ==================== storage handles: the Backend trait ==================== */
+/* The drop-in form of the trait (orca-tensor/src/backend.rs:7-315): a backend object
+ * owns the planning state a Rust `HipBackend` would otherwise have to keep above the
+ * ABI, and every trait method is one call that takes and returns storage handles.
+ *
+ * A storage handle stands for `HipBackend::Storage`: reference counted (Storage::clone is
+ * orca_hip_storage_retain, Drop is orca_hip_storage_release), immutable, and possibly not
+ * yet computed.  Behind a handle the backend keeps, invisible to the tape
+ * (orca-autograd/src/backend.rs records each op as usual):
+ *   - lazy last-two-dims transposes: a view the next matmul reads with the transpose folded
+ *     into its loads (MatMulBackward, orca-autograd/src/backend.rs:1467-1495);
+ *   - elementwise ops (add ... div_backward_rhs, accumulate_grad, broadcasts, identity
+ *     sum_to_shape / max_to_shape) left pending and run as one fused program at their first
+ *     use (orca_hip_ew_program), writing every pending value that something else holds;
+ *   - products left pending; when their first use is a GEMM epilogue (Linear's bias + ReLU,
+ *     ReluBackward's mask) they run with it (orca_hip_gemm);
+ *   - the bias gradient sum_to_shape([R, N] -> [1, N]) left pending until the weight
+ *     gradient matmul of the same storage computes it (orca_hip_matmul_colsum), and each
+ *     storage's identity sum_to_shape computed once;
+ *   - one-element uploads (the backward seed, scalars) kept on the host and applied as
+ *     instruction scalars;
+ *   - with the fused optimizer passes, the events that let part of an update run on the
+ *     context's second stream.
+ * Every value has the bits the ops run one by one would give.  Whether a pending value is
+ * written out is decided by its reference count: a binding must release a handle as soon
+ * as it drops it (as Rust's Drop and CPython's reference counting do).
+ *
+ * A backend and its storages are used under the backend's own lock, from any thread.  The
+ * context must outlive the backend and every storage of it. */
+typedef struct orca_hip_backend orca_hip_backend;
+typedef struct orca_hip_storage orca_hip_storage;
+
+typedef struct {
+  int lazy;         /* elementwise ops and products pending (fused at first use); 0: every op runs at once */
+  int deferred;     /* the identity memo and the pending bias column sums */
+  int fold;         /* pending products run with their epilogue chain (needs lazy) */
+  int overlap;      /* fused optimizer passes may run part of the update on the second stream */
+  double side_frac; /* share of that part run beside the product after its gradients (0..1) */
+  int side_bpc;     /* blocks per CU of that share (<= 0: the full grid) */
+} orca_hip_backend_options;
+
+/* Defaults: every switch on, side_frac 0.7, side_bpc 3 (the environment variables
+ * ORCA_HIP_OVERLAP=0, ORCA_HIP_OPT_SIDE_FRAC=<percent>, ORCA_HIP_OPT_SIDE_BPC=<n> override them). */
+int orca_hip_backend_default_options(orca_hip_backend_options* out);
+/* Creates a backend on ctx (opts NULL: the defaults).  Replaces GpuBackend::new
+ * (orca-backend-gpu/src/backend.rs:53-211) behind global_backend_gpu() (orca-python/src/lib.rs:23-33). */
+int orca_hip_backend_create(orca_hip_ctx* ctx, const orca_hip_backend_options* opts, orca_hip_backend** out);
+/* Drops the caller's reference; the backend goes when its last storage does. */
+int orca_hip_backend_destroy(orca_hip_backend* be);
+
+/* Storage::clone / Drop / len (orca-tensor/src/backend.rs:7-15). */
+int orca_hip_storage_retain(orca_hip_storage* s);
+int orca_hip_storage_release(orca_hip_storage* s);
+int orca_hip_storage_len(const orca_hip_storage* s, size_t* n);
+/* State flags of a storage (no counterpart in the reference; for tests and tools). */
+#define ORCA_HIP_STORAGE_PENDING 1u     /* not computed yet */
+#define ORCA_HIP_STORAGE_TRANSPOSED 2u  /* a lazy transpose view */
+#define ORCA_HIP_STORAGE_MARKED 4u      /* written on the second stream; its first use waits there */
+#define ORCA_HIP_STORAGE_CONSTANT 8u    /* a one-element value known on the host */
+int orca_hip_storage_flags(const orca_hip_storage* s, uint32_t* flags);
+/* The device address of a storage's values, computing them first (a transpose view gives
+ * its untransposed buffer).  No counterpart in the reference: for interop and tests. */
+int orca_hip_storage_device_ptr(orca_hip_backend* be, orca_hip_storage* s, void** ptr);
+
+/* The Backend trait's 42 methods (orca-tensor/src/backend.rs:19-315), in its order.  Shapes
+ * and dtypes as the trait passes them; `out` receives a new handle.  Off-path methods (conv2d*,
+ * scatter / gather*, cast to another dtype) return ORCA_HIP_ERR_UNSUPPORTED_DTYPE. */
+int orca_hip_trait_device(orca_hip_backend* be, int* kind, int* index);  /* Device::Gpu(ordinal) */
+int orca_hip_trait_zeros(orca_hip_backend* be, const size_t* shape, size_t rank, int dtype, orca_hip_storage** out);
+int orca_hip_trait_from_f32_slice(orca_hip_backend* be, const size_t* shape, size_t rank, const float* data, size_t n,
+                                  orca_hip_storage** out);
+int orca_hip_trait_to_f32_vec(orca_hip_backend* be, orca_hip_storage* s, float* host, size_t n);
+int orca_hip_trait_matmul(orca_hip_backend* be, orca_hip_storage* lhs, orca_hip_storage* rhs, const size_t* lhs_shape,
+                          size_t lhs_rank, const size_t* rhs_shape, size_t rhs_rank, int dtype, orca_hip_storage** out);
+int orca_hip_trait_transpose(orca_hip_backend* be, orca_hip_storage* s, const size_t* shape, size_t rank, size_t dim0,
+                             size_t dim1, int dtype, orca_hip_storage** out);
+int orca_hip_trait_add(orca_hip_backend* be, orca_hip_storage* lhs, orca_hip_storage* rhs, const size_t* shape,
+                       size_t rank, int dtype, orca_hip_storage** out);
+int orca_hip_trait_sub(orca_hip_backend* be, orca_hip_storage* lhs, orca_hip_storage* rhs, const size_t* shape,
+                       size_t rank, int dtype, orca_hip_storage** out);
+int orca_hip_trait_mul_scalar(orca_hip_backend* be, orca_hip_storage* s, float scalar, const size_t* shape, size_t rank,
+                              int dtype, orca_hip_storage** out);
+int orca_hip_trait_mul(orca_hip_backend* be, orca_hip_storage* lhs, orca_hip_storage* rhs, const size_t* shape,
+                       size_t rank, int dtype, orca_hip_storage** out);
+int orca_hip_trait_relu(orca_hip_backend* be, orca_hip_storage* s, const size_t* shape, size_t rank, int dtype,
+                        orca_hip_storage** out);
+int orca_hip_trait_sigmoid(orca_hip_backend* be, orca_hip_storage* s, const size_t* shape, size_t rank, int dtype,
+                           orca_hip_storage** out);
+/* relu_backward(grad, input), sigmoid_backward(grad, output): lhs is the gradient */
+int orca_hip_trait_relu_backward(orca_hip_backend* be, orca_hip_storage* lhs, orca_hip_storage* rhs, const size_t* shape,
+                                 size_t rank, int dtype, orca_hip_storage** out);
+int orca_hip_trait_sigmoid_backward(orca_hip_backend* be, orca_hip_storage* lhs, orca_hip_storage* rhs, const size_t* shape,
+                                    size_t rank, int dtype, orca_hip_storage** out);
+int orca_hip_trait_expand(orca_hip_backend* be, orca_hip_storage* s, const size_t* in_shape, size_t in_rank,
+                          const size_t* out_shape, size_t out_rank, int dtype, orca_hip_storage** out);
+int orca_hip_trait_sum_to_shape(orca_hip_backend* be, orca_hip_storage* s, const size_t* in_shape, size_t in_rank,
+                                const size_t* out_shape, size_t out_rank, int dtype, orca_hip_storage** out);
+int orca_hip_trait_reshape(orca_hip_backend* be, orca_hip_storage* s, const size_t* in_shape, size_t in_rank,
+                           const size_t* out_shape, size_t out_rank, int dtype, orca_hip_storage** out);
+int orca_hip_trait_exp(orca_hip_backend* be, orca_hip_storage* s, const size_t* shape, size_t rank, int dtype,
+                       orca_hip_storage** out);
+int orca_hip_trait_log(orca_hip_backend* be, orca_hip_storage* s, const size_t* shape, size_t rank, int dtype,
+                       orca_hip_storage** out);
+/* (grad, output) */
+int orca_hip_trait_exp_backward(orca_hip_backend* be, orca_hip_storage* lhs, orca_hip_storage* rhs, const size_t* shape,
+                                size_t rank, int dtype, orca_hip_storage** out);
+/* (grad, input) */
+int orca_hip_trait_log_backward(orca_hip_backend* be, orca_hip_storage* lhs, orca_hip_storage* rhs, const size_t* shape,
+                                size_t rank, int dtype, orca_hip_storage** out);
+int orca_hip_trait_div(orca_hip_backend* be, orca_hip_storage* lhs, orca_hip_storage* rhs, const size_t* shape,
+                       size_t rank, int dtype, orca_hip_storage** out);
+int orca_hip_trait_sqrt(orca_hip_backend* be, orca_hip_storage* s, const size_t* shape, size_t rank, int dtype,
+                        orca_hip_storage** out);
+/* (grad, rhs primal) */
+int orca_hip_trait_div_backward_lhs(orca_hip_backend* be, orca_hip_storage* lhs, orca_hip_storage* rhs, const size_t* shape,
+                                    size_t rank, int dtype, orca_hip_storage** out);
+int orca_hip_trait_div_backward_rhs(orca_hip_backend* be, orca_hip_storage* grad, orca_hip_storage* lhs,
+                                    orca_hip_storage* rhs, const size_t* shape, size_t rank, int dtype,
+                                    orca_hip_storage** out);
+/* (grad, output) */
+int orca_hip_trait_sqrt_backward(orca_hip_backend* be, orca_hip_storage* lhs, orca_hip_storage* rhs, const size_t* shape,
+                                 size_t rank, int dtype, orca_hip_storage** out);
+int orca_hip_trait_accumulate_grad(orca_hip_backend* be, orca_hip_storage* lhs, orca_hip_storage* rhs,
+                                   orca_hip_storage** out);
+/* conv2d and its backward (backend.rs:189-236): bias may be NULL (Option::None) */
+int orca_hip_trait_conv2d(orca_hip_backend* be, orca_hip_storage* input, orca_hip_storage* weight,
+                          orca_hip_storage* bias, const size_t* in_shape, size_t in_rank, const size_t* weight_shape,
+                          size_t weight_rank, size_t padding, size_t stride, size_t dilation, size_t groups, int dtype,
+                          orca_hip_storage** out);
+int orca_hip_trait_conv2d_backward_input(orca_hip_backend* be, orca_hip_storage* grad_out, orca_hip_storage* weight,
+                                         const size_t* in_shape, size_t in_rank, const size_t* weight_shape,
+                                         size_t weight_rank, size_t padding, size_t stride, size_t dilation,
+                                         size_t groups, int dtype, orca_hip_storage** out);
+int orca_hip_trait_conv2d_backward_weight(orca_hip_backend* be, orca_hip_storage* grad_out, orca_hip_storage* input,
+                                          const size_t* in_shape, size_t in_rank, const size_t* weight_shape,
+                                          size_t weight_rank, size_t padding, size_t stride, size_t dilation,
+                                          size_t groups, int dtype, orca_hip_storage** out);
+int orca_hip_trait_conv2d_backward_bias(orca_hip_backend* be, orca_hip_storage* grad_out, const size_t* out_shape,
+                                        size_t out_rank, int dtype, orca_hip_storage** out);
+/* cast (backend.rs:239-245): f32 -> f32 returns the storage, anything else is unsupported */
+int orca_hip_trait_cast(orca_hip_backend* be, orca_hip_storage* s, const size_t* shape, size_t rank, int current_dtype,
+                        int target_dtype, orca_hip_storage** out);
+/* scatter / gather and their backward (backend.rs:248-293) */
+int orca_hip_trait_scatter(orca_hip_backend* be, orca_hip_storage* s, size_t dim, orca_hip_storage* index,
+                           orca_hip_storage* src, const size_t* shape, size_t rank, const size_t* index_shape,
+                           size_t index_rank, int dtype, orca_hip_storage** out);
+int orca_hip_trait_gather(orca_hip_backend* be, orca_hip_storage* s, size_t dim, orca_hip_storage* index,
+                          const size_t* shape, size_t rank, const size_t* index_shape, size_t index_rank, int dtype,
+                          orca_hip_storage** out);
+int orca_hip_trait_scatter_backward_src(orca_hip_backend* be, orca_hip_storage* grad_out, size_t dim,
+                                        orca_hip_storage* index, const size_t* shape, size_t rank,
+                                        const size_t* index_shape, size_t index_rank, int dtype,
+                                        orca_hip_storage** out);
+int orca_hip_trait_scatter_backward_base(orca_hip_backend* be, orca_hip_storage* grad_out, size_t dim,
+                                         orca_hip_storage* index, const size_t* shape, size_t rank,
+                                         const size_t* index_shape, size_t index_rank, int dtype,
+                                         orca_hip_storage** out);
+int orca_hip_trait_gather_backward(orca_hip_backend* be, orca_hip_storage* grad_out, size_t dim,
+                                   orca_hip_storage* index, const size_t* shape, size_t rank,
+                                   const size_t* index_shape, size_t index_rank, int dtype, orca_hip_storage** out);
+int orca_hip_trait_from_bytes(orca_hip_backend* be, const size_t* shape, size_t rank, const uint8_t* bytes,
+                              size_t n_bytes, int dtype, orca_hip_storage** out);
+/* to_bytes: the storage's len() * 4 bytes */
+int orca_hip_trait_to_bytes(orca_hip_backend* be, orca_hip_storage* s, uint8_t* host, size_t n_bytes);
+int orca_hip_trait_has_nan_or_inf(orca_hip_backend* be, orca_hip_storage* s, int dtype, int* result);
+int orca_hip_trait_max_to_shape(orca_hip_backend* be, orca_hip_storage* s, const size_t* in_shape, size_t in_rank,
+                                const size_t* out_shape, size_t out_rank, int dtype, orca_hip_storage** out);
+int orca_hip_trait_max_to_shape_backward(orca_hip_backend* be, orca_hip_storage* grad, orca_hip_storage* in_primal,
+                                         orca_hip_storage* out_primal, const size_t* in_shape, size_t in_rank,
+                                         const size_t* out_shape, size_t out_rank, int dtype, orca_hip_storage** out);
+
+/* Inherent HipBackend methods beside the trait (no counterpart in the reference's trait, which
+ * has no loss or optimizer op): the opt-in fused paths (nn.CrossEntropyLoss(fused=True),
+ * optim.SGD / AdamW(fused=True)) call them when the backend has them. */
+/* Mean softmax cross-entropy of [B, C] logits against one-hot targets and, if want_grad,
+ * dL/dlogits for a loss seed of 1 (orca_hip_softmax_ce; python/orca/nn/loss.py:59-100). */
+int orca_hip_be_softmax_ce(orca_hip_backend* be, orca_hip_storage* logits, orca_hip_storage* onehot, size_t B, size_t C,
+                           int want_grad, orca_hip_storage** loss, orca_hip_storage** dlogits);
+/* A new storage holding the same values (device to device). */
+int orca_hip_be_clone(orca_hip_backend* be, orca_hip_storage* s, orca_hip_storage** out);
+/* A flat arena of n floats (set to `value` when fill != 0); view: n floats at `offset` floats of
+ * an arena (256-byte aligned when offset is a multiple of 64), sharing its memory;
+ * copy_into: dst <- src, device to device, for a slice nothing reads yet. */
+int orca_hip_be_arena(orca_hip_backend* be, size_t n, int fill, float value, orca_hip_storage** out);
+int orca_hip_be_view(orca_hip_backend* be, orca_hip_storage* arena, size_t offset, size_t n, orca_hip_storage** out);
+int orca_hip_be_copy_into(orca_hip_backend* be, orca_hip_storage* dst, orca_hip_storage* src);
+/* *exclusive = 1 when no other handle, view or pending work refers to the arena's memory
+ * (the caller's handle aside): it can be written without changing a value anybody holds. */
+int orca_hip_be_arena_exclusive(orca_hip_backend* be, orca_hip_storage* arena, int* exclusive);
+/* One optimizer pass over many parameters (orca_hip_adamw_multi / orca_hip_sgd_multi): rows of
+ * (p_src, p_dst, g, m, v, n); p_dst, m and v are written in place (m, v NULL for SGD).  Values
+ * derived lazily from the storages written are computed first.  With overlap, the rows whose
+ * gradients a weight-gradient product made before the step's last one run on the second stream
+ * right after that product; the storages they write carry its event, and their first use makes
+ * the context stream wait for it (same kernel, same bits). */
+typedef struct {
+  orca_hip_storage* p_src;
+  orca_hip_storage* p_dst;
+  orca_hip_storage* g;
+  orca_hip_storage* m;
+  orca_hip_storage* v;
+  size_t n;
+} orca_hip_opt_row;
+int orca_hip_be_adamw_multi(orca_hip_backend* be, const orca_hip_opt_row* rows, size_t n_rows, double lr, double beta1,
+                            double beta2, double eps, double weight_decay, int64_t t);
+int orca_hip_be_sgd_multi(orca_hip_backend* be, const orca_hip_opt_row* rows, size_t n_rows, double lr);
+/* In place on p (and m, v): one parameter's update (orca_hip_adamw_step / orca_hip_sgd_step). */
+int orca_hip_be_adamw_step(orca_hip_backend* be, orca_hip_storage* p, orca_hip_storage* g, orca_hip_storage* m,
+                           orca_hip_storage* v, size_t n, double lr, double beta1, double beta2, double eps,
+                           double weight_decay, int64_t t);
+int orca_hip_be_sgd_step(orca_hip_backend* be, orca_hip_storage* p, orca_hip_storage* g, size_t n, double lr);
 
 /* ================ fused elementwise programs (lazy trait ops) ================ */
 /* The elementwise trait ops (Backend::add ... div_backward_rhs, accumulate_grad,

@@ -34,15 +34,28 @@ VIEW_TRANSPOSED = 1
 
 EPI_NONE, EPI_BIAS, EPI_BIAS_RELU, EPI_RELU_MASK, EPI_BIAS_RELU_PRE, EPI_RELU_MASK_PRE = range(6)
 
+# Elementwise program opcodes and interpreter limits (include/orca_hip.h ORCA_HIP_EW_*).
+EW_ADD, EW_SUB, EW_MUL, EW_DIV, EW_MUL_SCALAR, EW_RELU, EW_RELU_BW, EW_EXP, EW_LOG, EW_SQRT = range(10)
+EW_SIGMOID, EW_EXP_BW, EW_LOG_BW, EW_SQRT_BW, EW_SIGMOID_BW, EW_DIV_BW_RHS, EW_SUM_VISIT, EW_MAX_VISIT = range(10, 18)
+EW_COPY, EW_ADD_SCALAR = 18, 19
+EW_MAX_INPUTS, EW_MAX_OUTPUTS, EW_MAX_OPS, EW_MAX_REGS = 8, 8, 64, 16
+
+
+class EwInput(ctypes.Structure):
+    """orca_hip_ew_input: element e of a program reads ptr[(e / div) % mod]."""
+    _fields_ = [("ptr", ctypes.c_void_p), ("div", ctypes.c_uint64), ("mod", ctypes.c_uint64)]
+
 
 class OrcaHipError(ValueError):
-    """A failed C-ABI call; `.code` is the ORCA_HIP_ERR_* status.  It is a
-    ValueError because orca-python maps every OrcaError to ValueError
+    """A failed C-ABI call; `.code` is the ORCA_HIP_ERR_* status and `.fields` the OrcaError
+    variant's fields (orca_hip_last_error_info: op, expected, got, dtype, dtype_got, devices).
+    It is a ValueError because orca-python maps every OrcaError to ValueError
     (orca-python/src/lib.rs:124,128)."""
 
-    def __init__(self, code: int, message: str):
+    def __init__(self, code: int, message: str, fields: dict | None = None):
         super().__init__(f"{ERROR_NAMES.get(code, code)}: {message}")
         self.code = code
+        self.fields = fields or {}
 
 
 class Epilogue(ctypes.Structure):
@@ -67,6 +80,25 @@ class Optim(ctypes.Structure):
     ]
 
 
+class BackendOptions(ctypes.Structure):
+    """orca_hip_backend_options."""
+    _fields_ = [("lazy", ctypes.c_int), ("deferred", ctypes.c_int), ("fold", ctypes.c_int), ("overlap", ctypes.c_int),
+                ("side_frac", ctypes.c_double), ("side_bpc", ctypes.c_int)]
+
+
+class OptRow(ctypes.Structure):
+    """orca_hip_opt_row: storage handles of one parameter's optimizer update."""
+    _fields_ = [("p_src", ctypes.c_void_p), ("p_dst", ctypes.c_void_p), ("g", ctypes.c_void_p),
+                ("m", ctypes.c_void_p), ("v", ctypes.c_void_p), ("n", ctypes.c_size_t)]
+
+
+class ErrorInfo(ctypes.Structure):
+    """orca_hip_error_info: the last failure as its OrcaError variant's fields."""
+    _fields_ = [("code", ctypes.c_int), ("op", ctypes.c_char_p), ("expected", ctypes.c_char_p),
+                ("got", ctypes.c_char_p), ("dtype", ctypes.c_int), ("dtype_got", ctypes.c_int),
+                ("device_kind", ctypes.c_int * 2), ("device_index", ctypes.c_int * 2), ("message", ctypes.c_char_p)]
+
+
 _P = ctypes.c_void_p
 _PP = ctypes.POINTER(ctypes.c_void_p)
 _SZ = ctypes.c_size_t
@@ -79,7 +111,73 @@ _EW1 = [_P, _P, _SZP, _SZ, _I, _PP]
 _EW2 = [_P, _P, _P, _SZP, _SZ, _I, _PP]
 _RESHAPE = [_P, _P, _SZP, _SZ, _SZP, _SZ, _I, _PP]
 
+_TB = [_P, _P, _P, _SZP, _SZ, _I, _PP]  # trait binary: backend, lhs, rhs, shape, rank, dtype, out
+_TU = [_P, _P, _SZP, _SZ, _I, _PP]  # trait unary
+_TR = [_P, _P, _SZP, _SZ, _SZP, _SZ, _I, _PP]  # trait reshape-like
+_TIDX = [_P, _P, _SZ, _P, _SZP, _SZ, _SZP, _SZ, _I, _PP]  # gather / scatter backward
+
 SIGNATURES = {
+    "orca_hip_last_error_info": [ctypes.POINTER(ErrorInfo)],
+    "orca_hip_backend_default_options": [ctypes.POINTER(BackendOptions)],
+    "orca_hip_backend_create": [_P, ctypes.POINTER(BackendOptions), _PP],
+    "orca_hip_backend_destroy": [_P],
+    "orca_hip_storage_retain": [_P],
+    "orca_hip_storage_release": [_P],
+    "orca_hip_storage_len": [_P, _SZP],
+    "orca_hip_storage_flags": [_P, ctypes.POINTER(ctypes.c_uint32)],
+    "orca_hip_storage_device_ptr": [_P, _P, _PP],
+    "orca_hip_trait_device": [_P, ctypes.POINTER(_I), ctypes.POINTER(_I)],
+    "orca_hip_trait_zeros": [_P, _SZP, _SZ, _I, _PP],
+    "orca_hip_trait_from_f32_slice": [_P, _SZP, _SZ, _P, _SZ, _PP],
+    "orca_hip_trait_to_f32_vec": [_P, _P, _P, _SZ],
+    "orca_hip_trait_matmul": [_P, _P, _P, _SZP, _SZ, _SZP, _SZ, _I, _PP],
+    "orca_hip_trait_transpose": [_P, _P, _SZP, _SZ, _SZ, _SZ, _I, _PP],
+    "orca_hip_trait_add": _TB,
+    "orca_hip_trait_sub": _TB,
+    "orca_hip_trait_mul_scalar": [_P, _P, _F, _SZP, _SZ, _I, _PP],
+    "orca_hip_trait_mul": _TB,
+    "orca_hip_trait_relu": _TU,
+    "orca_hip_trait_sigmoid": _TU,
+    "orca_hip_trait_relu_backward": _TB,
+    "orca_hip_trait_sigmoid_backward": _TB,
+    "orca_hip_trait_expand": _TR,
+    "orca_hip_trait_sum_to_shape": _TR,
+    "orca_hip_trait_reshape": _TR,
+    "orca_hip_trait_exp": _TU,
+    "orca_hip_trait_log": _TU,
+    "orca_hip_trait_exp_backward": _TB,
+    "orca_hip_trait_log_backward": _TB,
+    "orca_hip_trait_div": _TB,
+    "orca_hip_trait_sqrt": _TU,
+    "orca_hip_trait_div_backward_lhs": _TB,
+    "orca_hip_trait_div_backward_rhs": [_P, _P, _P, _P, _SZP, _SZ, _I, _PP],
+    "orca_hip_trait_sqrt_backward": _TB,
+    "orca_hip_trait_accumulate_grad": [_P, _P, _P, _PP],
+    "orca_hip_trait_conv2d": [_P, _P, _P, _P, _SZP, _SZ, _SZP, _SZ, _SZ, _SZ, _SZ, _SZ, _I, _PP],
+    "orca_hip_trait_conv2d_backward_input": [_P, _P, _P, _SZP, _SZ, _SZP, _SZ, _SZ, _SZ, _SZ, _SZ, _I, _PP],
+    "orca_hip_trait_conv2d_backward_weight": [_P, _P, _P, _SZP, _SZ, _SZP, _SZ, _SZ, _SZ, _SZ, _SZ, _I, _PP],
+    "orca_hip_trait_conv2d_backward_bias": [_P, _P, _SZP, _SZ, _I, _PP],
+    "orca_hip_trait_cast": [_P, _P, _SZP, _SZ, _I, _I, _PP],
+    "orca_hip_trait_scatter": [_P, _P, _SZ, _P, _P, _SZP, _SZ, _SZP, _SZ, _I, _PP],
+    "orca_hip_trait_gather": [_P, _P, _SZ, _P, _SZP, _SZ, _SZP, _SZ, _I, _PP],
+    "orca_hip_trait_scatter_backward_src": _TIDX,
+    "orca_hip_trait_scatter_backward_base": _TIDX,
+    "orca_hip_trait_gather_backward": _TIDX,
+    "orca_hip_trait_from_bytes": [_P, _SZP, _SZ, _P, _SZ, _I, _PP],
+    "orca_hip_trait_to_bytes": [_P, _P, _P, _SZ],
+    "orca_hip_trait_has_nan_or_inf": [_P, _P, _I, ctypes.POINTER(_I)],
+    "orca_hip_trait_max_to_shape": _TR,
+    "orca_hip_trait_max_to_shape_backward": [_P, _P, _P, _P, _SZP, _SZ, _SZP, _SZ, _I, _PP],
+    "orca_hip_be_softmax_ce": [_P, _P, _P, _SZ, _SZ, _I, _PP, _PP],
+    "orca_hip_be_clone": [_P, _P, _PP],
+    "orca_hip_be_arena": [_P, _SZ, _I, _F, _PP],
+    "orca_hip_be_view": [_P, _P, _SZ, _SZ, _PP],
+    "orca_hip_be_copy_into": [_P, _P, _P],
+    "orca_hip_be_arena_exclusive": [_P, _P, ctypes.POINTER(_I)],
+    "orca_hip_be_adamw_multi": [_P, ctypes.POINTER(OptRow), _SZ, _D, _D, _D, _D, _D, ctypes.c_int64],
+    "orca_hip_be_sgd_multi": [_P, ctypes.POINTER(OptRow), _SZ, _D],
+    "orca_hip_be_adamw_step": [_P, _P, _P, _P, _P, _SZ, _D, _D, _D, _D, _D, ctypes.c_int64],
+    "orca_hip_be_sgd_step": [_P, _P, _P, _SZ, _D],
     "orca_hip_ctx_create": [_I, ctypes.POINTER(_P)],
     "orca_hip_ctx_destroy": [_P],
     "orca_hip_device": [_P, ctypes.POINTER(_I)],
@@ -195,8 +293,15 @@ def load() -> ctypes.CDLL:
 
 def check(rc: int) -> None:
     if rc != OK:
-        msg = load().orca_hip_last_error()
-        raise OrcaHipError(rc, msg.decode() if msg else "")
+        lib = load()
+        info = ErrorInfo()
+        fields = {}
+        if lib.orca_hip_last_error_info(ctypes.byref(info)) == OK:
+            fields = dict(op=(info.op or b"").decode(), expected=(info.expected or b"").decode(),
+                          got=(info.got or b"").decode(), dtype=info.dtype, dtype_got=info.dtype_got,
+                          devices=[(info.device_kind[i], info.device_index[i]) for i in range(2)])
+        msg = lib.orca_hip_last_error()
+        raise OrcaHipError(rc, msg.decode() if msg else "", fields)
 
 
 _FNS: dict = {}

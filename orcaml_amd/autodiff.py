@@ -23,7 +23,6 @@ from __future__ import annotations
 
 import contextlib
 import math
-import sys
 from typing import Iterable
 
 import numpy as np
@@ -760,9 +759,9 @@ class _FlatParams:
         """run(segments) launches the update; segments are (i, p_src, p_dst, g) of the
         parameters with a gradient.  Parameters without one are copied across."""
         # Every view (and every storage derived from one: a lazy transpose, a pending op's
-        # operand) holds a reference to its arena, so an arena referenced only from here
-        # and by getrefcount's argument has no reader left.
-        if self.spare is not None and sys.getrefcount(self.spare) <= 2:
+        # operand) holds the arena's memory, so an arena nothing else refers to has no
+        # reader left (the backend tracks those references).
+        if self.spare is not None and self.be.arena_exclusive(self.spare):
             dst = self.spare
         else:
             dst = self.be.arena(self.total)

@@ -18,7 +18,7 @@ PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(PKG_DIR, "csrc")
 BUILD_DIR = os.path.join(PKG_DIR, "_build")
 LIB_PATH = os.path.join(PKG_DIR, "liborca_hip.so")
-SOURCES = ["runtime_host.cpp", "runtime.hip", "ops.hip", "gemm.hip", "fused.hip", "head.hip", "mlp.hip", "ewprog.hip"]
+SOURCES = ["runtime_host.cpp", "storage.cpp", "runtime.hip", "ops.hip", "gemm.hip", "fused.hip", "head.hip", "mlp.hip", "ewprog.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 

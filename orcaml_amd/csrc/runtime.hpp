@@ -21,16 +21,39 @@
 
 namespace orca_hip {
 
-// An error carrying one of the ORCA_HIP_ERR_* codes.
+// The fields of an orca_core::OrcaError variant (orca-core/src/error.rs:5-31)
+// beyond its code: ShapeMismatch {op, expected, got}, UnsupportedDType {op,
+// dtype}, DTypeMismatch {op, expected, got} (dtype codes in dtype / dtype_got),
+// DeviceMismatch (two devices as kind + index: 0 = Cpu, 1 = Cuda, 2 = Gpu).
+struct ErrorFields {
+  std::string op, expected, got;
+  int dtype = -1, dtype_got = -1;
+  int device_kind[2] = {-1, -1}, device_index[2] = {-1, -1};
+};
+
+// An error carrying one of the ORCA_HIP_ERR_* codes and, where known, its variant's fields.
 struct Error : std::runtime_error {
   int code;
+  ErrorFields fields;
   Error(int c, const std::string& m) : std::runtime_error(m), code(c) {}
+  Error(int c, const std::string& m, ErrorFields f) : std::runtime_error(m), code(c), fields(std::move(f)) {}
 };
 
 void set_last_error(const std::string& msg);
+void set_last_error(const std::string& msg, int code, const ErrorFields& fields);
 const char* last_error_cstr();  // the calling thread's last message
+void last_error_info(orca_hip_error_info* out);  // the calling thread's last error, with its fields
 
 [[noreturn]] inline void fail(int code, const std::string& msg) { throw Error(code, msg); }
+// OrcaError::ShapeMismatch, with the reference's message ("Shape mismatch during {op}: expected {e}, got {g}").
+[[noreturn]] void fail_shape(const std::string& op, const std::string& expected, const std::string& got);
+// OrcaError::UnsupportedDType ("Unsupported dtype for {op}: {dtype}").
+[[noreturn]] void fail_dtype(const std::string& op, int dtype);
+// OrcaError::DeviceMismatch of two GPUs ("Device mismatch: ... Got gpu:{a} and gpu:{b}").
+[[noreturn]] void fail_device(int gpu_a, int gpu_b);
+// The name of a dtype code in orca_core::DType's Display form ("float32", "bfloat16", ...,
+// orca-core/src/dtype.rs:146-160).
+const char* dtype_name(int dtype);
 
 #define ORCA_HIP_CHECK(expr)                                                                   \
   do {                                                                                         \
@@ -56,7 +79,7 @@ int guard(F&& f) {
     return ORCA_HIP_OK;
   } catch (const Error& e) {
     outputs_abort();
-    set_last_error(e.what());
+    set_last_error(e.what(), e.code, e.fields);
     return e.code;
   } catch (const std::exception& e) {
     outputs_abort();
@@ -261,9 +284,7 @@ inline void check_ctx(const orca_hip_ctx* ctx) {
 }
 
 inline void check_f32(int dtype, const char* op) {
-  if (dtype != ORCA_HIP_F32)
-    fail(ORCA_HIP_ERR_UNSUPPORTED_DTYPE, std::string("Unsupported dtype for ") + op + " (hip): code " +
-                                             std::to_string(dtype));
+  if (dtype != ORCA_HIP_F32) fail_dtype(op, dtype);
 }
 
 size_t numel(const size_t* shape, size_t rank);

@@ -15,8 +15,66 @@
 namespace orca_hip {
 
 static thread_local std::string g_last_error;
+static thread_local int g_last_code = ORCA_HIP_OK;
+static thread_local ErrorFields g_last_fields;
 
-void set_last_error(const std::string& msg) { g_last_error = msg; }
+void set_last_error(const std::string& msg) {
+  g_last_error = msg;
+  g_last_code = ORCA_HIP_ERR_INTERNAL;
+  g_last_fields = ErrorFields{};
+}
+
+void set_last_error(const std::string& msg, int code, const ErrorFields& fields) {
+  g_last_error = msg;
+  g_last_code = code;
+  g_last_fields = fields;
+}
+
+void last_error_info(orca_hip_error_info* out) {
+  out->code = g_last_error.empty() ? ORCA_HIP_OK : g_last_code;
+  out->op = g_last_fields.op.c_str();
+  out->expected = g_last_fields.expected.c_str();
+  out->got = g_last_fields.got.c_str();
+  out->dtype = g_last_fields.dtype;
+  out->dtype_got = g_last_fields.dtype_got;
+  for (int i = 0; i < 2; ++i) {
+    out->device_kind[i] = g_last_fields.device_kind[i];
+    out->device_index[i] = g_last_fields.device_index[i];
+  }
+  out->message = g_last_error.c_str();
+}
+
+const char* dtype_name(int dtype) {  // orca-core/src/dtype.rs Display
+  static const char* names[] = {"float32", "float64", "float16", "bfloat16", "int32", "int64", "uint8", "bool"};
+  return dtype >= 0 && dtype < 8 ? names[dtype] : "unknown";
+}
+
+void fail_shape(const std::string& op, const std::string& expected, const std::string& got) {
+  ErrorFields f;
+  f.op = op;
+  f.expected = expected;
+  f.got = got;
+  throw Error(ORCA_HIP_ERR_SHAPE, "Shape mismatch during " + op + ": expected " + expected + ", got " + got,
+              std::move(f));
+}
+
+void fail_dtype(const std::string& op, int dtype) {
+  ErrorFields f;
+  f.op = op;
+  f.dtype = dtype;
+  throw Error(ORCA_HIP_ERR_UNSUPPORTED_DTYPE, "Unsupported dtype for " + op + ": " + dtype_name(dtype), std::move(f));
+}
+
+void fail_device(int gpu_a, int gpu_b) {
+  ErrorFields f;
+  f.device_kind[0] = f.device_kind[1] = 2;  // Device::Gpu
+  f.device_index[0] = gpu_a;
+  f.device_index[1] = gpu_b;
+  throw Error(ORCA_HIP_ERR_DEVICE_MISMATCH,
+              "Device mismatch: tensors must be on the same device. Got gpu:" + std::to_string(gpu_a) + " and gpu:" +
+                  std::to_string(gpu_b),
+              std::move(f));
+}
 
 size_t numel(const size_t* shape, size_t rank) {
   size_t n = 1;

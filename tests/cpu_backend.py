@@ -3,6 +3,8 @@ the same method names as the `Backend` trait, so the tape in
 orcaml_amd.autodiff can run on it.  Storages are flat float32 numpy arrays."""
 from __future__ import annotations
 
+import sys
+
 import numpy as np
 
 from oracle import oracle as O
@@ -140,6 +142,12 @@ class OracleBackend:
 
     def copy_into(self, dst, src):
         dst[:] = src
+
+    def arena_exclusive(self, arena):
+        # every numpy view (and array derived from one) holds its base array: the caller's
+        # reference, the call's argument slot, this parameter and getrefcount's own argument
+        # are the only ones when none is alive (CPython 3.10)
+        return sys.getrefcount(arena) <= 4
 
     def adamw_multi_(self, segs, lr, beta1, beta2, eps, weight_decay, t):
         for ps, pd, g, m, v, n in segs:

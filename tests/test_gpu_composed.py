@@ -143,7 +143,7 @@ def test_fused_update_on_second_stream_changes_no_bit(ctx, wl, bias):
             opt.zero_grad()
             loss_fn(model(xt), tt).backward()
             opt.step()
-        marked = sum(p.tensor.storage.primal._ready is not None for p in model.parameters())
+        marked = sum(p.tensor.storage.primal.marked for p in model.parameters())
         assert (marked > 0) == overlap, marked
         # a snapshot of the moments first: device copies on the context stream, taken right
         # after the step, while the second stream may still be writing them
