@@ -597,8 +597,10 @@ int orca_hip_relu_bw_colsum(orca_hip_ctx* ctx, const float* grad, const float* p
  * fixed device array of 2^20 floats (4 MiB) per GPU, held until the process
  * ends, so with colsum != NULL ceil(rows / 64) * cols must not exceed 1048576
  * (larger calls fail with ORCA_HIP_ERR_INTERNAL before anything is launched).
- * Every call on a GPU shares that GPU's array: calls that overlap on one GPU
- * (other streams or contexts) race and must be ordered by the caller. */
+ * Every call on a GPU shares that GPU's array: a call's stream first waits on the
+ * device (no host wait) for the work of the previous call that used it, from any
+ * context or stream, so calls issued one after another on the host never overlap
+ * on the array.  The array and that event are set up at a GPU's first call. */
 int orca_hip_relu_bw_colsum_noalloc(orca_hip_ctx* ctx, const float* grad, const float* pre, size_t rows,
                                     size_t cols, float* dpre, float* colsum);
 

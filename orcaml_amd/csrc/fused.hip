@@ -730,20 +730,31 @@ size_t relu_bw_colsum_partial_floats(size_t rows, size_t cols, bool colsum);
 void relu_bw_colsum_launch(orca_hip_ctx* ctx, const float* grad, const float* pre, size_t rows, size_t cols,
                            float* dpre, float* colsum, float* part);
 
-// Device address of `scratch` on `device` (which the caller has made current),
-// resolved once per device and kept for the life of the process.
-float* static_scratch(int device) {
+// One GPU's copy of `scratch`: its device address (hipGetSymbolAddress) and an event that
+// marks the work of the last call that used it, on whichever stream that call ran.  Both are
+// set up once per device (which the caller has made current) and kept for the life of the
+// process; `mu` orders the calls' bookkeeping on the host.
+struct StaticScratch {
+  float* ptr = nullptr;
+  hipEvent_t last_use = nullptr;
+  bool used = false;
+  std::mutex mu;
+};
+
+StaticScratch& static_scratch(int device) {
   static std::mutex mu;
-  static std::map<int, float*> by_device;
+  static std::map<int, StaticScratch> by_device;
   std::lock_guard<std::mutex> lk(mu);
   auto it = by_device.find(device);
-  if (it != by_device.end()) return it->second;
+  if (it != by_device.end() && it->second.ptr) return it->second;
+  StaticScratch& s = by_device[device];
   float* ptr = nullptr;
   const hipError_t e = hipGetSymbolAddress((void**)&ptr, HIP_SYMBOL(scratch));
   if (e != hipSuccess || !ptr)
     fail(ORCA_HIP_ERR_INTERNAL, std::string("hipGetSymbolAddress(scratch) failed: ") + hipGetErrorString(e));
-  by_device[device] = ptr;
-  return ptr;
+  ORCA_HIP_CHECK(hipEventCreateWithFlags(&s.last_use, hipEventDisableTiming));
+  s.ptr = ptr;
+  return s;
 }
 
 }  // namespace orca_hip
@@ -789,8 +800,20 @@ int orca_hip_relu_bw_colsum_noalloc(orca_hip_ctx* ctx, const float* grad, const 
                                       " column-sum partials exceed the fixed device scratch of " +
                                       std::to_string(kStaticScratchFloats) + " floats");
     relu_bw_colsum_check(ctx, grad, pre, rows, cols, dpre, colsum);
-    // The kernels overwrite every partial they later read: nothing has to start at zero.
-    relu_bw_colsum_launch(ctx, grad, pre, rows, cols, dpre, colsum, need ? static_scratch(ctx->device) : nullptr);
+    if (!need) {  // no column sum: the scratch is not touched
+      relu_bw_colsum_launch(ctx, grad, pre, rows, cols, dpre, colsum, nullptr);
+      return;
+    }
+    // The GPU's one scratch is shared by every context and stream on it: this call's stream
+    // first waits (on the device) for the last call that used it, and this call's work is
+    // then the one the next call waits for.  The kernels overwrite every partial they later
+    // read, so nothing has to start at zero.
+    StaticScratch& s = static_scratch(ctx->device);
+    std::lock_guard<std::mutex> lk(s.mu);
+    if (s.used) ORCA_HIP_CHECK(hipStreamWaitEvent(ctx->stream, s.last_use, 0));
+    relu_bw_colsum_launch(ctx, grad, pre, rows, cols, dpre, colsum, s.ptr);
+    ORCA_HIP_CHECK(hipEventRecord(s.last_use, ctx->stream));
+    s.used = true;
   });
 }
 

@@ -61,3 +61,32 @@ def test_noalloc_rejects_sizes_beyond_its_scratch(ctx):
     assert ctx.mem_stats() == before
     want_d, _ = _run(ctx, "orca_hip_relu_bw_colsum", dg, dp, 128, 64)
     np.testing.assert_array_equal(d.download(count=128 * 64), want_d.download(count=128 * 64))
+
+
+def test_noalloc_calls_from_two_contexts_take_the_scratch_in_turn(ctx):
+    """Two contexts on one GPU (two streams) share its one scratch array: each call's stream first
+    waits on the device for the last call that used it, so calls issued back to back from both,
+    with no host wait between, each equal the allocating entry point bit for bit."""
+    from orcaml_amd.device import Context
+
+    other = Context(ctx.device)
+    try:
+        rng = np.random.default_rng(21)
+        jobs = []
+        for c, (rows, cols) in [(ctx, (8192, 4096)), (other, (4096, 2048)), (ctx, (1000, 1030)),
+                                (other, (8192, 4096)), (ctx, (64, 4096)), (other, (777, 130))]:
+            print(f"two contexts: rows={rows} cols={cols}", flush=True)
+            dg, dp = _inputs(c, rng, rows, cols)
+            want_d, want_cs = _run(c, "orca_hip_relu_bw_colsum", dg, dp, rows, cols)
+            out_d, out_cs = c.alloc(4 * rows * cols), c.alloc(4 * cols)
+            jobs.append((c, dg, dp, rows, cols, want_d, want_cs, out_d, out_cs))
+        ctx.sync()
+        other.sync()
+        for c, dg, dp, rows, cols, _, _, out_d, out_cs in jobs:  # back to back, alternating contexts
+            _lib.call("orca_hip_relu_bw_colsum_noalloc", c.handle, dg.ptr, dp.ptr, rows, cols, out_d.ptr, out_cs.ptr)
+        for c, dg, dp, rows, cols, want_d, want_cs, out_d, out_cs in jobs:
+            np.testing.assert_array_equal(out_d.download(count=rows * cols), want_d.download(count=rows * cols))
+            np.testing.assert_array_equal(out_cs.download(count=cols), want_cs.download(count=cols))
+        del jobs
+    finally:
+        other.close()
