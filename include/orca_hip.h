@@ -237,8 +237,9 @@ int orca_hip_has_nan_or_inf(orca_hip_ctx* ctx, const void* s, size_t n, int dtyp
  * owns the planning state a Rust `HipBackend` would otherwise have to keep above the
  * ABI, and every trait method is one call that takes and returns storage handles.
  *
- * A storage handle stands for `HipBackend::Storage`: reference counted (Storage::clone is
- * orca_hip_storage_retain, Drop is orca_hip_storage_release), immutable, and possibly not
+ * A storage handle stands for `HipBackend::Storage`: reference counted (a binding's clone
+ * either takes a reference of its own, orca_hip_storage_retain, or shares one among its
+ * clones; the last holder's Drop is orca_hip_storage_release), immutable, and possibly not
  * yet computed.  Behind a handle the backend keeps, invisible to the tape
  * (orca-autograd/src/backend.rs records each op as usual):
  *   - lazy last-two-dims transposes: a view the next matmul reads with the transpose folded
@@ -649,7 +650,10 @@ typedef struct {
 int orca_hip_mlp_create(orca_hip_ctx* ctx, const size_t* dims, size_t n_layers, size_t batch,
                         const orca_hip_optim* opt, orca_hip_mlp** out);
 int orca_hip_mlp_destroy(orca_hip_mlp* mlp);
-/* Parameter index i: W_{i/2} for even i ([dims[l]][dims[l+1]]), b_{i/2} ([1][dims[l+1]]) for odd i. */
+/* Parameter index i: W_{i/2} for even i ([dims[l]][dims[l+1]]), b_{i/2} ([1][dims[l+1]]) for odd i.
+ * set_param, set_moment and set_batch upload stream-ordered with no host wait (the host data may
+ * be reused on return): a checkpoint restore of every tensor never waits for the device, and the
+ * next step runs after the uploads.  The get_* calls synchronise. */
 int orca_hip_mlp_param_numel(const orca_hip_mlp* mlp, size_t index, size_t* n);
 int orca_hip_mlp_set_param(orca_hip_mlp* mlp, size_t index, const float* host, size_t n);
 int orca_hip_mlp_get_param(orca_hip_mlp* mlp, size_t index, float* host, size_t n);

@@ -430,13 +430,14 @@ int orca_hip_mlp_param_numel(const orca_hip_mlp* mlp, size_t index, size_t* n) {
   });
 }
 
+// Uploads are stream-ordered with no host wait (upload_async: a kernel argument or the
+// pinned staging ring), so a checkpoint restore of every tensor waits for the device not
+// once; the next step's kernels run after them on the context stream.
 int orca_hip_mlp_set_param(orca_hip_mlp* mlp, size_t index, const float* host, size_t n) {
   return guard([&] {
     checked(mlp);
     check_index(mlp, index, n);
-    ORCA_HIP_CHECK(hipMemcpyAsync(mlp->P + mlp->off[index], host, n * sizeof(float), hipMemcpyHostToDevice,
-                                  mlp->ctx->stream));
-    host_sync(mlp->ctx);
+    upload_async(mlp->ctx, mlp->P + mlp->off[index], host, n * sizeof(float));
   });
 }
 
@@ -472,9 +473,7 @@ int orca_hip_mlp_set_moment(orca_hip_mlp* mlp, int which, size_t index, const fl
     if (which != 0 && which != 1) fail(ORCA_HIP_ERR_INTERNAL, "moment index must be 0 (m) or 1 (v)");
     float* arena = which == 0 ? mlp->Mo : mlp->Vo;
     if (!arena) fail(ORCA_HIP_ERR_INTERNAL, "state not present for this optimizer");
-    ORCA_HIP_CHECK(hipMemcpyAsync(arena + mlp->off[index], host, n * sizeof(float), hipMemcpyHostToDevice,
-                                  mlp->ctx->stream));
-    host_sync(mlp->ctx);
+    upload_async(mlp->ctx, arena + mlp->off[index], host, n * sizeof(float));
   });
 }
 
@@ -483,16 +482,15 @@ int orca_hip_mlp_set_batch(orca_hip_mlp* mlp, const float* x, const float* oneho
     checked(mlp);
     if (!x || (onehot == nullptr) == (labels == nullptr))
       fail(ORCA_HIP_ERR_INTERNAL, "set_batch needs x and exactly one of one-hot targets or labels");
-    hipStream_t s = mlp->ctx->stream;
     const size_t B = mlp->B, C = mlp->dims[mlp->L];
-    ORCA_HIP_CHECK(hipMemcpyAsync(mlp->x, x, B * mlp->dims[0] * sizeof(float), hipMemcpyHostToDevice, s));
+    upload_async(mlp->ctx, mlp->x, x, B * mlp->dims[0] * sizeof(float));
     // The captured step bakes in which target buffer it reads.
     if ((onehot != nullptr) != (mlp->onehot != nullptr)) invalidate_graph(mlp);
     if (onehot) {
       if (!mlp->onehot) mlp->onehot = mlp->dev(B * C);
-      ORCA_HIP_CHECK(hipMemcpyAsync(mlp->onehot, onehot, B * C * sizeof(float), hipMemcpyHostToDevice, s));
+      upload_async(mlp->ctx, mlp->onehot, onehot, B * C * sizeof(float));
     } else {
-      ORCA_HIP_CHECK(hipMemcpyAsync(mlp->labels, labels, B * sizeof(int32_t), hipMemcpyHostToDevice, s));
+      upload_async(mlp->ctx, mlp->labels, labels, B * sizeof(int32_t));
       if (mlp->onehot) {  // switch to label targets
         mlp->ctx->alloc.release(mlp->onehot);
         for (auto& p : mlp->owned)
@@ -501,7 +499,6 @@ int orca_hip_mlp_set_batch(orca_hip_mlp* mlp, const float* x, const float* oneho
         mlp->onehot = nullptr;
       }
     }
-    host_sync(mlp->ctx, s);
     mlp->have_batch = true;
   });
 }

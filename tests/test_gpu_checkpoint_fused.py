@@ -114,7 +114,10 @@ def make_trainer(ctx, wl):
 def test_trainer_checkpoint_resume_matches_uninterrupted(ctx, tmp_path, workload):
     """3 steps, save, load into a fresh trainer, 2 more steps: the same
     parameters, moments, step count and metrics as 5 uninterrupted steps
-    (784-4096-4096-10 runs with two parameter arenas that swap each step)."""
+    (784-4096-4096-10 runs with two parameter arenas that swap each step).  The restore
+    and the batch upload are stream-ordered through the context's 16 MiB pinned staging ring:
+    they wait for the device only when the ring is full (at most once per 4 MiB region it
+    moves), never once per tensor, and not at all when everything fits in the ring."""
     w = synth.WORKLOADS[workload]
     params, x, labels, onehot = synth.mlp_problem(w["seed"], w["dims"], w["batch"])
     a = make_trainer(ctx, workload)
@@ -131,8 +134,15 @@ def test_trainer_checkpoint_resume_matches_uninterrupted(ctx, tmp_path, workload
     b.save(f)
     b.close()
     c = make_trainer(ctx, workload)
+    waits = ctx.sync_count()
     c.load(f)
     c.set_batch(x, labels=labels)
+    waits = ctx.sync_count() - waits
+    n_params = sum(int(np.prod(p.shape)) for p in params)
+    moved = 4 * n_params * (3 if w["opt"]["kind"] == "adamw" else 1) + x.nbytes + labels.nbytes
+    assert waits <= -(-moved // (4 << 20)), (waits, moved)
+    if moved <= 16 << 20:
+        assert waits == 0
     for _ in range(2):
         c.step()
     assert c.step_count() == a.step_count()
