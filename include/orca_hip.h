@@ -126,12 +126,13 @@ int orca_hip_sync_count(const orca_hip_ctx* ctx, uint64_t* count);
  * launches go to the side stream, every entry point that allocates device memory (its
  * result, or a workspace) fails with ORCA_HIP_ERR_INTERNAL: the caching allocator orders
  * the reuse of a block by the context stream alone, so only non-allocating launches (the
- * orca_hip_adamw_multi / orca_hip_sgd_multi passes, event records and waits) may run there.
+ * orca_hip_adamw_multi / orca_hip_sgd_multi passes, orca_hip_ew_program into buffers
+ * allocated beforehand, event records and waits) may run there.
  * orca_hip_event_record marks the current stream's work so far; orca_hip_event_wait
  * makes the current stream wait for such a mark (no host wait); orca_hip_event_release
  * hands the event back for reuse (waits already enqueued are unaffected).  An optimizer pass
- * launched on the side stream takes at most b blocks per CU when b > 0 (room for a
- * product that fills the CUs beside it) and its full grid when b < 0. */
+ * or elementwise program launched on the side stream takes at most b blocks per CU when
+ * b > 0 (room for a product that fills the CUs beside it) and its full grid when b < 0. */
 int orca_hip_use_side_stream(orca_hip_ctx* ctx, int blocks_per_cu);
 int orca_hip_event_record(orca_hip_ctx* ctx, orca_hip_event** out);
 int orca_hip_event_wait(orca_hip_ctx* ctx, orca_hip_event* ev);
@@ -171,6 +172,15 @@ int orca_hip_matmul(orca_hip_ctx* ctx, const void* lhs, const void* rhs, const s
  * the product's loads of G. */
 int orca_hip_matmul_colsum(orca_hip_ctx* ctx, const void* lhs, const void* rhs, size_t M, size_t K, size_t N,
                            int lhs_view, int dtype, void* colsum, void** out);
+/* orca_hip_matmul of rank-2 operands (colsum NULL; either view) or orca_hip_matmul_colsum
+ * (colsum non-null; rhs contiguous), and, when done != NULL, an event (*done) that completes
+ * with the product's last launch: that launch records it itself when it is the pipelined
+ * MFMA kernel, so no marker runs between the product and the next launch; otherwise it is
+ * recorded right after.  Give it back with orca_hip_event_release.  No reference
+ * counterpart (the reference's backends run on one queue): it lets work on the context's
+ * second stream wait for exactly this product. */
+int orca_hip_matmul_ev(orca_hip_ctx* ctx, const void* lhs, const void* rhs, size_t M, size_t K, size_t N,
+                       int lhs_view, int rhs_view, int dtype, void* colsum, void** out, orca_hip_event** done);
 /* Backend::transpose (backend.rs:48-55), materialised */
 int orca_hip_transpose(orca_hip_ctx* ctx, const void* s, const size_t* shape, size_t rank, size_t dim0,
                        size_t dim1, int dtype, void** out);
@@ -548,6 +558,8 @@ typedef struct {
   size_t ldmask;
   float* colsum;       /* optional [N]: column sums of op(B) over K (bias gradient of dW = X^T dY) */
   float* pre;          /* [M][ldc] for EPI_BIAS_RELU_PRE (acc + bias) and EPI_RELU_MASK_PRE (acc) */
+  orca_hip_event** done; /* optional: receives an event completing with the product's last launch,
+                            as orca_hip_matmul_ev's (no reference counterpart) */
 } orca_hip_epilogue;
 
 /* C[M,N] = op(A)[M,K] . op(B)[K,N] in f32 on the fp32 MFMA units.

@@ -66,6 +66,7 @@ class Epilogue(ctypes.Structure):
         ("ldmask", ctypes.c_size_t),
         ("colsum", ctypes.c_void_p),
         ("pre", ctypes.c_void_p),
+        ("done", ctypes.POINTER(ctypes.c_void_p)),
     ]
 
 
@@ -203,6 +204,7 @@ SIGNATURES = {
     "orca_hip_to_bytes": [_P, _P, _SZ, _P],
     "orca_hip_matmul": [_P, _P, _P, _SZP, _SZ, _SZP, _SZ, _I, _I, _I, _PP],
     "orca_hip_matmul_colsum": [_P, _P, _P, _SZ, _SZ, _SZ, _I, _I, _P, _PP],
+    "orca_hip_matmul_ev": [_P, _P, _P, _SZ, _SZ, _SZ, _I, _I, _I, _P, _PP, _PP],
     "orca_hip_transpose": [_P, _P, _SZP, _SZ, _SZ, _SZ, _I, _PP],
     "orca_hip_add": _EW2,
     "orca_hip_sub": _EW2,

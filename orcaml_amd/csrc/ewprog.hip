@@ -640,7 +640,10 @@ int orca_hip_ew_program(orca_hip_ctx* ctx, size_t n, const orca_hip_ew_input* in
     for (size_t k = 0; k < n_instrs; ++k) p.ins[k] = instrs[k];
     if (n == 0) return;
     ProfScope ps(ctx, "ew_program", 0.0, 4.0 * (double)n * (n_inputs + n_outputs));
-    const unsigned g = vec ? grid_for((n + 3) / 4, kEwBlock, ctx->num_cus * 8) : grid_for(n, kEwBlock, ctx->num_cus * 8);
+    // On the side stream a bounded grid leaves room for a product running beside it (the
+    // kernels stride over the grid, so any grid covers n).
+    const unsigned cap = ctx->main && ctx->side_bpc > 0 ? (unsigned)(ctx->side_bpc * ctx->num_cus) : ctx->num_cus * 8;
+    const unsigned g = vec ? grid_for((n + 3) / 4, kEwBlock, cap) : grid_for(n, kEwBlock, cap);
     if (hipFunction_t fn = jit_kernel(ctx, p, vec)) {
       JitArgs a{};
       for (size_t i = 0; i < n_inputs; ++i) {

@@ -1480,6 +1480,25 @@ void gemm(orca_hip_ctx* ctx, bool trans_a, bool trans_b, size_t M, size_t N, siz
   if (epi.done && !bound) ORCA_HIP_CHECK(hipEventRecord(epi.done, ctx->stream));
 }
 
+namespace {
+// gemm() of one 2-D product, handing back through `done` (when non-null) an event that
+// completes with the product's last launch (bound to it when gemm() can bind it).
+void gemm_with_event(orca_hip_ctx* ctx, bool ta, bool tb, size_t M, size_t N, size_t K, const float* A, size_t lda,
+                     const float* B, size_t ldb, float* C, size_t ldc, GemmEpi& e, orca_hip_event** done) {
+  if (done) {
+    *done = nullptr;
+    e.done = take_order_event(ctx);
+  }
+  try {
+    gemm(ctx, ta, tb, M, N, K, A, lda, 0, B, ldb, 0, C, ldc, 0, 1, e);
+  } catch (...) {
+    if (e.done) ctx->event_pool.push_back(e.done);
+    throw;
+  }
+  if (done) *done = reinterpret_cast<orca_hip_event*>(e.done);
+}
+}  // namespace
+
 }  // namespace orca_hip
 
 using namespace orca_hip;
@@ -1518,7 +1537,7 @@ int orca_hip_gemm(orca_hip_ctx* ctx, int trans_a, int trans_b, size_t M, size_t 
       if (has_mask) check_extent(ctx, e.mask, matrix_bytes(M, N, e.ldmask), "gemm (mask)");
       check_extent(ctx, e.colsum, N * sizeof(float), "gemm (colsum)");
     }
-    gemm(ctx, trans_a != 0, trans_b != 0, M, N, K, A, lda, 0, B, ldb, 0, C, ldc, 0, 1, e);
+    gemm_with_event(ctx, trans_a != 0, trans_b != 0, M, N, K, A, lda, B, ldb, C, ldc, e, epi ? epi->done : nullptr);
   });
 }
 
@@ -1547,6 +1566,46 @@ int orca_hip_matmul_colsum(orca_hip_ctx* ctx, const void* lhs, const void* rhs, 
     e.exact_colsum = true;
     gemm(ctx, ta, false, M, N, K, static_cast<const float*>(lhs), ta ? M : K, 0, static_cast<const float*>(rhs), N,
          0, o, N, 0, 1, e);
+    *out = o;
+  });
+}
+
+// orca_hip_matmul of rank-2 operands or orca_hip_matmul_colsum, with an event completing
+// with the product (for the storage layer's second-stream work).
+int orca_hip_matmul_ev(orca_hip_ctx* ctx, const void* lhs, const void* rhs, size_t M, size_t K, size_t N,
+                       int lhs_view, int rhs_view, int dtype, void* colsum, void** out, orca_hip_event** done) {
+  return guard([&] {
+    bind(ctx);
+    check_f32(dtype, "matmul");
+    if (!out) fail(ORCA_HIP_ERR_INTERNAL, "null output pointer");
+    const bool ta = lhs_view == ORCA_HIP_VIEW_TRANSPOSED, tb = rhs_view == ORCA_HIP_VIEW_TRANSPOSED;
+    if (colsum && tb) fail(ORCA_HIP_ERR_INTERNAL, "matmul_ev: a column sum needs a contiguous rhs");
+    check_extent(ctx, lhs, M * K * sizeof(float), "matmul (lhs)");
+    check_extent(ctx, rhs, K * N * sizeof(float), "matmul (rhs)");
+    check_extent(ctx, colsum, N * sizeof(float), "matmul_colsum (colsum)");
+    float* o = new_output(ctx, M * N);
+    GemmEpi e;
+    if (colsum) {
+      e.colsum = static_cast<float*>(colsum);
+      e.exact_colsum = true;
+    }
+    if (M == 0 || N == 0) {  // no product; a column sum still covers rhs
+      if (colsum && N) launch_colsum(ctx, static_cast<const float*>(rhs), K, N, N, static_cast<float*>(colsum));
+      if (done) {
+        *done = nullptr;
+        hipEvent_t ev = take_order_event(ctx);
+        const hipError_t er = hipEventRecord(ev, ctx->stream);
+        if (er != hipSuccess) {
+          ctx->event_pool.push_back(ev);
+          ORCA_HIP_CHECK(er);
+        }
+        *done = reinterpret_cast<orca_hip_event*>(ev);
+      }
+      *out = o;
+      return;
+    }
+    gemm_with_event(ctx, ta, tb, M, N, K, static_cast<const float*>(lhs), ta ? M : K, static_cast<const float*>(rhs),
+                    tb ? K : N, o, N, e, done);
     *out = o;
   });
 }

@@ -67,6 +67,23 @@ void launch_copy(orca_hip_ctx* ctx, float* dst, const float* src, size_t n) {
 
 using namespace orca_hip;
 
+// Events that order the two streams of one context: no system-scope fence at
+// record (the kernels' own release and acquire are at device scope).
+static constexpr unsigned kOrderEventFlags = hipEventDisableTiming | hipEventDisableSystemFence;
+
+namespace orca_hip {
+hipEvent_t take_order_event(orca_hip_ctx* ctx) {
+  hipEvent_t ev = nullptr;
+  if (!ctx->event_pool.empty()) {
+    ev = ctx->event_pool.back();
+    ctx->event_pool.pop_back();
+  } else {
+    ORCA_HIP_CHECK(hipEventCreateWithFlags(&ev, kOrderEventFlags));
+  }
+  return ev;
+}
+}  // namespace orca_hip
+
 // ============================================================== C ABI
 extern "C" {
 
@@ -126,10 +143,6 @@ int orca_hip_ctx_destroy(orca_hip_ctx* ctx) {
   });
 }
 
-// Events that order the two streams of one context: no system-scope fence at
-// record (the kernels' own release and acquire are at device scope).
-static constexpr unsigned kOrderEventFlags = hipEventDisableTiming | hipEventDisableSystemFence;
-
 int orca_hip_use_side_stream(orca_hip_ctx* ctx, int blocks_per_cu) {
   return guard([&] {
     bind(ctx);
@@ -156,13 +169,7 @@ int orca_hip_event_record(orca_hip_ctx* ctx, orca_hip_event** out) {
   return guard([&] {
     bind(ctx);
     if (!out) fail(ORCA_HIP_ERR_INTERNAL, "null output pointer");
-    hipEvent_t ev = nullptr;
-    if (!ctx->event_pool.empty()) {
-      ev = ctx->event_pool.back();
-      ctx->event_pool.pop_back();
-    } else {
-      ORCA_HIP_CHECK(hipEventCreateWithFlags(&ev, kOrderEventFlags));
-    }
+    hipEvent_t ev = take_order_event(ctx);
     const hipError_t e = hipEventRecord(ev, ctx->stream);
     if (e != hipSuccess) {
       (void)hipEventDestroy(ev);

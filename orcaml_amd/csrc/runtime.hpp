@@ -96,9 +96,17 @@ int guard(F&& f) {
 // stream, so a block returned here can be handed to the next request at once:
 // any later kernel using it is ordered after every earlier kernel that used
 // it.  Blocks are 256-byte aligned (hipMalloc alignment).
+//
+// Every release ticks a clock.  A block released at tick t was last used by work
+// enqueued before that release, so work on another stream that first waits for an
+// event recorded on the context stream when the clock read c >= t may use it.
 class CachingAllocator {
  public:
   void* allocate(size_t bytes, hipStream_t stream);
+  // A cached block released at or before tick `clock`, oldest first, or null (this never
+  // allocates device memory).
+  void* allocate_released_by(size_t bytes, uint64_t clock);
+  uint64_t clock();
   void release(void* p);
   void empty(hipStream_t stream);
   size_t size_of(void* p);
@@ -119,9 +127,15 @@ class CachingAllocator {
  private:
   std::mutex mu_;
   std::map<void*, size_t> live_;  // ordered: extent_from finds the block around an interior pointer
-  std::multimap<size_t, void*> cached_;
+  struct Cached {
+    void* p;
+    uint64_t released;  // the clock tick of its release
+  };
+  // per size class in release order (a multimap keeps equal keys in insertion order)
+  std::multimap<size_t, Cached> cached_;
   std::map<void*, size_t> cached_at_;  // the cached blocks by address, for locate()
   size_t live_bytes_ = 0, cached_bytes_ = 0, mallocs_ = 0;
+  uint64_t clock_ = 0;
 };
 
 // Pinned host memory through which uploads reach the device without a host
@@ -248,6 +262,15 @@ class ProfScope {
 // (orca_hip_use_side_stream): a block released after side-stream work could be
 // handed to context-stream work that the side stream has not finished with.
 void* ctx_allocate(orca_hip_ctx* ctx, size_t bytes);
+// For work that will run on the side stream after waiting for an event recorded on the
+// context stream when the allocator's clock read `clock`: a cached block released by then
+// (its last users are all before that event), or null.  Called while launches still go to
+// the context stream, like ctx_allocate.
+void* ctx_allocate_released_by(orca_hip_ctx* ctx, size_t bytes, uint64_t clock);
+uint64_t ctx_release_clock(orca_hip_ctx* ctx);
+// An unrecorded event for ordering the context's two streams (from the context's pool;
+// orca_hip_event_release gives it back).
+hipEvent_t take_order_event(orca_hip_ctx* ctx);
 
 // RAII device buffer from the context allocator (freed stream-ordered).
 class Scratch {

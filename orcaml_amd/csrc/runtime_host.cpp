@@ -110,9 +110,10 @@ void* CachingAllocator::allocate(size_t bytes, hipStream_t stream) {
   size_t r = round_size(bytes);
   {
     std::lock_guard<std::mutex> lk(mu_);
-    auto it = cached_.find(r);
-    if (it != cached_.end()) {
-      void* p = it->second;
+    auto hi = cached_.upper_bound(r);
+    if (hi != cached_.begin() && std::prev(hi)->first == r) {  // the most recently released
+      auto it = std::prev(hi);
+      void* p = it->second.p;
       cached_.erase(it);
       cached_at_.erase(p);
       cached_bytes_ -= r;
@@ -140,6 +141,25 @@ void* CachingAllocator::allocate(size_t bytes, hipStream_t stream) {
   return p;
 }
 
+void* CachingAllocator::allocate_released_by(size_t bytes, uint64_t clock) {
+  const size_t r = round_size(bytes);
+  std::lock_guard<std::mutex> lk(mu_);
+  auto it = cached_.find(r);  // the oldest release of this size
+  if (it == cached_.end() || it->second.released > clock) return nullptr;
+  void* p = it->second.p;
+  cached_.erase(it);
+  cached_at_.erase(p);
+  cached_bytes_ -= r;
+  live_[p] = r;
+  live_bytes_ += r;
+  return p;
+}
+
+uint64_t CachingAllocator::clock() {
+  std::lock_guard<std::mutex> lk(mu_);
+  return clock_;
+}
+
 void CachingAllocator::release(void* p) {
   if (!p) return;
   std::lock_guard<std::mutex> lk(mu_);
@@ -148,7 +168,7 @@ void CachingAllocator::release(void* p) {
   size_t r = it->second;
   live_.erase(it);
   live_bytes_ -= r;
-  cached_.emplace(r, p);
+  cached_.emplace(r, Cached{p, ++clock_});
   cached_at_[p] = r;
   cached_bytes_ += r;
 }
@@ -209,7 +229,7 @@ void CachingAllocator::empty(hipStream_t stream) {
     (void)hipStreamSynchronize(stream);
   }
   std::lock_guard<std::mutex> lk(mu_);
-  for (auto& kv : cached_) (void)hipFree(kv.second);
+  for (auto& kv : cached_) (void)hipFree(kv.second.p);
   cached_.clear();
   cached_at_.clear();
   cached_bytes_ = 0;
@@ -223,7 +243,7 @@ void CachingAllocator::stats(size_t* live, size_t* cached, size_t* mallocs) {
 }
 
 CachingAllocator::~CachingAllocator() {
-  for (auto& kv : cached_) (void)hipFree(kv.second);
+  for (auto& kv : cached_) (void)hipFree(kv.second.p);
   for (auto& kv : live_) (void)hipFree(kv.first);
 }
 
@@ -397,6 +417,16 @@ void* ctx_allocate(orca_hip_ctx* ctx, size_t bytes) {
          "(only non-allocating launches may run there)");
   return ctx->alloc.allocate(bytes, ctx->stream);
 }
+
+void* ctx_allocate_released_by(orca_hip_ctx* ctx, size_t bytes, uint64_t clock) {
+  if (ctx->main)
+    fail(ORCA_HIP_ERR_INTERNAL,
+         "Internal error: a device allocation was requested while launches go to the side stream "
+         "(only non-allocating launches may run there)");
+  return ctx->alloc.allocate_released_by(bytes, clock);
+}
+
+uint64_t ctx_release_clock(orca_hip_ctx* ctx) { return ctx->alloc.clock(); }
 
 float* new_output(orca_hip_ctx* ctx, size_t n) {
   void* p = ctx_allocate(ctx, n * sizeof(float));

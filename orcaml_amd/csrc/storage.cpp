@@ -106,6 +106,9 @@ struct Mark {
   Backend* be = nullptr;
   orca_hip_event* ev = nullptr;
   uint64_t seq = 0;
+  // the allocator's release clock when the mark was recorded: blocks released by then
+  // were last used by work before it
+  uint64_t clock = 0;
   std::vector<Node*> keep;
   bool settled = false;
   ~Mark();
@@ -155,6 +158,13 @@ struct Node {
   MarkP ready;
   // Made by a weight-gradient product: the mark just after that launch.
   MarkP made;
+  // The mark count when the value was computed on the context stream: the context stream's
+  // marks with a higher count come after that work.
+  uint64_t done_seq = 0;
+  // Computed on the second stream (later work there is ordered after it).
+  bool side_made = false;
+  // Written in place by an update after it was computed (never read on the second stream).
+  bool in_place = false;
   bool in_pending = false;
   uint64_t pseq = 0;  // creation order among pending nodes
 
@@ -187,6 +197,8 @@ struct Planner {
   std::deque<MarkP> recent;
   uint64_t mark_seq = 0;
   bool on_side = false;
+  // the weight or bias gradient that an elementwise op read last (an address, never followed)
+  const Node* grad_read = nullptr;
   // nodes created with a pending elementwise op or product and not yet computed, in
   // creation order
   std::map<uint64_t, Node*> pending;
@@ -304,6 +316,7 @@ Node* new_node(Backend* be, size_t n) {
 Node* value_node(Backend* be, size_t n, BufP buf) {
   Node* x = new_node(be, n);
   x->buf = std::move(buf);
+  x->done_seq = be->mark_seq;
   return x;
 }
 
@@ -348,6 +361,7 @@ void set_value(Node* x, BufP buf) {
   if (x->kind == Kind::kColsum) unwait(x);
   x->buf = std::move(buf);
   x->kind = Kind::kValue;
+  x->done_seq = be->mark_seq;
   x->ew_ops = 0;
   x->ew_leaves = 1;
   if (x->in_pending) {
@@ -366,6 +380,11 @@ void destroy_node(Node* x) {
   if (x->ident) x->ident->ident_of = nullptr;
   if (x->ident_of) x->ident_of->ident = nullptr;
   drop_operands(x);
+  if (x->ready && !x->ready->settled && x->buf && !be->on_side) {
+    // written on the second stream and never used on the context stream: that stream
+    // waits for the write before the block can go back to the allocator
+    (void)orca_hip_event_wait(be->ctx, x->ready->ev);
+  }
   x->ready.reset();
   x->made.reset();
   x->buf.reset();
@@ -382,20 +401,32 @@ Mark::~Mark() {
   if (be && be->ctx && ev) (void)orca_hip_event_release(be->ctx, ev);
 }
 
-MarkP new_mark(Backend* be) {  // on the current stream
+// A mark on the current stream: `ev` when given (an event a launch records itself), else an
+// event recorded now.
+MarkP new_mark(Backend* be, orca_hip_event* ev = nullptr) {
   auto m = std::make_shared<Mark>();
   m->be = be;
-  ck(orca_hip_event_record(be->ctx, &m->ev));
+  if (ev) {
+    m->ev = ev;
+  } else {
+    ck(orca_hip_event_record(be->ctx, &m->ev));
+  }
   m->seq = ++be->mark_seq;
+  m->clock = ctx_release_clock(be->ctx);
   return m;
 }
 
-MarkP record_mark(Backend* be) {  // a backward product's mark, kept among the recent ones
-  MarkP m = new_mark(be);
+// A backward product's mark on the context stream, kept among the recent ones.
+MarkP record_mark(Backend* be, orca_hip_event* ev = nullptr) {
+  MarkP m = new_mark(be, ev);
   be->recent.push_back(m);
   while (be->recent.size() > 8) be->recent.pop_front();
   return m;
 }
+
+// Whether backward products leave marks: with the second stream allowed, or once a fused
+// optimizer pass has asked for them.
+bool marking(Backend* be) { return be->marking || be->opt.overlap; }
 
 // The context stream waits for the mark (once); the kept storages can go.
 void settle(Backend* be, Mark& m) {
@@ -431,12 +462,9 @@ void flush_all(Backend* be) {
 }
 
 
-// The node's values on the device (computing what is pending); the buffer.
+// The node's values on the device (computing what is pending); the buffer.  A value written
+// on the second stream (before, or by computing it just now) is waited for first.
 Buf* materialize(Backend* be, Node* x) {
-  if (x->ready) {
-    MarkP m = std::move(x->ready);
-    settle(be, *m);
-  }
   switch (x->kind) {
     case Kind::kEw:
       flush(be, x);
@@ -465,6 +493,10 @@ Buf* materialize(Backend* be, Node* x) {
     case Kind::kValue:
       break;
   }
+  if (x->ready) {
+    MarkP m = std::move(x->ready);
+    settle(be, *m);
+  }
   if (!x->buf) fail(ORCA_HIP_ERR_INTERNAL, "storage has no values (a product folded into its epilogue)");
   return x->buf.get();
 }
@@ -489,13 +521,15 @@ void run_product(Backend* be, Node* x) {
   const bool lt = x->lt, rt = x->rt;
   float* a = dptr(be, lhs.get());
   float* b = dptr(be, rhs.get());
-  const size_t ls[2] = {M, K}, rs[2] = {K, N};
+  const bool mark = marking(be) && (lt || rt);  // a backward product
   void* out = nullptr;
-  ck(orca_hip_matmul(be->ctx, a, b, ls, 2, rs, 2, ORCA_HIP_F32, lt ? ORCA_HIP_VIEW_TRANSPOSED : ORCA_HIP_VIEW_CONTIGUOUS,
-                     rt ? ORCA_HIP_VIEW_TRANSPOSED : ORCA_HIP_VIEW_CONTIGUOUS, &out));
+  orca_hip_event* ev = nullptr;
+  ck(orca_hip_matmul_ev(be->ctx, a, b, M, K, N, lt ? ORCA_HIP_VIEW_TRANSPOSED : ORCA_HIP_VIEW_CONTIGUOUS,
+                        rt ? ORCA_HIP_VIEW_TRANSPOSED : ORCA_HIP_VIEW_CONTIGUOUS, ORCA_HIP_F32, nullptr, &out,
+                        mark ? &ev : nullptr));
   set_value(x, own(be->ctx, out, 4 * M * N));
-  if (be->marking && (lt || rt)) {  // a backward product
-    MarkP m = record_mark(be);
+  if (mark) {
+    MarkP m = record_mark(be, ev);
     if (lt) x->made = m;  // a weight gradient X^T G
   }
 }
@@ -683,8 +717,11 @@ bool fold_chain(Backend* be, Walk& w, const std::vector<int>& out_idx, bool shar
     pre = alloc_buf(be, M * N);
     e.pre = pre->ptr;
   }
+  const bool mark = marking(be) && (lt || rt);  // a backward product
+  orca_hip_event* ev = nullptr;
+  e.done = mark ? &ev : nullptr;
   ck(orca_hip_gemm(be->ctx, lt ? 1 : 0, rt ? 1 : 0, M, N, K, lp, lt ? M : K, rp, rt ? K : N, c->ptr, N, &e));
-  if (be->marking && (lt || rt)) record_mark(be);  // a backward product
+  if (mark) record_mark(be, ev);
   if (kind == ORCA_HIP_EPI_RELU_MASK_PRE) {
     set_value(prod, pre);  // the product itself, for its other holders
     pre.reset();
@@ -713,6 +750,74 @@ void flush_operands_first(Backend* be, Node* root) {
     }
   }
   if (root->kind == Kind::kEw) flush(be, root);
+}
+
+// Runs a chain on the context's second stream, beside the products launched after its
+// inputs, when the second stream is allowed, every input is computed and such a product
+// exists (an optimizer update whose gradient came before the backward's last products).
+// The program waits for the first context-stream mark after its inputs were computed there
+// (inputs written on the second stream are ordered there already); its outputs take cached
+// blocks released before that mark, so no context-stream work still uses them; they carry
+// the second stream's mark, which their first use on the context stream waits for, and what
+// the program reads stays referenced until then.  False when this does not apply (nothing
+// launched): the chain then runs on the context stream.
+bool side_flush(Backend* be, const Walk& w, const Program& prog, const std::vector<int>& out_idx) {
+  if (!be->opt.overlap || be->on_side || be->recent.empty() || w.leaves.empty()) return false;
+  const size_t n = w.order.back()->n;
+  if (n == 0) return false;
+  std::vector<Node*> src(w.leaves.size());  // the nodes read (a broadcast reads its source)
+  uint64_t need = 0;
+  for (size_t i = 0; i < w.leaves.size(); ++i) {
+    Node* lf = w.leaves[i];
+    Node* x = lf->kind == Kind::kBcast ? lf->lhs : lf;
+    // computed, contiguous, its own memory (not an arena slice), never updated in place
+    if (!x || x->kind != Kind::kValue || !x->buf || x->buf->owner || !x->tshape.empty() || x->in_place) return false;
+    src[i] = x;
+    if (!x->side_made) need = std::max(need, x->done_seq + 1);
+  }
+  MarkP wait;
+  for (auto& m : be->recent) {
+    if (m->seq >= need) {
+      wait = m;
+      break;
+    }
+  }
+  if (!wait || wait == be->recent.back()) return false;  // no product launched after it to run beside
+  std::vector<BufP> bufs;
+  for (size_t i = 0; i < out_idx.size(); ++i) {
+    void* p = ctx_allocate_released_by(be->ctx, 4 * n, wait->clock);
+    if (!p) return false;  // the blocks taken so far go back to the cache
+    bufs.push_back(own(be->ctx, p, 4 * n));
+  }
+  std::vector<orca_hip_ew_input> ins(w.leaves.size());
+  for (size_t i = 0; i < w.leaves.size(); ++i) {
+    Node* lf = w.leaves[i];
+    ins[i].ptr = src[i]->buf->ptr;
+    ins[i].div = lf->kind == Kind::kBcast ? lf->div : 1;
+    ins[i].mod = lf->kind == Kind::kBcast ? lf->mod : n;
+  }
+  std::vector<float*> outs;
+  for (auto& b : bufs) outs.push_back(b->ptr);
+  ck(orca_hip_use_side_stream(be->ctx, be->opt.side_bpc > 0 ? be->opt.side_bpc : -1));
+  be->on_side = true;
+  int rc = orca_hip_event_wait(be->ctx, wait->ev);
+  if (rc == ORCA_HIP_OK)
+    rc = orca_hip_ew_program(be->ctx, n, ins.data(), ins.size(), outs.data(), prog.oregs.data(), outs.size(),
+                             prog.instrs.data(), prog.instrs.size(), prog.n_regs);
+  MarkP done;
+  if (rc == ORCA_HIP_OK) rc = guard_nodes([&] { done = new_mark(be); });
+  be->on_side = false;
+  const int rc2 = orca_hip_use_side_stream(be->ctx, 0);
+  ck(rc);
+  ck(rc2);
+  for (Node* x : src) done->keep.push_back(ref(x));
+  for (size_t i = 0; i < out_idx.size(); ++i) {
+    Node* o = w.order[out_idx[i]];
+    set_value(o, bufs[i]);
+    o->side_made = true;
+    o->ready = done;
+  }
+  return true;
 }
 
 // Runs root's pending chain as one program.  Pending values in the chain referenced from
@@ -752,6 +857,7 @@ void flush(Backend* be, Node* root) {
     return;
   }
   for (int k : prog.scalar_at) prog.instrs[k].scalar = w.scalars[k];
+  if (side_flush(be, w, prog, out_idx)) return;
   const size_t n = root->n;
   std::vector<orca_hip_ew_input> ins(std::max<size_t>(1, w.leaves.size()));
   for (size_t i = 0; i < w.leaves.size(); ++i) {
@@ -780,12 +886,58 @@ void flush(Backend* be, Node* root) {
 // ---- creating pending nodes
 bool is_lazy_f32(Backend* be, int dtype) { return be->opt.lazy && dtype == ORCA_HIP_F32; }
 
+// The reference's optimizers update the parameters one after another, so the update that
+// reads one weight or bias gradient is complete once the update after it has started.  When
+// an op reads a gradient g (the previous one read being `prev`), every pending chain that
+// reads a gradient other than those two and whose inputs are all computed runs now rather
+// than at its first use: while the backward's last products may still run, so that the ones
+// on the second stream run beside them.  (Not at the first read after it: the finished
+// update's temporaries can still be held by the caller then, and would be written out.)
+void flush_finished_updates(Backend* be, const Node* g, const Node* prev) {
+  std::unordered_set<const Node*> consumed;  // operands of pending nodes
+  for (auto& kv : be->pending) {
+    const Node* p = kv.second;
+    for (int i = 0; i < p->nopd; ++i) consumed.insert(p->opd[i]);
+    if (p->lhs) consumed.insert(p->lhs);
+    if (p->rhs) consumed.insert(p->rhs);
+  }
+  std::vector<Ref> roots;
+  for (auto& kv : be->pending) {
+    Node* p = kv.second;
+    if (p->kind != Kind::kEw || consumed.count(p)) continue;
+    Walk w;
+    w.visit(p);
+    bool ready = true, other_grad = false;
+    for (Node* lf : w.leaves) {
+      Node* x = lf->kind == Kind::kBcast ? lf->lhs : lf;
+      if (!x || x->kind != Kind::kValue) {
+        ready = false;
+        break;
+      }
+      if (x->made && x != g && x != prev) other_grad = true;
+    }
+    if (ready && other_grad) roots.emplace_back(ref(p));
+  }
+  for (auto& r : roots)
+    if (r->kind == Kind::kEw) flush(be, r.get());
+}
+
 // A pending elementwise op over equally long operands (transposed views are
 // materialised first).  Operands whose pending chains would push this one past the
 // interpreter's limits are run first.
 Node* ew(Backend* be, uint8_t op, std::vector<Ref> opds, size_t n, float scalar = 0.0f) {
   for (auto& o : opds)
     if (o->kind != Kind::kBcast && !o->tshape.empty()) o = plain(be, o.get());
+  if (be->opt.overlap && be->opt.lazy && !be->on_side) {
+    for (auto& o : opds) {
+      if (o->kind != Kind::kBcast && o->made && o.get() != be->grad_read) {
+        const Node* prev = be->grad_read;
+        be->grad_read = o.get();  // compared by address only
+        flush_finished_updates(be, o.get(), prev);
+        break;
+      }
+    }
+  }
   int ops, leaves;
   for (;;) {
     ops = 1;
@@ -884,6 +1036,7 @@ void mutating(Backend* be, const Targets& targets) {
   flush_all(be);
   for (Node* s : targets) {
     if (!s) continue;
+    s->in_place = true;
     std::vector<Node*> ws = s->waiters;
     for (Node* t : ws) {
       Ref tt(ref(t));
@@ -1361,11 +1514,14 @@ int orca_hip_trait_matmul(orca_hip_backend* be, orca_hip_storage* lhs, orca_hip_
         float* rp = dptr(b, r);
         BufP cs = alloc_buf(b, N);
         void* o = nullptr;
-        ck(orca_hip_matmul_colsum(b->ctx, lp, rp, M, K, N, lv, dtype, cs->ptr, &o));
+        const bool mark = marking(b);
+        orca_hip_event* ev = nullptr;
+        ck(orca_hip_matmul_ev(b->ctx, lp, rp, M, K, N, lv, ORCA_HIP_VIEW_CONTIGUOUS, dtype, cs->ptr, &o,
+                              mark ? &ev : nullptr));
         set_value(target, cs);
         Node* res = value_node(b, M * N, own(b->ctx, o, 4 * M * N));
-        if (b->marking) {
-          MarkP m = record_mark(b);
+        if (mark) {
+          MarkP m = record_mark(b, ev);
           if (lv == ORCA_HIP_VIEW_TRANSPOSED) res->made = target->made = m;  // a weight gradient and its bias gradient
         }
         put(out, res);
@@ -1788,6 +1944,7 @@ int orca_hip_be_copy_into(orca_hip_backend* be, orca_hip_storage* dst, orca_hip_
     Node* d = arg(b, dst, "copy_into");
     Ref s = plain(b, arg(b, src, "copy_into"));
     if (s->n != d->n) fail_shape("copy_into", std::to_string(d->n) + " elements", std::to_string(s->n) + " elements");
+    d->in_place = true;
     if (s->n) ck(orca_hip_d2d(b->ctx, dptr(b, d), dptr(b, s.get()), 4 * s->n));
   });
 }

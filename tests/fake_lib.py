@@ -59,6 +59,8 @@ def load(path: str) -> ctypes.CDLL:
     lib.orca_hip_last_error.argtypes = []
     lib.orca_hip_last_error.restype = ctypes.c_char_p
     lib.fake_log_text.argtypes = [ctypes.c_char_p, ctypes.c_size_t, ctypes.POINTER(ctypes.c_size_t)]
+    lib.fake_race_count.argtypes = []
+    lib.fake_race_count.restype = ctypes.c_uint64
     return lib
 
 
@@ -79,3 +81,9 @@ def log(lib) -> list:
 
 def clear(lib) -> None:
     lib.fake_log_clear()
+
+
+def races(lib) -> int:
+    """Accesses of one stream to memory the other stream touched after the last point it
+    waited for (the stand-in's happens-before check), since the library was loaded."""
+    return int(lib.fake_race_count())

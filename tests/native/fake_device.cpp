@@ -10,6 +10,7 @@
 #include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <map>
 #include <sstream>
 #include <string>
 #include <vector>
@@ -29,10 +30,79 @@ void logf(const std::string& line) {
 
 float* F(const void* p) { return static_cast<float*>(const_cast<void*>(p)); }
 
+// ---- a happens-before check of a context's two streams.  Launches are synchronous here,
+// so an order that only the real GPU would get wrong has to be checked: every launch
+// declares the byte ranges it reads and writes, and an access on one stream to a range that
+// the other stream touched after the last of its points this stream waited for (an event,
+// or a host read's join) is logged as "RACE <launch> ...".
+struct Range {
+  uintptr_t lo, hi;
+  uint64_t main_write, main_read, side_write, side_read;  // each stream's launch count at its last access
+};
+struct Streams {
+  uint64_t main_clock = 0, side_clock = 0;            // launches so far on each stream
+  uint64_t side_knows_main = 0, main_knows_side = 0;  // the other stream's launches each has waited for
+  uint64_t side_at_switch = 0;                        // side launches when launches last went back
+  std::vector<Range> ranges;
+};
+std::map<const orca_hip_ctx*, Streams> g_streams;
+std::map<uintptr_t, std::pair<bool, uint64_t>> g_event_at;  // event -> (recorded on the side stream, clock)
+std::string g_launch = "?";
+uint64_t g_races = 0;
+
+bool on_side(const orca_hip_ctx* ctx) { return ctx->main != nullptr; }
+
+void launch(orca_hip_ctx* ctx, const std::string& what) {
+  Streams& st = g_streams[ctx];
+  if (on_side(ctx))
+    ++st.side_clock;
+  else
+    ++st.main_clock;
+  g_launch = what;
+}
+
+void touch(orca_hip_ctx* ctx, const void* p, size_t bytes, bool write) {
+  if (!p || !bytes) return;
+  Streams& st = g_streams[ctx];
+  const uintptr_t lo = reinterpret_cast<uintptr_t>(p), hi = lo + bytes;
+  const bool side = on_side(ctx);
+  size_t exact = st.ranges.size();
+  for (size_t i = 0; i < st.ranges.size(); ++i) {
+    const Range& r = st.ranges[i];
+    if (r.hi <= lo || r.lo >= hi) continue;
+    const bool race = side ? (r.main_write > st.side_knows_main || (write && r.main_read > st.side_knows_main))
+                           : (r.side_write > st.main_knows_side || (write && r.side_read > st.main_knows_side));
+    if (race) {
+      ++g_races;
+      logf("RACE " + g_launch + (write ? " writes" : " reads") + (side ? " on the side stream" : " on the context stream"));
+    }
+    if (r.lo == lo && r.hi == hi) exact = i;
+  }
+  if (exact == st.ranges.size()) st.ranges.push_back(Range{lo, hi, 0, 0, 0, 0});
+  Range& r = st.ranges[exact];
+  const uint64_t now = side ? st.side_clock : st.main_clock;
+  (side ? (write ? r.side_write : r.side_read) : (write ? r.main_write : r.main_read)) = now;
+}
+void R(orca_hip_ctx* ctx, const void* p, size_t bytes) { touch(ctx, p, bytes, false); }
+void W(orca_hip_ctx* ctx, const void* p, size_t bytes) { touch(ctx, p, bytes, true); }
+
+void event_at(orca_hip_ctx* ctx, orca_hip_event* ev) {
+  const Streams& st = g_streams[ctx];
+  g_event_at[reinterpret_cast<uintptr_t>(ev)] = {on_side(ctx), on_side(ctx) ? st.side_clock : st.main_clock};
+}
+
+// A host read or sync: the library first makes the context stream wait for the side stream.
+void join(orca_hip_ctx* ctx) {
+  Streams& st = g_streams[ctx];
+  st.main_knows_side = std::max(st.main_knows_side, st.side_at_switch);
+}
+
+
 float* out_buf(orca_hip_ctx* ctx, size_t n, void** out) {
   if (!out) fail(ORCA_HIP_ERR_INTERNAL, "null output pointer");
   float* o = new_output(ctx, n ? n : 1);
   *out = o;
+  W(ctx, o, 4 * n);
   return o;
 }
 
@@ -60,6 +130,11 @@ std::vector<float> product(const float* A, bool ta, size_t lda, const float* B, 
   return c;
 }
 
+// Rethrows a failed nested entry point's error.
+void ck_fake(int rc) {
+  if (rc != ORCA_HIP_OK) fail(rc, last_error_cstr());
+}
+
 void check_oracle(int rc, const char* op) {
   if (rc != 0) fail(ORCA_HIP_ERR_SHAPE, std::string("Shape mismatch during ") + op + " (oracle)");
 }
@@ -75,6 +150,8 @@ int fake_log_text(char* buf, size_t len, size_t* needed) {
   return ORCA_HIP_OK;
 }
 void fake_log_clear(void) { g_log.clear(); }
+// Accesses that the two streams' order did not cover, since the library was loaded.
+uint64_t fake_race_count(void) { return g_races; }
 
 // ---- context and memory
 const char* orca_hip_last_error(void) { return last_error_cstr(); }
@@ -94,6 +171,7 @@ int orca_hip_ctx_destroy(orca_hip_ctx* ctx) {
   return guard([&] {
     if (!ctx) return;
     if (ctx->main) ctx->stream = ctx->main;
+    g_streams.erase(ctx);
     delete ctx;
   });
 }
@@ -131,7 +209,10 @@ int orca_hip_mem_stats(orca_hip_ctx* ctx, size_t* live, size_t* cached, size_t* 
 }
 
 int orca_hip_sync(orca_hip_ctx* ctx) {
-  return guard([&] { host_sync(ctx); });
+  return guard([&] {
+    host_sync(ctx);
+    join(ctx);
+  });
 }
 
 int orca_hip_sync_count(const orca_hip_ctx* ctx, uint64_t* count) {
@@ -141,6 +222,9 @@ int orca_hip_sync_count(const orca_hip_ctx* ctx, uint64_t* count) {
 int orca_hip_h2d(orca_hip_ctx* ctx, void* dst, const void* src, size_t bytes) {
   return guard([&] {
     check_extent(ctx, dst, bytes, "h2d");
+    join(ctx);
+    launch(ctx, "h2d");
+    W(ctx, dst, bytes);
     std::memcpy(dst, src, bytes);
   });
 }
@@ -148,6 +232,9 @@ int orca_hip_h2d(orca_hip_ctx* ctx, void* dst, const void* src, size_t bytes) {
 int orca_hip_d2h(orca_hip_ctx* ctx, void* dst, const void* src, size_t bytes) {
   return guard([&] {
     check_extent(ctx, src, bytes, "d2h");
+    join(ctx);
+    launch(ctx, "d2h");
+    R(ctx, src, bytes);
     std::memcpy(dst, src, bytes);
   });
 }
@@ -156,6 +243,9 @@ int orca_hip_d2d(orca_hip_ctx* ctx, void* dst, const void* src, size_t bytes) {
   return guard([&] {
     check_extent(ctx, dst, bytes, "d2d");
     check_extent(ctx, src, bytes, "d2d");
+    launch(ctx, "d2d");
+    R(ctx, src, bytes);
+    W(ctx, dst, bytes);
     std::memmove(dst, src, bytes);
     logf("d2d " + std::to_string(bytes));
   });
@@ -164,6 +254,8 @@ int orca_hip_d2d(orca_hip_ctx* ctx, void* dst, const void* src, size_t bytes) {
 int orca_hip_fill(orca_hip_ctx* ctx, float* dst, float value, size_t n) {
   return guard([&] {
     check_extent(ctx, dst, 4 * n, "fill");
+    launch(ctx, "fill");
+    W(ctx, dst, 4 * n);
     for (size_t i = 0; i < n; ++i) dst[i] = value;
   });
 }
@@ -179,6 +271,7 @@ int orca_hip_use_side_stream(orca_hip_ctx* ctx, int blocks_per_cu) {
       logf("side " + std::to_string(blocks_per_cu));
     } else {
       if (!ctx->main) fail(ORCA_HIP_ERR_INTERNAL, "launches do not go to the side stream");
+      g_streams[ctx].side_at_switch = g_streams[ctx].side_clock;
       ctx->stream = ctx->main;
       ctx->main = nullptr;
       logf("main");
@@ -186,17 +279,30 @@ int orca_hip_use_side_stream(orca_hip_ctx* ctx, int blocks_per_cu) {
   });
 }
 
+orca_hip_event* next_event() {
+  static uintptr_t next = 16;
+  next += 16;
+  return reinterpret_cast<orca_hip_event*>(next);
+}
+
 int orca_hip_event_record(orca_hip_ctx* ctx, orca_hip_event** out) {
   return guard([&] {
-    static uintptr_t next = 16;
-    next += 16;
-    *out = reinterpret_cast<orca_hip_event*>(next);
-    logf("record " + std::to_string(next) + (ctx->main ? " side" : ""));
+    *out = next_event();
+    event_at(ctx, *out);
+    logf("record " + std::to_string(reinterpret_cast<uintptr_t>(*out)) + (ctx->main ? " side" : ""));
   });
 }
 
 int orca_hip_event_wait(orca_hip_ctx* ctx, orca_hip_event* ev) {
-  return guard([&] { logf("wait " + std::to_string(reinterpret_cast<uintptr_t>(ev)) + (ctx->main ? " side" : "")); });
+  return guard([&] {
+    auto it = g_event_at.find(reinterpret_cast<uintptr_t>(ev));
+    if (it != g_event_at.end()) {
+      Streams& st = g_streams[ctx];
+      if (it->second.first && !on_side(ctx)) st.main_knows_side = std::max(st.main_knows_side, it->second.second);
+      if (!it->second.first && on_side(ctx)) st.side_knows_main = std::max(st.side_knows_main, it->second.second);
+    }
+    logf("wait " + std::to_string(reinterpret_cast<uintptr_t>(ev)) + (ctx->main ? " side" : ""));
+  });
 }
 
 int orca_hip_event_release(orca_hip_ctx*, orca_hip_event*) { return ORCA_HIP_OK; }
@@ -206,6 +312,7 @@ int orca_hip_zeros(orca_hip_ctx* ctx, const size_t* shape, size_t rank, int dtyp
   return guard([&] {
     check_f32(dtype, "zeros");
     const size_t n = numel(shape, rank);
+    launch(ctx, "zeros");
     float* o = out_buf(ctx, n, out);
     for (size_t i = 0; i < n; ++i) o[i] = 0.0f;
   });
@@ -215,6 +322,7 @@ int orca_hip_from_f32_slice(orca_hip_ctx* ctx, const size_t* shape, size_t rank,
                             void** out) {
   return guard([&] {
     if (numel(shape, rank) != n) fail(ORCA_HIP_ERR_SHAPE, "Shape mismatch during from_f32_slice");
+    launch(ctx, "upload");
     float* o = out_buf(ctx, n, out);
     if (n) std::memcpy(o, data, 4 * n);
     logf("upload " + std::to_string(n));
@@ -224,6 +332,9 @@ int orca_hip_from_f32_slice(orca_hip_ctx* ctx, const size_t* shape, size_t rank,
 int orca_hip_to_f32_vec(orca_hip_ctx* ctx, const void* s, size_t n, float* host) {
   return guard([&] {
     check_extent(ctx, s, 4 * n, "to_f32_vec");
+    join(ctx);
+    launch(ctx, "to_f32_vec");
+    R(ctx, s, 4 * n);
     if (n) std::memcpy(host, s, 4 * n);
   });
 }
@@ -234,6 +345,7 @@ int orca_hip_from_bytes(orca_hip_ctx* ctx, const size_t* shape, size_t rank, con
     check_f32(dtype, "from_bytes");
     const size_t n = numel(shape, rank);
     if (n_bytes != 4 * n) fail(ORCA_HIP_ERR_SHAPE, "Shape mismatch during from_bytes");
+    launch(ctx, "from_bytes");
     float* o = out_buf(ctx, n, out);
     if (n) std::memcpy(o, bytes, n_bytes);
   });
@@ -242,13 +354,19 @@ int orca_hip_from_bytes(orca_hip_ctx* ctx, const size_t* shape, size_t rank, con
 int orca_hip_to_bytes(orca_hip_ctx* ctx, const void* s, size_t n_bytes, uint8_t* host) {
   return guard([&] {
     check_extent(ctx, s, n_bytes, "to_bytes");
+    join(ctx);
+    launch(ctx, "to_bytes");
+    R(ctx, s, n_bytes);
     if (n_bytes) std::memcpy(host, s, n_bytes);
   });
 }
 
-int orca_hip_has_nan_or_inf(orca_hip_ctx*, const void* s, size_t n, int dtype, int* result) {
+int orca_hip_has_nan_or_inf(orca_hip_ctx* ctx, const void* s, size_t n, int dtype, int* result) {
   return guard([&] {
     check_f32(dtype, "has_nan_or_inf");
+    join(ctx);
+    launch(ctx, "has_nan_or_inf");
+    R(ctx, s, 4 * n);
     *result = orc_has_nan_or_inf(F(s), n);
   });
 }
@@ -260,6 +378,9 @@ int orca_hip_matmul(orca_hip_ctx* ctx, const void* lhs, const void* rhs, const s
     if (lr != 2 || rr != 2) fail(ORCA_HIP_ERR_INTERNAL, "the stand-in multiplies 2-D operands only");
     const size_t M = ls[0], K = ls[1], N = rs[1];
     if (rs[0] != K) fail_shape("matmul", std::to_string(K), std::to_string(rs[0]));
+    launch(ctx, "matmul");
+    R(ctx, lhs, 4 * M * K);
+    R(ctx, rhs, 4 * K * N);
     std::vector<float> c = product(F(lhs), lv != 0, lv ? M : K, F(rhs), rv != 0, rv ? K : N, M, N, K);
     float* o = out_buf(ctx, M * N, out);
     std::copy(c.begin(), c.end(), o);
@@ -272,6 +393,10 @@ int orca_hip_matmul_colsum(orca_hip_ctx* ctx, const void* lhs, const void* rhs, 
                            int lhs_view, int dtype, void* colsum, void** out) {
   return guard([&] {
     check_f32(dtype, "matmul_colsum");
+    launch(ctx, "matmul_colsum");
+    R(ctx, lhs, 4 * M * K);
+    R(ctx, rhs, 4 * K * N);
+    W(ctx, colsum, 4 * N);
     std::vector<float> c = product(F(lhs), lhs_view != 0, lhs_view ? M : K, F(rhs), false, N, M, N, K);
     float* o = out_buf(ctx, M * N, out);
     std::copy(c.begin(), c.end(), o);
@@ -282,11 +407,42 @@ int orca_hip_matmul_colsum(orca_hip_ctx* ctx, const void* lhs, const void* rhs, 
   });
 }
 
-int orca_hip_gemm(orca_hip_ctx*, int ta, int tb, size_t M, size_t N, size_t K, const float* A, size_t lda,
+// Products that hand back an event completing with them: "bound N" follows the launch's
+// log line (a real launch records it itself).
+int orca_hip_matmul_ev(orca_hip_ctx* ctx, const void* lhs, const void* rhs, size_t M, size_t K, size_t N, int lv,
+                       int rv, int dtype, void* colsum, void** out, orca_hip_event** done) {
+  return guard([&] {
+    if (done) *done = nullptr;
+    if (colsum && rv) fail(ORCA_HIP_ERR_INTERNAL, "matmul_ev: a column sum needs a contiguous rhs");
+    if (colsum) {
+      ck_fake(orca_hip_matmul_colsum(ctx, lhs, rhs, M, K, N, lv, dtype, colsum, out));
+    } else {
+      const size_t ls[2] = {M, K}, rs[2] = {K, N};
+      ck_fake(orca_hip_matmul(ctx, lhs, rhs, ls, 2, rs, 2, dtype, lv, rv, out));
+    }
+    if (done) {
+      *done = next_event();
+      event_at(ctx, *done);
+      logf("bound " + std::to_string(reinterpret_cast<uintptr_t>(*done)));
+    }
+  });
+}
+
+int orca_hip_gemm(orca_hip_ctx* ctx, int ta, int tb, size_t M, size_t N, size_t K, const float* A, size_t lda,
                   const float* B, size_t ldb, float* C, size_t ldc, const orca_hip_epilogue* epi) {
   return guard([&] {
+    launch(ctx, "gemm");
+    R(ctx, A, 4 * (ta ? K * lda : M * lda));
+    R(ctx, B, 4 * (tb ? N * ldb : K * ldb));
+    W(ctx, C, 4 * M * ldc);
     std::vector<float> p = product(A, ta != 0, lda, B, tb != 0, ldb, M, N, K);
     const int kind = epi ? epi->kind : ORCA_HIP_EPI_NONE;
+    if (epi) {
+      R(ctx, epi->bias, 4 * N);
+      R(ctx, epi->mask, 4 * M * epi->ldmask);
+      W(ctx, epi->pre, 4 * M * ldc);
+      W(ctx, epi->colsum, 4 * N);
+    }
     std::vector<float> v(M * N), bias_row(M * N);
     if (kind == ORCA_HIP_EPI_BIAS || kind == ORCA_HIP_EPI_BIAS_RELU || kind == ORCA_HIP_EPI_BIAS_RELU_PRE) {
       const size_t bd[2] = {1, N}, od[2] = {M, N};
@@ -311,6 +467,11 @@ int orca_hip_gemm(orca_hip_ctx*, int ta, int tb, size_t M, size_t N, size_t K, c
     }
     logf("gemm " + std::to_string(M) + "x" + std::to_string(N) + "x" + std::to_string(K) + " " + std::to_string(ta) +
          std::to_string(tb) + " epi " + std::to_string(kind));
+    if (epi && epi->done) {
+      *epi->done = next_event();
+      event_at(ctx, *epi->done);
+      logf("bound " + std::to_string(reinterpret_cast<uintptr_t>(*epi->done)));
+    }
   });
 }
 
@@ -319,6 +480,8 @@ int orca_hip_transpose(orca_hip_ctx* ctx, const void* s, const size_t* shape, si
   return guard([&] {
     check_f32(dtype, "transpose");
     const size_t n = numel(shape, rank);
+    launch(ctx, "transpose");
+    R(ctx, s, 4 * n);
     float* o = out_buf(ctx, n, out);
     check_oracle(orc_transpose(F(s), o, shape, rank, d0, d1), "transpose");
     logf("transpose " + std::to_string(n));
@@ -330,6 +493,8 @@ int orca_hip_transpose(orca_hip_ctx* ctx, const void* s, const size_t* shape, si
     return guard([&] {                                                                                         \
       check_f32(dtype, #NAME);                                                                                 \
       const size_t n = numel(shape, rank);                                                                     \
+      launch(ctx, #NAME);                                                                                      \
+      R(ctx, s, 4 * n);                                                                                        \
       FN(F(s), out_buf(ctx, n, out), n);                                                                       \
       logf(std::string("op ") + #NAME);                                                                        \
     });                                                                                                        \
@@ -340,6 +505,9 @@ int orca_hip_transpose(orca_hip_ctx* ctx, const void* s, const size_t* shape, si
     return guard([&] {                                                                                       \
       check_f32(dtype, #NAME);                                                                               \
       const size_t n = numel(shape, rank);                                                                   \
+      launch(ctx, #NAME);                                                                                    \
+      R(ctx, a, 4 * n);                                                                                      \
+      R(ctx, b, 4 * n);                                                                                      \
       FN(F(a), F(b), out_buf(ctx, n, out), n);                                                               \
       logf(std::string("op ") + #NAME);                                                                      \
     });                                                                                                      \
@@ -365,6 +533,8 @@ int orca_hip_mul_scalar(orca_hip_ctx* ctx, const void* s, float scalar, const si
   return guard([&] {
     check_f32(dtype, "mul_scalar");
     const size_t n = numel(shape, rank);
+    launch(ctx, "mul_scalar");
+    R(ctx, s, 4 * n);
     orc_mul_scalar(F(s), scalar, out_buf(ctx, n, out), n);
     logf("op mul_scalar");
   });
@@ -375,6 +545,10 @@ int orca_hip_div_backward_rhs(orca_hip_ctx* ctx, const void* g, const void* l, c
   return guard([&] {
     check_f32(dtype, "div_backward_rhs");
     const size_t n = numel(shape, rank);
+    launch(ctx, "div_backward_rhs");
+    R(ctx, g, 4 * n);
+    R(ctx, l, 4 * n);
+    R(ctx, r, 4 * n);
     orc_div_backward_rhs(F(g), F(l), F(r), out_buf(ctx, n, out), n);
     logf("op div_backward_rhs");
   });
@@ -382,6 +556,9 @@ int orca_hip_div_backward_rhs(orca_hip_ctx* ctx, const void* g, const void* l, c
 
 int orca_hip_accumulate_grad(orca_hip_ctx* ctx, const void* a, const void* b, size_t n, void** out) {
   return guard([&] {
+    launch(ctx, "accumulate_grad");
+    R(ctx, a, 4 * n);
+    R(ctx, b, 4 * n);
     orc_accumulate_grad(F(a), F(b), out_buf(ctx, n, out), n);
     logf("op accumulate_grad");
   });
@@ -392,6 +569,8 @@ int orca_hip_accumulate_grad(orca_hip_ctx* ctx, const void* a, const void* b, si
                       int dtype, void** out) {                                                             \
     return guard([&] {                                                                                     \
       check_f32(dtype, #NAME);                                                                             \
+      launch(ctx, #NAME);                                                                                  \
+      R(ctx, s, 4 * numel(in, ir));                                                                        \
       check_oracle(FN(F(s), out_buf(ctx, numel(os, orank), out), in, ir, os, orank), #NAME);               \
       logf(std::string("op ") + #NAME);                                                                    \
     });                                                                                                    \
@@ -404,6 +583,10 @@ int orca_hip_max_to_shape_backward(orca_hip_ctx* ctx, const void* g, const void*
                                    size_t ir, const size_t* os, size_t orank, int dtype, void** out) {
   return guard([&] {
     check_f32(dtype, "max_to_shape_backward");
+    launch(ctx, "max_to_shape_backward");
+    R(ctx, g, 4 * numel(os, orank));
+    R(ctx, x, 4 * numel(in, ir));
+    R(ctx, y, 4 * numel(os, orank));
     check_oracle(orc_max_to_shape_backward(F(g), F(x), F(y), out_buf(ctx, numel(in, ir), out), in, ir, os, orank),
                  "max_to_shape_backward");
     logf("op max_to_shape_backward");
@@ -419,6 +602,9 @@ int orca_hip_ew_program(orca_hip_ctx* ctx, size_t n, const orca_hip_ew_input* in
         n_regs > ORCA_HIP_EW_MAX_REGS || n_inputs > n_regs)
       fail(ORCA_HIP_ERR_INTERNAL, "program exceeds the interpreter's limits");
     std::vector<std::vector<float>> reg(n_regs, std::vector<float>(n));
+    launch(ctx, "program");
+    for (size_t i = 0; i < n_inputs; ++i) R(ctx, inputs[i].ptr, 4 * std::min<uint64_t>(inputs[i].mod, n ? n : 1));
+    for (size_t o = 0; o < n_outputs; ++o) W(ctx, outputs[o], 4 * n);
     for (size_t i = 0; i < n_inputs; ++i) {
       const orca_hip_ew_input& in = inputs[i];
       if (!in.mod || !in.div) fail(ORCA_HIP_ERR_INTERNAL, "bad input map");
@@ -475,15 +661,20 @@ int orca_hip_ew_program(orca_hip_ctx* ctx, size_t n, const orca_hip_ew_input* in
       std::copy(reg[out_regs[o]].begin(), reg[out_regs[o]].end(), outputs[o]);
     }
     logf("program " + std::to_string(n_inputs) + " " + std::to_string(n_outputs) + " " + std::to_string(n_instrs) +
-         " " + std::to_string(n_regs));
+         " " + std::to_string(n_regs) + (ctx->main ? " side" : ""));
   });
 }
 
 // ---- fused loss and optimizers
-int orca_hip_softmax_ce(orca_hip_ctx*, const float* logits, size_t B, size_t C, const float* onehot,
+int orca_hip_softmax_ce(orca_hip_ctx* ctx, const float* logits, size_t B, size_t C, const float* onehot,
                         const int32_t* labels, float* loss, float* dlogits, int32_t* preds, int64_t* correct) {
   return guard([&] {
     if (!onehot || labels || preds || correct) fail(ORCA_HIP_ERR_INTERNAL, "the stand-in takes one-hot targets only");
+    launch(ctx, "softmax_ce");
+    R(ctx, logits, 4 * B * C);
+    R(ctx, onehot, 4 * B * C);
+    W(ctx, loss, 4);
+    W(ctx, dlogits, 4 * B * C);
     std::vector<float> d(B * C);
     float l = 0.0f;
     if (orc_cross_entropy(logits, onehot, B, C, &l, d.data()) != 0) fail(ORCA_HIP_ERR_INTERNAL, "oracle CE failed");
@@ -509,6 +700,20 @@ int orca_hip_adamw_multi(orca_hip_ctx* ctx, const orca_hip_opt_segment* segs, si
   return guard([&] {
     const orc_opt o = make_opt(1, lr, beta1, beta2, eps, weight_decay);
     size_t total = 0;
+    launch(ctx, "adamw_multi");
+    for (size_t i = 0; i < n_segs; ++i) {
+      const orca_hip_opt_segment& s = segs[i];
+      R(ctx, s.p_src, 4 * s.n);
+      R(ctx, s.g, 4 * s.n);
+      R(ctx, s.m, 4 * s.n);
+      R(ctx, s.v, 4 * s.n);
+    }
+    for (size_t i = 0; i < n_segs; ++i) {
+      const orca_hip_opt_segment& s = segs[i];
+      W(ctx, s.p_dst, 4 * s.n);
+      W(ctx, s.m, 4 * s.n);
+      W(ctx, s.v, 4 * s.n);
+    }
     for (size_t i = 0; i < n_segs; ++i) {
       const orca_hip_opt_segment& s = segs[i];
       std::vector<float> p(s.p_src, s.p_src + s.n);
@@ -524,6 +729,13 @@ int orca_hip_sgd_multi(orca_hip_ctx* ctx, const orca_hip_opt_segment* segs, size
   return guard([&] {
     const orc_opt o = make_opt(0, lr, 0, 0, 0, 0);
     size_t total = 0;
+    launch(ctx, "sgd_multi");
+    for (size_t i = 0; i < n_segs; ++i) {
+      const orca_hip_opt_segment& s = segs[i];
+      R(ctx, s.p_src, 4 * s.n);
+      R(ctx, s.g, 4 * s.n);
+    }
+    for (size_t i = 0; i < n_segs; ++i) W(ctx, segs[i].p_dst, 4 * segs[i].n);
     for (size_t i = 0; i < n_segs; ++i) {
       const orca_hip_opt_segment& s = segs[i];
       std::vector<float> p(s.p_src, s.p_src + s.n);
@@ -535,17 +747,25 @@ int orca_hip_sgd_multi(orca_hip_ctx* ctx, const orca_hip_opt_segment* segs, size
   });
 }
 
-int orca_hip_adamw_step(orca_hip_ctx*, float* p, const float* g, float* m, float* v, size_t n, double lr, double beta1,
-                        double beta2, double eps, double weight_decay, int64_t t) {
+int orca_hip_adamw_step(orca_hip_ctx* ctx, float* p, const float* g, float* m, float* v, size_t n, double lr,
+                        double beta1, double beta2, double eps, double weight_decay, int64_t t) {
   return guard([&] {
+    launch(ctx, "adamw_step");
+    R(ctx, g, 4 * n);
+    W(ctx, p, 4 * n);
+    W(ctx, m, 4 * n);
+    W(ctx, v, 4 * n);
     const orc_opt o = make_opt(1, lr, beta1, beta2, eps, weight_decay);
     orc_adamw_update(p, g, m, v, n, &o, t);
     logf("adamw_step");
   });
 }
 
-int orca_hip_sgd_step(orca_hip_ctx*, float* p, const float* g, size_t n, double lr) {
+int orca_hip_sgd_step(orca_hip_ctx* ctx, float* p, const float* g, size_t n, double lr) {
   return guard([&] {
+    launch(ctx, "sgd_step");
+    R(ctx, g, 4 * n);
+    W(ctx, p, 4 * n);
     const orc_opt o = make_opt(0, lr, 0, 0, 0, 0);
     orc_sgd_update(p, g, n, &o);
     logf("sgd_step");

@@ -112,6 +112,45 @@ def test_composed_mlp784_1024_b256_teacher_forced(hb, fused):
     assert run.opt.t == 12
 
 
+@pytest.mark.parametrize("wl", [synth.MLP_LARGE, synth.MLP_SMALL])
+def test_composed_update_on_second_stream_changes_no_bit(ctx, wl):
+    """The unchanged drop-in step (the reference's composed optimizer): an update program whose
+    gradient came from an earlier weight-gradient product runs on the context's second stream,
+    beside the backward's remaining products, into blocks released before that product.  Four
+    steps and the next forward with and without that, from the same start, no host read in
+    between: logits, parameters and moments bit-identical, and the second stream wrote moments
+    when it was allowed."""
+    from orcaml_amd.backend import HipBackend
+
+    w = synth.WORKLOADS[wl]
+    o = w["opt"]
+    params, x, labels, onehot = synth.mlp_problem(w["seed"], w["dims"], w["batch"])
+    out = {}
+    for overlap in (True, False):
+        print(f"composed update, {wl}, overlap={overlap}", flush=True)
+        ad = A.Autodiff(HipBackend(ctx, overlap=overlap))
+        model = A.build_mlp(ad, params)
+        if o["kind"] == "adamw":
+            opt = A.AdamW(model.parameters(), lr=o["lr"], weight_decay=o["weight_decay"])
+        else:
+            opt = A.SGD(model.parameters(), lr=o["lr"])
+        loss_fn = A.CrossEntropyLoss()
+        xt, tt = A.Tensor.from_numpy(ad, x), A.Tensor.from_numpy(ad, onehot)
+        for _ in range(4):
+            opt.zero_grad()
+            loss_fn(model(xt), tt).backward()
+            opt.step()
+        logits = model(xt).numpy()  # runs the last update's programs, then the forward
+        if o["kind"] == "adamw":
+            marked = sum(m.storage.primal.marked for m in opt.m)  # written there, not yet read here
+            assert (marked > 0) == overlap, marked
+        out[overlap] = [logits] + [p.tensor.numpy() for p in model.parameters()]
+        if o["kind"] == "adamw":
+            out[overlap] += [m.numpy() for m in opt.m] + [v.numpy() for v in opt.v]
+    for i, (a, b) in enumerate(zip(out[True], out[False])):
+        np.testing.assert_array_equal(a, b, err_msg=f"array {i}")
+
+
 @pytest.mark.parametrize("wl,bias", [(synth.MLP_LARGE, True), (synth.MLP_SMALL, True), (synth.MLP_MEDIUM, False)])
 def test_fused_update_on_second_stream_changes_no_bit(ctx, wl, bias):
     """The fused optimizer pass (AdamW at 784-4096-4096-10 / B 1024, SGD at 784-128-128-10 /

@@ -35,7 +35,11 @@ def lib(fake_path, monkeypatch):
     lib = fake_lib.load(fake_path)
     fake_lib.install(monkeypatch, lib)
     fake_lib.clear(lib)
-    return lib
+    before = fake_lib.races(lib)
+    yield lib
+    gc.collect()
+    # every access the two streams make is ordered by the events and joins the library placed
+    assert fake_lib.races(lib) == before, [line for line in fake_lib.log(lib) if line.startswith("RACE")]
 
 
 @pytest.fixture()
@@ -66,7 +70,7 @@ def down(hb, s):
 
 def programs(lib):
     """(inputs, outputs, ops, registers) of every program launched since the last clear."""
-    return [tuple(int(v) for v in line.split()[1:]) for line in fake_lib.log(lib) if line.startswith("program ")]
+    return [tuple(int(v) for v in line.split()[1:5]) for line in fake_lib.log(lib) if line.startswith("program ")]
 
 
 def test_adamw_chain_is_one_program_with_three_outputs(lib, hb):
@@ -362,6 +366,46 @@ def test_composed_step_folds_and_fuses(lib, ctx):
 
 
 @pytest.mark.parametrize("kind", ["adamw", "sgd"])
+def test_composed_update_runs_beside_the_backward_products(lib, ctx, kind):
+    """The reference's own composed optimizer (unchanged user code): an update program whose
+    inputs were all computed before the backward's last product runs on the second stream,
+    after the mark of the product its gradient came from, with every output written there
+    (the program's launch is the only thing between the switch to the second stream, its
+    wait and its mark), and every later access to what it read or wrote is ordered after it
+    (the stand-in's happens-before check).  The values equal the same steps without overlap
+    and the oracle's loop."""
+    from orcaml_amd.backend import HipBackend
+
+    dims, B = (784, 48, 40, 10), 16
+    params, x, labels, onehot = synth.mlp_problem(15, dims, B)
+    opt = dict(lr=0.1) if kind == "sgd" else dict(lr=1e-3, weight_decay=0.01)
+    out = {}
+    for overlap in (True, False):
+        fake_lib.clear(lib)
+        ad = A.Autodiff(HipBackend(ctx, overlap=overlap))
+        out[overlap] = composed(ad, params, x, onehot, kind, 3, **opt)
+        log = fake_lib.log(lib)
+        side = [i for i, line in enumerate(log) if line.startswith("program ") and line.endswith(" side")]
+        if overlap:
+            # the updates of layers 1 and 2 (flushed when the next step or the final read needs them)
+            assert len(side) >= 4, log
+            for i in side:
+                assert re.match(r"side [1-9]", log[i - 2]) and log[i - 1].startswith("wait ") and \
+                    log[i - 1].endswith(" side"), log[i - 3:i + 3]
+                assert log[i + 1].startswith("record ") and log[i + 1].endswith(" side") and log[i + 2] == "main"
+            # and whatever reads what they wrote waits for them: the stand-in's order check
+            assert not [line for line in log if line.startswith("RACE")], log
+        else:
+            assert not side and not any(line.startswith("side ") for line in log)
+    for a, b in zip(out[True][3], out[False][3]):
+        np.testing.assert_array_equal(a, b)
+    np.testing.assert_array_equal(out[True][0], out[False][0])
+    ref = O.mlp_train(dims, params, x, onehot, O.make_opt(kind, **opt), steps=3)
+    for p, r in zip(out[True][3], ref["params"]):
+        np.testing.assert_array_equal(p.reshape(r.shape), r)
+
+
+@pytest.mark.parametrize("kind", ["adamw", "sgd"])
 def test_fused_update_on_the_second_stream_changes_no_bit(lib, ctx, kind):
     """The fused optimizer's pass with overlap: the parameters whose gradients came from an
     earlier weight-gradient product are updated on the second stream (split between a bounded
@@ -380,10 +424,11 @@ def test_fused_update_on_the_second_stream_changes_no_bit(lib, ctx, kind):
         log = fake_lib.log(lib)
         side = [line for line in log if line.startswith(f"{kind}_multi") and line.endswith(" side")]
         if overlap:
-            # from the second step on, layers >= 1 (W, b of layers 1 and 2) go to the second stream
+            # in every step (the backward products leave marks whenever overlap is allowed), layers
+            # >= 1 (W, b of layers 1 and 2) go to the second stream
             n_side = sum(int(line.split()[2]) for line in side)
             per_step = sum(int(np.prod(p.shape)) for p in params[2:])
-            assert n_side == 2 * per_step, (side, per_step)
+            assert n_side == 3 * per_step, (side, per_step)
             assert any(re.match(r"side [1-9]", line) for line in log) and "side -1" in log
         else:
             assert not side
