@@ -556,7 +556,8 @@ typedef struct {
   const float* bias;   /* [N] for EPI_BIAS / EPI_BIAS_RELU */
   const float* mask;   /* [M][ldmask] for EPI_RELU_MASK: the ReLU output (or pre-activation) */
   size_t ldmask;
-  float* colsum;       /* optional [N]: column sums of op(B) over K (bias gradient of dW = X^T dY) */
+  float* colsum;       /* optional [N]: column sums of op(B) over K in ascending k, the bits
+                          sum_to_shape gives (bias gradient of dW = X^T dY) */
   float* pre;          /* [M][ldc] for EPI_BIAS_RELU_PRE (acc + bias) and EPI_RELU_MASK_PRE (acc) */
   orca_hip_event** done; /* optional: receives an event completing with the product's last launch,
                             as orca_hip_matmul_ev's (no reference counterpart) */

@@ -1521,6 +1521,7 @@ int orca_hip_gemm(orca_hip_ctx* ctx, int trans_a, int trans_b, size_t M, size_t 
       e.mask = epi->mask;
       e.ldmask = epi->ldmask;
       e.colsum = epi->colsum;
+      e.exact_colsum = true;
       const bool has_bias = e.kind == ORCA_HIP_EPI_BIAS || e.kind == ORCA_HIP_EPI_BIAS_RELU ||
                             e.kind == ORCA_HIP_EPI_BIAS_RELU_PRE;
       const bool has_mask = e.kind == ORCA_HIP_EPI_RELU_MASK || e.kind == ORCA_HIP_EPI_RELU_MASK_PRE;

@@ -106,6 +106,8 @@ class CachingAllocator {
   // A cached block released at or before tick `clock`, oldest first, or null (this never
   // allocates device memory).
   void* allocate_released_by(size_t bytes, uint64_t clock);
+  // How many cached blocks of this size were released at or before tick `clock`.
+  size_t count_released_by(size_t bytes, uint64_t clock);
   uint64_t clock();
   void release(void* p);
   void empty(hipStream_t stream);
@@ -267,6 +269,7 @@ void* ctx_allocate(orca_hip_ctx* ctx, size_t bytes);
 // (its last users are all before that event), or null.  Called while launches still go to
 // the context stream, like ctx_allocate.
 void* ctx_allocate_released_by(orca_hip_ctx* ctx, size_t bytes, uint64_t clock);
+size_t ctx_count_released_by(orca_hip_ctx* ctx, size_t bytes, uint64_t clock);
 uint64_t ctx_release_clock(orca_hip_ctx* ctx);
 // An unrecorded event for ordering the context's two streams (from the context's pool;
 // orca_hip_event_release gives it back).

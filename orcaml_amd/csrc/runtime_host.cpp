@@ -155,6 +155,15 @@ void* CachingAllocator::allocate_released_by(size_t bytes, uint64_t clock) {
   return p;
 }
 
+size_t CachingAllocator::count_released_by(size_t bytes, uint64_t clock) {
+  const size_t r = round_size(bytes);
+  std::lock_guard<std::mutex> lk(mu_);
+  size_t n = 0;
+  for (auto it = cached_.lower_bound(r); it != cached_.end() && it->first == r && it->second.released <= clock; ++it)
+    ++n;
+  return n;
+}
+
 uint64_t CachingAllocator::clock() {
   std::lock_guard<std::mutex> lk(mu_);
   return clock_;
@@ -424,6 +433,10 @@ void* ctx_allocate_released_by(orca_hip_ctx* ctx, size_t bytes, uint64_t clock) 
          "Internal error: a device allocation was requested while launches go to the side stream "
          "(only non-allocating launches may run there)");
   return ctx->alloc.allocate_released_by(bytes, clock);
+}
+
+size_t ctx_count_released_by(orca_hip_ctx* ctx, size_t bytes, uint64_t clock) {
+  return ctx->alloc.count_released_by(bytes, clock);
 }
 
 uint64_t ctx_release_clock(orca_hip_ctx* ctx) { return ctx->alloc.clock(); }

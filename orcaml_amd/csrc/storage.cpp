@@ -775,18 +775,21 @@ bool side_flush(Backend* be, const Walk& w, const Program& prog, const std::vect
     src[i] = x;
     if (!x->side_made) need = std::max(need, x->done_seq + 1);
   }
+  // The earliest mark after the inputs for which cached blocks released before it can take
+  // the outputs; not the latest mark, so that a product launched after it runs beside.
   MarkP wait;
-  for (auto& m : be->recent) {
-    if (m->seq >= need) {
+  for (size_t i = 0; i + 1 < be->recent.size(); ++i) {
+    const MarkP& m = be->recent[i];
+    if (m->seq >= need && ctx_count_released_by(be->ctx, 4 * n, m->clock) >= out_idx.size()) {
       wait = m;
       break;
     }
   }
-  if (!wait || wait == be->recent.back()) return false;  // no product launched after it to run beside
+  if (!wait) return false;
   std::vector<BufP> bufs;
   for (size_t i = 0; i < out_idx.size(); ++i) {
     void* p = ctx_allocate_released_by(be->ctx, 4 * n, wait->clock);
-    if (!p) return false;  // the blocks taken so far go back to the cache
+    if (!p) fail(ORCA_HIP_ERR_INTERNAL, "side_flush: a counted cached block was not there");
     bufs.push_back(own(be->ctx, p, 4 * n));
   }
   std::vector<orca_hip_ew_input> ins(w.leaves.size());

@@ -466,7 +466,8 @@ int orca_hip_gemm(orca_hip_ctx* ctx, int ta, int tb, size_t M, size_t N, size_t 
       check_oracle(orc_sum_to_shape(b.data(), epi->colsum, in, 2, cs, 2), "gemm colsum");
     }
     logf("gemm " + std::to_string(M) + "x" + std::to_string(N) + "x" + std::to_string(K) + " " + std::to_string(ta) +
-         std::to_string(tb) + " epi " + std::to_string(kind));
+         std::to_string(tb) + " epi " + std::to_string(kind) + (epi && epi->colsum ? " colsum" : "") +
+         (ctx->main ? " side" : ""));
     if (epi && epi->done) {
       *epi->done = next_event();
       event_at(ctx, *epi->done);

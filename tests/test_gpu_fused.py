@@ -220,24 +220,18 @@ def test_gemm_grid_of_half_the_cus_splits_k(ctx):
     np.testing.assert_array_equal(got, (A.astype(np.int64) @ B.astype(np.int64)).astype(np.float32))
 
 
-@pytest.mark.parametrize("M,N,K,exact", [(128, 256, 64, True), (784, 4096, 1024, True), (4096, 10, 1024, False),
-                                         (33, 70, 5, True), (512, 384, 96, True), (128, 128, 4096, False),
-                                         (784, 4092, 1020, True), (132, 260, 36, True)])
-def test_gemm_colsum_is_bias_gradient(ctx, M, N, K, exact):
-    """dW = X^T dY with the bias column sum fused.  With one K-chunk per tile
-    the column sum equals sum_to_shape(dY, [1, N]) bit for bit (same ascending
-    row order); a split-K launch (skinny N) sums per-chunk partials in chunk
-    order, so it matches to f32 rounding."""
+@pytest.mark.parametrize("M,N,K", [(128, 256, 64), (784, 4096, 1024), (4096, 10, 1024), (33, 70, 5), (512, 384, 96),
+                                   (128, 128, 4096), (784, 4092, 1020), (132, 260, 36)])
+def test_gemm_colsum_is_bias_gradient(ctx, M, N, K):
+    """dW = X^T dY with the bias column sum fused.  The column sum equals
+    sum_to_shape(dY, [1, N]) bit for bit (ascending row order): folded into the
+    product's loads of dY with one K-chunk per tile, else (a split K, a narrow
+    product) taken in a pass of its own."""
     rng = np.random.default_rng(M + N + K)
     X = rng.standard_normal((K, M)).astype(np.float32)  # stored [B][in]
     dY = rng.standard_normal((K, N)).astype(np.float32)
     dW, cs = run_gemm(ctx, True, False, X, dY, colsum=True)
-    want = O.sum_to_shape(dY, (1, N)).reshape(N)
-    if exact:
-        np.testing.assert_array_equal(cs, want)
-    else:
-        bound = K * 2.0 ** -24 * np.abs(dY.astype(np.float64)).sum(0)
-        assert (np.abs(cs.astype(np.float64) - want) <= bound).all()
+    np.testing.assert_array_equal(cs, O.sum_to_shape(dY, (1, N)).reshape(N))
     assert_gemm_error_bound(dW, X.T, dY)
 
 

@@ -355,7 +355,7 @@ def test_composed_step_folds_and_fuses(lib, ctx):
     optim.step()
     log = fake_lib.log(lib)
     gemms = [line for line in log if line.startswith("gemm ")]
-    epis = sorted(int(line.split()[-1]) for line in gemms)
+    epis = sorted(int(line.split()[line.split().index("epi") + 1]) for line in gemms)
     # forward: two hidden layers with bias + ReLU (pre-activation kept for ReluBackward) and the
     # head with its bias; backward: dX through the two ReLUs with the mask epilogue
     assert epis.count(_lib.EPI_BIAS_RELU_PRE) == 2 and epis.count(_lib.EPI_BIAS) == 1, gemms
