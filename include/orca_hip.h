@@ -572,6 +572,20 @@ typedef struct {
 int orca_hip_gemm(orca_hip_ctx* ctx, int trans_a, int trans_b, size_t M, size_t N, size_t K, const float* A,
                   size_t lda, const float* B, size_t ldb, float* C, size_t ldc, const orca_hip_epilogue* epi);
 
+/* The backward of a Linear with at most 16 outputs (a classifier head), as the separate
+ * products compute it but from one grid: dW[K][C] = H^T G with H [B][K] and G [B][C]
+ * (MatMulBackward's grad_W, orca-autograd/src/backend.rs:1467-1495), db[C] = the column sums
+ * of G in ascending row order (ExpandBackward's sum_to_shape, 1684-1697; optional), and
+ * dH[B][K] = G W^T with W [K][C] (grad_X) through an optional ReLU mask (mask[b][k] > 0, and
+ * dH_pre = the unmasked product when non-null: orca_hip_gemm's EPI_RELU_MASK and
+ * EPI_RELU_MASK_PRE).  Every value has the bits of orca_hip_matmul_colsum and orca_hip_gemm
+ * computing them one by one: the same kernels' sums in one launch, plus the weight gradient's
+ * slice reduction.  `done` (optional) as orca_hip_matmul_ev's.  Requires 1 <= C <= 16.  No
+ * reference counterpart: it takes the launches of three trait calls. */
+int orca_hip_narrow_linear_backward(orca_hip_ctx* ctx, const float* H, size_t B, size_t K, const float* G, size_t C,
+                                    const float* W, const float* mask, float* dH, float* dH_pre, float* dW, float* db,
+                                    orca_hip_event** done);
+
 /* Fused softmax cross-entropy forward + gradient, one wavefront per row
  * (replaces the ~21-op composition of python/orca/nn/loss.py:59-100 and its
  * tape backward).  Targets are either one-hot rows `onehot` [B][C] or class

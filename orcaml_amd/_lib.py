@@ -231,6 +231,7 @@ SIGNATURES = {
     "orca_hip_max_to_shape_backward": [_P, _P, _P, _P, _SZP, _SZ, _SZP, _SZ, _I, _PP],
     "orca_hip_has_nan_or_inf": [_P, _P, _SZ, _I, ctypes.POINTER(_I)],
     "orca_hip_gemm": [_P, _I, _I, _SZ, _SZ, _SZ, _P, _SZ, _P, _SZ, _P, _SZ, ctypes.POINTER(Epilogue)],
+    "orca_hip_narrow_linear_backward": [_P, _P, _SZ, _SZ, _P, _SZ, _P, _P, _P, _P, _P, _P, _PP],
     "orca_hip_softmax_ce": [_P, _P, _SZ, _SZ, _P, _P, _P, _P, _P, _P],
     "orca_hip_head_forward_ce": [_P, _P, _SZ, _SZ, _P, _P, _SZ, _P, _P, _P, _P, _P, _P, _P],
     "orca_hip_head_backward": [_P, _P, _SZ, _SZ, _P, _SZ, _P, _I, _P, _P, _P],

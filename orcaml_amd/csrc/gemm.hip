@@ -876,23 +876,22 @@ __global__ void __launch_bounds__(NW_THREADS) gemm_nn_narrow_kernel(const float*
 // C[M x N] = A[M x K] B^T with B stored [N][K], K <= KP.  Thread t of block
 // (x, y) owns column 256 x + t (its row of B in registers) for rows
 // rows_per_block y .. + rows_per_block - 1, whose A values are staged in LDS
-// per pass of 64 rows and read as broadcasts.  Each output is a dot product
-// over k in order; a wave's stores cover 64 consecutive columns of a row.
+// (`as`, 64 x KP floats) per pass of 64 rows and read as broadcasts.  Each output
+// is a dot product over k in order; a wave's stores cover 64 consecutive columns
+// of a row.
 template <int KP>
-__global__ void __launch_bounds__(NW_THREADS) gemm_nt_smallk_kernel(const float* __restrict__ A, int64_t lda,
-                                                                     const float* __restrict__ B, int64_t ldb,
-                                                                     float* __restrict__ C, int64_t ldc, int M, int N,
-                                                                     int K, int rows_per_block,
-                                                                     const float* __restrict__ mask, int64_t ldmask,
-                                                                     float* __restrict__ pre) {
+__device__ __forceinline__ void nt_smallk_block(int bx, int by, float* as, const float* __restrict__ A, int64_t lda,
+                                                const float* __restrict__ B, int64_t ldb, float* __restrict__ C,
+                                                int64_t ldc, int M, int N, int K, int rows_per_block,
+                                                const float* __restrict__ mask, int64_t ldmask,
+                                                float* __restrict__ pre) {
   constexpr int PASS = 64;
-  __shared__ __align__(16) float as[PASS * KP];
   const int tid = threadIdx.x;
-  const int n = blockIdx.x * NW_THREADS + tid;
+  const int n = bx * NW_THREADS + tid;
   float b[KP];
 #pragma unroll
   for (int k = 0; k < KP; ++k) b[k] = n < N && k < K ? B[(int64_t)n * ldb + k] : 0.0f;
-  const int m_beg = blockIdx.y * rows_per_block, m_end = min(M, m_beg + rows_per_block);
+  const int m_beg = by * rows_per_block, m_end = min(M, m_beg + rows_per_block);
   for (int p0 = m_beg; p0 < m_end; p0 += PASS) {
     const int cnt = min(PASS, m_end - p0);
     float av[PASS * KP / NW_THREADS];
@@ -937,26 +936,36 @@ __global__ void __launch_bounds__(NW_THREADS) gemm_nt_smallk_kernel(const float*
   }
 }
 
+template <int KP>
+__global__ void __launch_bounds__(NW_THREADS) gemm_nt_smallk_kernel(const float* __restrict__ A, int64_t lda,
+                                                                     const float* __restrict__ B, int64_t ldb,
+                                                                     float* __restrict__ C, int64_t ldc, int M, int N,
+                                                                     int K, int rows_per_block,
+                                                                     const float* __restrict__ mask, int64_t ldmask,
+                                                                     float* __restrict__ pre) {
+  __shared__ __align__(16) float as[64 * KP];
+  nt_smallk_block<KP>(blockIdx.x, blockIdx.y, as, A, lda, B, ldb, C, ldc, M, N, K, rows_per_block, mask, ldmask, pre);
+}
+
 // C[M x N] = A^T B with A stored [K][M], B [K][N], N <= NP.  Block (x, y):
 // columns 256 x .. + 255 (4 per lane, a float4 of an A row when aligned) and
-// K slice y.  Per 64-row chunk the block stages B's rows in LDS and wave w
-// takes chunk rows 16 w .. 16 w + 15; the next chunk's loads are in flight
-// while a chunk is computed.  The lane's sums run in k order, then the 4
-// waves are added in wave order.  With one slice the result is C, else
-// part[slice][M][N] (ldo = N).
+// K slice y.  Per 64-row chunk the block stages B's rows in LDS (`bs`,
+// TN_CHUNK x NP floats) and wave w takes chunk rows 16 w .. 16 w + 15; the next
+// chunk's loads are in flight while a chunk is computed.  The lane's sums run in
+// k order, then the 4 waves are added in wave order: waves 1, 2 and 3 hand theirs
+// to wave 0 in turn through `red` (64 x (4 NP + 1) floats), and wave 0 stores.
+// With one slice the result is C, else part[slice][M][N] (ldo = N).
 template <int NP>
-__global__ void __launch_bounds__(NW_THREADS) gemm_tn_narrow_kernel(const float* __restrict__ A, int64_t lda,
-                                                                     const float* __restrict__ B, int64_t ldb,
-                                                                     float* __restrict__ out, int64_t ldo, int M, int N,
-                                                                     int K, int kslice, int vec_a) {
+__device__ __forceinline__ void tn_narrow_block(int bx, int by, float* bs, float* red, const float* __restrict__ A,
+                                                int64_t lda, const float* __restrict__ B, int64_t ldb,
+                                                float* __restrict__ out, int64_t ldo, int M, int N, int K, int kslice,
+                                                int vec_a) {
   constexpr int RED = 4 * NP + 1;
   constexpr int PER_WAVE = TN_CHUNK / 4;
   constexpr int PER_T = TN_CHUNK * NP / NW_THREADS;  // staged B values per thread
-  __shared__ __align__(16) float bs[TN_CHUNK * NP];
-  __shared__ float red[4 * 64 * RED];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int m0 = blockIdx.x * 256 + 4 * lane;
-  const int k_beg = blockIdx.y * kslice, k_end = min(K, k_beg + kslice);
+  const int m0 = bx * 256 + 4 * lane;
+  const int k_beg = by * kslice, k_end = min(K, k_beg + kslice);
   const bool vec = vec_a && m0 + 3 < M;
   float acc[4][NP];
 #pragma unroll
@@ -1010,23 +1019,45 @@ __global__ void __launch_bounds__(NW_THREADS) gemm_tn_narrow_kernel(const float*
         for (int n = 0; n < NP; ++n) acc[i][n] = fmaf(ac[r][i], b[n], acc[i][n]);
     }
   }
+  float* mine = red + lane * RED;
+  for (int src = 1; src < 4; ++src) {
+    __syncthreads();  // wave 0 has read the previous hand-over
+    if (w == src) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+      for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int n = 0; n < NP; ++n) red[(w * 64 + lane) * RED + i * NP + n] = acc[i][n];
-  __syncthreads();
-  // 256 threads store the block's 256 x N outputs: thread t takes entries t, t + 256, ...
-  float* o = out + (int64_t)blockIdx.y * M * N;
-  const int mb = blockIdx.x * 256;
-  for (int q = tid; q < 256 * NP; q += NW_THREADS) {
-    const int col = q / NP, n = q % NP, m = mb + col;
-    if (m < M && n < N) {
-      const int l = col / 4, src = (col % 4) * NP + n;
-      const float sum = ((red[l * RED + src] + red[(64 + l) * RED + src]) + red[(128 + l) * RED + src]) +
-                        red[(192 + l) * RED + src];
-      o[(int64_t)m * ldo + n] = sum;
+        for (int n = 0; n < NP; ++n) mine[i * NP + n] = acc[i][n];
+    }
+    __syncthreads();
+    if (w == 0) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int n = 0; n < NP; ++n) acc[i][n] = acc[i][n] + mine[i * NP + n];
     }
   }
+  if (w == 0) {
+    float* o = out + (int64_t)by * M * N;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int m = m0 + i;
+      if (m < M) {
+#pragma unroll
+        for (int n = 0; n < NP; ++n)
+          if (n < N) o[(int64_t)m * ldo + n] = acc[i][n];
+      }
+    }
+  }
+}
+
+template <int NP>
+__global__ void __launch_bounds__(NW_THREADS) gemm_tn_narrow_kernel(const float* __restrict__ A, int64_t lda,
+                                                                     const float* __restrict__ B, int64_t ldb,
+                                                                     float* __restrict__ out, int64_t ldo, int M, int N,
+                                                                     int K, int kslice, int vec_a) {
+  __shared__ __align__(16) float bs[TN_CHUNK * NP];
+  __shared__ float red[64 * (4 * NP + 1)];
+  tn_narrow_block<NP>(blockIdx.x, blockIdx.y, bs, red, A, lda, B, ldb, out, ldo, M, N, K, kslice, vec_a);
 }
 
 // C[m][n] = sum over slices s (in order) of part[s][m][n] (+ bias[n] when given).
@@ -1047,6 +1078,93 @@ __global__ void __launch_bounds__(NW_THREADS) gemm_narrow_reduce_kernel(const fl
     if (bias) sum = sum + bias[e % N];  // the bias epilogue
     C[(e / N) * ldc + e % N] = sum;
   }
+}
+
+// colsum[c] = the sum over rows r of G[r][c] (row stride ldg) in ascending r, for C <= 16
+// columns: the additions of sum_to_shape's loop (and of colreduce_kernel), so the same bits.
+// Chunks of 256 rows are staged transposed in LDS (`st`, 16 x CS_LD floats) and thread c adds
+// its column's values in row order.
+constexpr int CS_ROWS = 256, CS_LD = CS_ROWS + 4;
+__device__ __forceinline__ void colsum_narrow_block(float* st, const float* __restrict__ G, int64_t ldg, int rows, int C,
+                                                    float* __restrict__ colsum) {
+  constexpr int PER_T = CS_ROWS * NW_MAX / NW_THREADS;
+  const int t = threadIdx.x;
+  float acc = 0.0f;
+  for (int r0 = 0; r0 < rows; r0 += CS_ROWS) {
+    const int cnt = min(CS_ROWS, rows - r0), total = cnt * C;
+    float v[PER_T];
+#pragma unroll
+    for (int j = 0; j < PER_T; ++j) {
+      const int e = t + j * NW_THREADS;
+      v[j] = e < total ? G[(int64_t)(r0 + e / C) * ldg + e % C] : 0.0f;
+    }
+    __syncthreads();  // the previous chunk has been added up
+#pragma unroll
+    for (int j = 0; j < PER_T; ++j) {
+      const int e = t + j * NW_THREADS;
+      if (e < total) st[(e % C) * CS_LD + e / C] = v[j];
+    }
+    __syncthreads();
+    if (t < C) {
+      const float* col = st + t * CS_LD;
+      int r = 0;
+      for (; r + 32 <= cnt; r += 32) {
+        floatx4 x[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) x[u] = *reinterpret_cast<const floatx4*>(col + r + 4 * u);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          acc = acc + x[u].x;
+          acc = acc + x[u].y;
+          acc = acc + x[u].z;
+          acc = acc + x[u].w;
+        }
+      }
+      for (; r < cnt; ++r) acc = acc + col[r];
+    }
+  }
+  if (t < C) colsum[t] = acc;
+}
+
+// The three products of a narrow Linear's backward in one grid (block roles by index): the
+// column sum of G (one block), the weight gradient's slices (tn_narrow_block) and the input
+// gradient's row groups (nt_smallk_block), each role the same code as its own kernel.
+struct NarrowLinearBwArgs {
+  const float* H;   // [B][K]
+  const float* G;   // [B][C]
+  const float* W;   // [K][C]
+  const float* mask;
+  float* dw_out;    // dW, or its slice partials
+  float* dH;
+  float* dH_pre;
+  float* db;
+  int B, K, C;
+  int tn_gx, tn_blocks, tn_kslice, tn_vec;
+  int nt_gx, nt_blocks, nt_rows;
+};
+
+template <int NP>
+__global__ void __launch_bounds__(NW_THREADS) narrow_linear_bw_kernel(NarrowLinearBwArgs a) {
+  constexpr int TN_SMEM = TN_CHUNK * NP + 64 * (4 * NP + 1);
+  constexpr int CS_SMEM = NW_MAX * CS_LD;
+  constexpr int SMEM = TN_SMEM > CS_SMEM ? TN_SMEM : CS_SMEM;
+  __shared__ __align__(16) float smem[SMEM];
+  int b = blockIdx.x;
+  if (a.db) {
+    if (b == 0) {
+      colsum_narrow_block(smem, a.G, a.C, a.B, a.C, a.db);
+      return;
+    }
+    --b;
+  }
+  if (b < a.tn_blocks) {
+    tn_narrow_block<NP>(b % a.tn_gx, b / a.tn_gx, smem, smem + TN_CHUNK * NP, a.H, a.K, a.G, a.C, a.dw_out, a.C,
+                        a.K, a.C, a.B, a.tn_kslice, a.tn_vec);
+    return;
+  }
+  b -= a.tn_blocks;
+  nt_smallk_block<NP>(b % a.nt_gx, b / a.nt_gx, smem, a.G, a.C, a.W, a.C, a.dH, a.K, a.B, a.K, a.C, a.nt_rows, a.mask,
+                      a.K, a.dH_pre);
 }
 
 const char* kernel_name(bool ta, bool tb, bool pipelined) {
@@ -1172,6 +1290,16 @@ size_t plan_workspace_floats(const GemmPlan& g, size_t M, size_t N, size_t batch
 
 namespace {
 
+// The grid of a narrow NT product: about two blocks per CU, each walking `rows` rows with
+// its columns of B in registers.
+void nt_grid(orca_hip_ctx* ctx, size_t M, size_t N, size_t& gx, size_t& gy, size_t& rows) {
+  gx = (N + NW_THREADS - 1) / NW_THREADS;
+  const size_t want = std::max<size_t>(1, (2 * (size_t)ctx->num_cus + gx - 1) / gx);
+  rows = std::max<size_t>((M + want - 1) / want, (M + 65534) / 65535);
+  gy = (M + rows - 1) / rows;
+  if (gx > 0x7fffffff) fail(ORCA_HIP_ERR_INTERNAL, "gemm: too many columns");
+}
+
 // A narrow product (plan.narrow): one launch, plus the slice reduction of a
 // sliced product and, when asked for, the exact column sum of B.
 template <int NP>
@@ -1183,12 +1311,8 @@ void launch_narrow(orca_hip_ctx* ctx, const GemmPlan& plan, size_t M, size_t N, 
                        A, (int64_t)lda, B, (int64_t)ldb, out, ldo, (int)M, (int)N, (int)K, plan.k_chunk,
                        plan.splits == 1 && epi.kind == ORCA_HIP_EPI_BIAS ? epi.bias : nullptr);
   } else if (plan.narrow == 2) {
-    // about two blocks per CU, each walking rows_per_block rows with its columns of B in registers
-    const size_t gx = (N + NW_THREADS - 1) / NW_THREADS;
-    const size_t want = std::max<size_t>(1, (2 * (size_t)ctx->num_cus + gx - 1) / gx);
-    size_t rows = std::max<size_t>((M + want - 1) / want, (M + 65534) / 65535);
-    const size_t gy = (M + rows - 1) / rows;
-    if (gx > 0x7fffffff) fail(ORCA_HIP_ERR_INTERNAL, "gemm: too many columns");
+    size_t gx, gy, rows;
+    nt_grid(ctx, M, N, gx, gy, rows);
     hipLaunchKernelGGL(gemm_nt_smallk_kernel<NP>, dim3((unsigned)gx, (unsigned)gy), dim3(NW_THREADS), 0, ctx->stream,
                        A, (int64_t)lda, B, (int64_t)ldb, out, ldo, (int)M, (int)N, (int)K, (int)rows,
                        epi.kind == ORCA_HIP_EPI_RELU_MASK || epi.kind == ORCA_HIP_EPI_RELU_MASK_PRE ? epi.mask : nullptr,
@@ -1243,6 +1367,66 @@ void gemm_narrow(orca_hip_ctx* ctx, const GemmPlan& plan, size_t M, size_t N, si
     if (plan.narrow == 2) fail(ORCA_HIP_ERR_INTERNAL, "gemm colsum epilogue requires row-major B");
     launch_colsum(ctx, B, K, N, ldb, epi.colsum);
   }
+}
+
+// dW = H^T G (+ db, the column sums of G) and dH = G W^T (+ ReLU mask) in one grid plus the
+// weight gradient's slice reduction, with the plans the separate products would take (so the
+// same sums).  False when either product would not run on the narrow kernels.
+bool narrow_linear_backward(orca_hip_ctx* ctx, const float* H, size_t B, size_t K, const float* G, size_t C,
+                            const float* W, const float* mask, float* dH, float* dH_pre, float* dW, float* db) {
+  const int nt_kind = mask ? (dH_pre ? ORCA_HIP_EPI_RELU_MASK_PRE : ORCA_HIP_EPI_RELU_MASK) : ORCA_HIP_EPI_NONE;
+  const GemmPlan tn = plan_gemm(ctx, true, false, K, C, B, H, K, 0, G, C, 0, 1, ORCA_HIP_EPI_NONE);
+  const GemmPlan nt = plan_gemm(ctx, false, true, B, K, C, G, C, 0, W, C, 0, 1, nt_kind);
+  if (tn.narrow != 3 || nt.narrow != 2 || B == 0 || K == 0 || C == 0) return false;
+  NarrowLinearBwArgs a{};
+  a.H = H;
+  a.G = G;
+  a.W = W;
+  a.mask = mask;
+  a.dH = dH;
+  a.dH_pre = mask ? dH_pre : nullptr;
+  a.db = db;
+  a.B = (int)B;
+  a.K = (int)K;
+  a.C = (int)C;
+  a.tn_gx = (int)((K + 255) / 256);
+  a.tn_blocks = a.tn_gx * tn.splits;
+  a.tn_kslice = tn.k_chunk;
+  a.tn_vec = aligned16(H) && K % 4 == 0;
+  size_t gx, gy, rows;
+  nt_grid(ctx, B, K, gx, gy, rows);
+  a.nt_gx = (int)gx;
+  a.nt_blocks = (int)(gx * gy);
+  a.nt_rows = (int)rows;
+  std::unique_ptr<Scratch> scratch;
+  a.dw_out = dW;
+  if (tn.splits > 1) {
+    scratch.reset(new Scratch(ctx, sizeof(float) * (size_t)tn.splits * K * C));
+    a.dw_out = scratch->as<float>();
+  }
+  const size_t blocks = (db ? 1 : 0) + (size_t)a.tn_blocks + (size_t)a.nt_blocks;
+  if (blocks > 0x7fffffff) fail(ORCA_HIP_ERR_INTERNAL, "narrow_linear_backward: too many blocks");
+  {
+    ProfScope ps(ctx, "narrow_linear_bw", 2.0 * 2.0 * (double)B * K * C,
+                 4.0 * (double)(B * K * (mask ? 2 : 1) + B * C + 2 * K * C + B * K * (dH_pre ? 2 : 1) +
+                                (tn.splits > 1 ? tn.splits * K * C : 0)));
+    const int np = narrow_pad(C);
+    if (np == 4)
+      hipLaunchKernelGGL(narrow_linear_bw_kernel<4>, dim3((unsigned)blocks), dim3(NW_THREADS), 0, ctx->stream, a);
+    else if (np == 8)
+      hipLaunchKernelGGL(narrow_linear_bw_kernel<8>, dim3((unsigned)blocks), dim3(NW_THREADS), 0, ctx->stream, a);
+    else
+      hipLaunchKernelGGL(narrow_linear_bw_kernel<16>, dim3((unsigned)blocks), dim3(NW_THREADS), 0, ctx->stream, a);
+    ORCA_HIP_CHECK(hipGetLastError());
+  }
+  if (tn.splits > 1) {
+    ProfScope ps(ctx, "gemm_narrow_reduce", 0.0, 4.0 * (double)K * C * (tn.splits + 1));
+    const unsigned g = grid_for(K * C, NW_THREADS, ctx->num_cus * 4);
+    hipLaunchKernelGGL(gemm_narrow_reduce_kernel, dim3(g), dim3(NW_THREADS), 0, ctx->stream, a.dw_out, tn.splits, dW,
+                       (int64_t)C, (int)K, (int)C, nullptr);
+    ORCA_HIP_CHECK(hipGetLastError());
+  }
+  return true;
 }
 
 }  // namespace
@@ -1568,6 +1752,36 @@ int orca_hip_matmul_colsum(orca_hip_ctx* ctx, const void* lhs, const void* rhs, 
     gemm(ctx, ta, false, M, N, K, static_cast<const float*>(lhs), ta ? M : K, 0, static_cast<const float*>(rhs), N,
          0, o, N, 0, 1, e);
     *out = o;
+  });
+}
+
+int orca_hip_narrow_linear_backward(orca_hip_ctx* ctx, const float* H, size_t B, size_t K, const float* G, size_t C,
+                                    const float* W, const float* mask, float* dH, float* dH_pre, float* dW, float* db,
+                                    orca_hip_event** done) {
+  return guard([&] {
+    bind(ctx);
+    if (done) *done = nullptr;
+    if (C < 1 || C > NW_MAX) fail(ORCA_HIP_ERR_INTERNAL, "narrow_linear_backward: needs 1 <= C <= 16");
+    if (!H || !G || !W || !dH || !dW) fail(ORCA_HIP_ERR_INTERNAL, "narrow_linear_backward: null operand");
+    check_extent(ctx, H, B * K * sizeof(float), "narrow_linear_backward (H)");
+    check_extent(ctx, G, B * C * sizeof(float), "narrow_linear_backward (G)");
+    check_extent(ctx, W, K * C * sizeof(float), "narrow_linear_backward (W)");
+    check_extent(ctx, mask, B * K * sizeof(float), "narrow_linear_backward (mask)");
+    check_extent(ctx, dH, B * K * sizeof(float), "narrow_linear_backward (dH)");
+    check_extent(ctx, dH_pre, B * K * sizeof(float), "narrow_linear_backward (dH_pre)");
+    check_extent(ctx, dW, K * C * sizeof(float), "narrow_linear_backward (dW)");
+    check_extent(ctx, db, C * sizeof(float), "narrow_linear_backward (db)");
+    if (!narrow_linear_backward(ctx, H, B, K, G, C, W, mask, dH, dH_pre, dW, db))
+      fail(ORCA_HIP_ERR_INTERNAL, "narrow_linear_backward: the products do not take the narrow kernels");
+    if (done) {
+      hipEvent_t ev = take_order_event(ctx);
+      const hipError_t er = hipEventRecord(ev, ctx->stream);
+      if (er != hipSuccess) {
+        ctx->event_pool.push_back(ev);
+        ORCA_HIP_CHECK(er);
+      }
+      *done = reinterpret_cast<orca_hip_event*>(ev);
+    }
   });
 }
 

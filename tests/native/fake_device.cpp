@@ -476,6 +476,44 @@ int orca_hip_gemm(orca_hip_ctx* ctx, int ta, int tb, size_t M, size_t N, size_t 
   });
 }
 
+// The three products one by one, as the library's grid computes them (the same sums).
+int orca_hip_narrow_linear_backward(orca_hip_ctx* ctx, const float* H, size_t B, size_t K, const float* G, size_t C,
+                                    const float* Wc, const float* mask, float* dH, float* dH_pre, float* dW, float* db,
+                                    orca_hip_event** done) {
+  return guard([&] {
+    if (done) *done = nullptr;
+    launch(ctx, "narrow_linear_backward");
+    R(ctx, H, 4 * B * K);
+    R(ctx, G, 4 * B * C);
+    R(ctx, Wc, 4 * K * C);
+    R(ctx, mask, 4 * B * K);
+    W(ctx, dH, 4 * B * K);
+    W(ctx, dH_pre, 4 * B * K);
+    W(ctx, dW, 4 * K * C);
+    W(ctx, db, 4 * C);
+    std::vector<float> w = product(H, true, K, G, false, C, K, C, B);
+    std::copy(w.begin(), w.end(), dW);
+    if (db) {
+      const size_t in[2] = {B, C}, cs[2] = {1, C};
+      check_oracle(orc_sum_to_shape(G, db, in, 2, cs, 2), "narrow_linear_backward colsum");
+    }
+    std::vector<float> h = product(G, false, C, Wc, true, C, B, K, C);
+    if (mask) {
+      if (dH_pre) std::copy(h.begin(), h.end(), dH_pre);
+      orc_relu_backward(h.data(), mask, dH, B * K);
+    } else {
+      std::copy(h.begin(), h.end(), dH);
+    }
+    logf("narrow_linear_backward " + std::to_string(B) + "x" + std::to_string(K) + "x" + std::to_string(C) +
+         (mask ? (dH_pre ? " mask pre" : " mask") : "") + (db ? " colsum" : ""));
+    if (done) {
+      *done = next_event();
+      event_at(ctx, *done);
+      logf("bound " + std::to_string(reinterpret_cast<uintptr_t>(*done)));
+    }
+  });
+}
+
 int orca_hip_transpose(orca_hip_ctx* ctx, const void* s, const size_t* shape, size_t rank, size_t d0, size_t d1,
                        int dtype, void** out) {
   return guard([&] {
