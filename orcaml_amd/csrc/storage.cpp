@@ -144,6 +144,10 @@ struct Node {
   Node* rhs = nullptr;
   size_t M = 0, K = 0, N = 0;
   bool lt = false, rt = false;
+  // A pending weight gradient X^T G whose bias gradient (a pending column sum of G) it computes
+  // (held); and, on that column sum, the product that will (weak).
+  Node* cs = nullptr;
+  Node* via = nullptr;
   uint64_t div = 1, mod = 1;  // kBcast
   // a one-element value known on the host (kConst, and after its upload)
   bool has_const = false;
@@ -346,6 +350,11 @@ void drop_operands(Node* x) {
   x->lhs = x->rhs = nullptr;
   unref(l);
   unref(r);
+  if (Node* c = x->cs) {
+    x->cs = nullptr;
+    c->via = nullptr;
+    unref(c);
+  }
 }
 
 void unwait(Node* colsum_node) {  // removes a pending column sum from its source's waiters
@@ -473,6 +482,11 @@ Buf* materialize(Backend* be, Node* x) {
       run_product(be, x);
       break;
     case Kind::kColsum: {
+      if (x->via) {  // the weight gradient that computes it as well
+        Ref v(ref(x->via));
+        materialize(be, v.get());
+        if (x->kind == Kind::kValue) break;
+      }
       Ref src(ref(x->lhs));
       Buf* sb = materialize(be, src.get());
       const size_t in_shape[2] = {x->M, x->N}, out_shape[2] = {1, x->N};
@@ -515,13 +529,73 @@ Ref plain(Backend* be, Node* x) {
   return Ref(value_node(be, x->n, own(be->ctx, out, 4 * std::max<size_t>(x->n, 1))));
 }
 
+// The pending weight gradient H^T G (with its bias gradient) beside the narrow product
+// p = G W^T (a classifier head's backward, K <= 16), or null.
+Node* narrow_sibling(Node* p) {
+  if (!p || p->kind != Kind::kProd || p->lt || !p->rt || p->K > 16) return nullptr;
+  Node* g = p->lhs;
+  for (Node* t : g->waiters) {
+    Node* x = t->kind == Kind::kColsum ? t->via : nullptr;
+    if (x && x->kind == Kind::kProd && x->cs == t && x->rhs == g && x->lt && !x->lhs->tshape.empty() &&
+        x->M == p->N && x->K == p->M && x->N == p->K)
+      return x;
+  }
+  return nullptr;
+}
+
+// p = G W^T (into c, through the ReLU mask of `mask_node` when given, with the unmasked
+// product into `pre` when given), its sibling weight gradient x = H^T G and x's bias gradient
+// from one grid (orca_hip_narrow_linear_backward: the same sums as the three run one by one).
+// Sets x and its bias gradient; the caller sets p and the epilogue's outputs.
+void run_narrow_backward(Backend* be, Node* p, Node* x, Node* mask_node, float* c, float* pre) {
+  Ref px(ref(p)), xx(ref(x)), tt(ref(x->cs));
+  Node* target = tt.get();
+  float* hp = dptr(be, x->lhs);  // H's own buffer (H^T is a view of it)
+  float* gp = dptr(be, p->lhs);
+  float* wp = dptr(be, p->rhs);  // W's own buffer (W^T is a view of it)
+  float* mp = mask_node ? dptr(be, mask_node) : nullptr;
+  const size_t B = p->M, K = p->N, C = p->K;
+  BufP dw = alloc_buf(be, K * C), db = alloc_buf(be, C);
+  const bool mark = marking(be);
+  orca_hip_event* ev = nullptr;
+  ck(orca_hip_narrow_linear_backward(be->ctx, hp, B, K, gp, C, wp, mp, c, pre, dw->ptr, db->ptr, mark ? &ev : nullptr));
+  set_value(target, db);
+  set_value(x, dw);
+  if (mark) {
+    MarkP m = record_mark(be, ev);
+    x->made = target->made = m;  // a weight gradient and its bias gradient
+  }
+}
+
 void run_product(Backend* be, Node* x) {
+  if (Node* w = narrow_sibling(x)) {  // a head's input gradient, with the weight gradient beside it
+    BufP c = alloc_buf(be, x->M * x->N);
+    run_narrow_backward(be, x, w, nullptr, c->ptr, nullptr);
+    set_value(x, c);
+    return;
+  }
   Ref lhs(ref(x->lhs)), rhs(ref(x->rhs));
   const size_t M = x->M, K = x->K, N = x->N;
   const bool lt = x->lt, rt = x->rt;
   float* a = dptr(be, lhs.get());
   float* b = dptr(be, rhs.get());
   const bool mark = marking(be) && (lt || rt);  // a backward product
+  if (x->cs) {  // a weight gradient run alone, with its bias gradient in the same launch
+    Ref tt(ref(x->cs));
+    Node* target = tt.get();
+    BufP cs = alloc_buf(be, N);
+    void* out = nullptr;
+    orca_hip_event* ev = nullptr;
+    ck(orca_hip_matmul_ev(be->ctx, a, b, M, K, N, ORCA_HIP_VIEW_TRANSPOSED, ORCA_HIP_VIEW_CONTIGUOUS, ORCA_HIP_F32,
+                          cs->ptr, &out, mark ? &ev : nullptr));
+    set_value(target, cs);
+    set_value(x, own(be->ctx, out, 4 * M * N));
+    if (mark) {
+      MarkP m = record_mark(be, ev);
+      x->made = target->made = m;
+    }
+    return;
+  }
   void* out = nullptr;
   orca_hip_event* ev = nullptr;
   ck(orca_hip_matmul_ev(be->ctx, a, b, M, K, N, lt ? ORCA_HIP_VIEW_TRANSPOSED : ORCA_HIP_VIEW_CONTIGUOUS,
@@ -717,11 +791,16 @@ bool fold_chain(Backend* be, Walk& w, const std::vector<int>& out_idx, bool shar
     pre = alloc_buf(be, M * N);
     e.pre = pre->ptr;
   }
-  const bool mark = marking(be) && (lt || rt);  // a backward product
-  orca_hip_event* ev = nullptr;
-  e.done = mark ? &ev : nullptr;
-  ck(orca_hip_gemm(be->ctx, lt ? 1 : 0, rt ? 1 : 0, M, N, K, lp, lt ? M : K, rp, rt ? K : N, c->ptr, N, &e));
-  if (mark) record_mark(be, ev);
+  Node* wg = mask_node ? narrow_sibling(prod) : nullptr;
+  if (wg) {  // a head's input gradient, with the weight gradient beside it
+    run_narrow_backward(be, prod, wg, mask_node, c->ptr, pre ? pre->ptr : nullptr);
+  } else {
+    const bool mark = marking(be) && (lt || rt);  // a backward product
+    orca_hip_event* ev = nullptr;
+    e.done = mark ? &ev : nullptr;
+    ck(orca_hip_gemm(be->ctx, lt ? 1 : 0, rt ? 1 : 0, M, N, K, lp, lt ? M : K, rp, rt ? K : N, c->ptr, N, &e));
+    if (mark) record_mark(be, ev);
+  }
   if (kind == ORCA_HIP_EPI_RELU_MASK_PRE) {
     set_value(prod, pre);  // the product itself, for its other holders
     pre.reset();
@@ -1342,6 +1421,17 @@ Node* deferred_colsum(Backend* be, Node* s, size_t rows, size_t cols) {
   return x;
 }
 
+// Whether a pending product G W^T ([rows, k] x [k, cols] with W^T a view) waits beside a
+// weight gradient of G.
+bool pending_input_gradient(Backend* be, Node* g, size_t rows, size_t k, size_t cols) {
+  for (auto& kv : be->pending) {
+    const Node* p = kv.second;
+    if (p->kind == Kind::kProd && p->lhs == g && p->rt && !p->lt && p->M == rows && p->K == k && p->N == cols)
+      return true;
+  }
+  return false;
+}
+
 // Removes and returns a still-pending column sum of s with `cols` columns (null if none).
 Node* take_colsum_waiter(Node* s, size_t cols) {
   for (size_t i = 0; i < s->waiters.size(); ++i) {
@@ -1513,6 +1603,24 @@ int orca_hip_trait_matmul(orca_hip_backend* be, orca_hip_storage* lhs, orca_hip_
       if (target) {
         Ref t(ref(target));
         const int lv = l->tshape.empty() ? ORCA_HIP_VIEW_CONTIGUOUS : ORCA_HIP_VIEW_TRANSPOSED;
+        // A classifier head's weight gradient (G with at most 16 columns) waits for the input
+        // gradient G W^T pending beside it: both, and this bias gradient, then run from one grid.
+        if (b->opt.fold && lv == ORCA_HIP_VIEW_TRANSPOSED && N <= 16 && M > 0 && K > 0 &&
+            pending_input_gradient(b, r, K, N, M)) {
+          Node* x = new_node(b, M * N);
+          x->kind = Kind::kProd;
+          x->lhs = ref(l);
+          x->rhs = ref(r);
+          x->M = M;
+          x->K = K;
+          x->N = N;
+          x->lt = true;
+          x->cs = ref(target);
+          target->via = x;
+          track_pending(b, x);
+          put(out, x);
+          return;
+        }
         float* lp = dptr(b, l);
         float* rp = dptr(b, r);
         BufP cs = alloc_buf(b, N);

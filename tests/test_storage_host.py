@@ -337,8 +337,9 @@ def test_composed_steps_equal_the_oracle_loop_bit_for_bit(ctx, kind, steps, swit
 def test_composed_step_folds_and_fuses(lib, ctx):
     """What one steady-state composed step launches: the Linear forwards as products with the
     bias (+ ReLU) epilogue, each ReluBackward as the next product's mask epilogue, the weight
-    gradients with their bias column sums in one launch, and no single elementwise op (only the
-    loss's row reductions run as kernels of their own)."""
+    gradients with their bias column sums in one launch, the head's weight, bias and masked
+    input gradients from one grid, and no single elementwise op (only the loss's row reductions
+    run as kernels of their own)."""
     from orcaml_amd.backend import HipBackend
 
     dims, B = (784, 48, 40, 10), 16
@@ -359,8 +360,10 @@ def test_composed_step_folds_and_fuses(lib, ctx):
     # forward: two hidden layers with bias + ReLU (pre-activation kept for ReluBackward) and the
     # head with its bias; backward: dX through the two ReLUs with the mask epilogue
     assert epis.count(_lib.EPI_BIAS_RELU_PRE) == 2 and epis.count(_lib.EPI_BIAS) == 1, gemms
-    assert epis.count(_lib.EPI_RELU_MASK) + epis.count(_lib.EPI_RELU_MASK_PRE) == 2, gemms
-    assert sum(line.startswith("matmul_colsum ") for line in log) == 3, log  # dW with its db
+    assert epis.count(_lib.EPI_RELU_MASK) + epis.count(_lib.EPI_RELU_MASK_PRE) == 1, gemms
+    # the hidden layers' dW with its db; the head's dW, db and masked dX from one grid
+    assert sum(line.startswith("matmul_colsum ") for line in log) == 2, log
+    assert sum(line.startswith("narrow_linear_backward 16x40x10 mask") for line in log) == 1, log
     reductions = ("op max_to_shape", "op sum_to_shape", "op max_to_shape_backward")
     assert not [line for line in log if line.startswith("op ") and line not in reductions], log
 
