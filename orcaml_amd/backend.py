@@ -32,6 +32,7 @@ from ._lib import (EW_ADD, EW_ADD_SCALAR, EW_COPY, EW_DIV, EW_DIV_BW_RHS, EW_EXP
 from .device import Context
 
 _VP = ctypes.c_void_p
+_byref = ctypes.byref
 _FLAG_PENDING, _FLAG_TRANSPOSED, _FLAG_MARKED, _FLAG_CONSTANT = 1, 2, 4, 8
 
 
@@ -94,12 +95,18 @@ class HipStorage:
 
     def __del__(self):
         be = self.be
-        if be is None or not self.h:
+        h = self.h
+        if be is None or not h:
             return
         try:
-            be._forget(self.h)
+            live = be._live
+            r = live.get(h)
+            if r is not None and r() is None:
+                del live[h]
             if be.ctx.handle:
-                be._release(self.h)
+                rc = be._release_fn(h)
+                if rc != _lib.OK:
+                    _lib.check(rc)
         except Exception:
             pass
         self.h = None
@@ -176,9 +183,23 @@ class HipBackend:
         return w
 
     def _out(self, name: str, *args) -> HipStorage:
+        fn = _lib._FNS.get(name)
+        if fn is None:
+            fn = _lib._FNS[name] = getattr(_lib.load(), name)
         out = _VP()
-        _lib.call(name, self.handle, *args, ctypes.byref(out))
-        return self._wrap(out.value)
+        rc = fn(self.handle, *args, _byref(out))
+        if rc != _lib.OK:
+            _lib.check(rc)
+        h = out.value
+        r = self._live.get(h)
+        if r is not None:
+            w = r()
+            if w is not None:
+                self._release(h)  # the call's reference: the wrapper holds one already
+                return w
+        w = HipStorage(self, h)
+        self._live[h] = weakref.ref(w)
+        return w
 
     # ---- trait methods (orca-tensor/src/backend.rs) ----
     def device(self) -> str:

@@ -880,18 +880,59 @@ bool side_flush(Backend* be, const Walk& w, const Program& prog, const std::vect
   }
   std::vector<float*> outs;
   for (auto& b : bufs) outs.push_back(b->ptr);
-  ck(orca_hip_use_side_stream(be->ctx, be->opt.side_bpc > 0 ? be->opt.side_bpc : -1));
-  be->on_side = true;
-  int rc = orca_hip_event_wait(be->ctx, wait->ev);
-  if (rc == ORCA_HIP_OK)
-    rc = orca_hip_ew_program(be->ctx, n, ins.data(), ins.size(), outs.data(), prog.oregs.data(), outs.size(),
-                             prog.instrs.data(), prog.instrs.size(), prog.n_regs);
+  // As the fused optimizer pass splits its second-stream part: side_frac of the elements on
+  // side_bpc blocks per CU beside the product after `wait`, the rest on the full grid after
+  // the mark before the latest (beside the last product, which leaves CUs idle).  Only a
+  // program without broadcast inputs splits (its element ranges are independent).
+  MarkP mid;
+  for (auto& m : be->recent)
+    if (m->seq > wait->seq && m != be->recent.back()) mid = m;
+  bool plain = true;
+  for (Node* lf : w.leaves) plain = plain && lf->kind != Kind::kBcast;
+  size_t n1 = n;
+  if (mid && plain && be->opt.side_frac < 1.0) {
+    n1 = (size_t)((double)n * std::max(0.0, be->opt.side_frac)) / 64 * 64;  // 256-byte aligned split
+    if (n1 == 0) n1 = n;
+  }
+  struct Part {
+    size_t from, cnt;
+    MarkP after;
+    int bpc;
+  };
+  const int bpc = be->opt.side_bpc > 0 ? be->opt.side_bpc : -1;
+  std::vector<Part> parts;
+  if (n1 < n) {
+    parts.push_back(Part{0, n1, wait, bpc});
+    parts.push_back(Part{n1, n - n1, mid, -1});
+  } else {
+    parts.push_back(Part{0, n, wait, bpc});
+  }
+  int rc = ORCA_HIP_OK;
   MarkP done;
-  if (rc == ORCA_HIP_OK) rc = guard_nodes([&] { done = new_mark(be); });
-  be->on_side = false;
-  const int rc2 = orca_hip_use_side_stream(be->ctx, 0);
+  for (size_t i = 0; i < parts.size() && rc == ORCA_HIP_OK; ++i) {
+    const Part& pt = parts[i];
+    rc = orca_hip_use_side_stream(be->ctx, pt.bpc);
+    if (rc != ORCA_HIP_OK) break;
+    be->on_side = true;
+    std::vector<orca_hip_ew_input> in = ins;
+    std::vector<float*> o = outs;
+    if (pt.cnt != n) {  // a range of the elements (every input is read elementwise)
+      for (auto& x : in) {
+        x.ptr += pt.from;
+        x.mod = pt.cnt;
+      }
+      for (auto& q : o) q += pt.from;
+    }
+    rc = orca_hip_event_wait(be->ctx, pt.after->ev);
+    if (rc == ORCA_HIP_OK)
+      rc = orca_hip_ew_program(be->ctx, pt.cnt, in.data(), in.size(), o.data(), prog.oregs.data(), o.size(),
+                               prog.instrs.data(), prog.instrs.size(), prog.n_regs);
+    if (rc == ORCA_HIP_OK && i + 1 == parts.size()) rc = guard_nodes([&] { done = new_mark(be); });
+    be->on_side = false;
+    const int rc2 = orca_hip_use_side_stream(be->ctx, 0);
+    if (rc == ORCA_HIP_OK) rc = rc2;
+  }
   ck(rc);
-  ck(rc2);
   for (Node* x : src) done->keep.push_back(ref(x));
   for (size_t i = 0; i < out_idx.size(); ++i) {
     Node* o = w.order[out_idx[i]];

@@ -393,9 +393,13 @@ def test_composed_update_runs_beside_the_backward_products(lib, ctx, kind):
             # the updates of layers 1 and 2 (flushed when the next step or the final read needs them)
             assert len(side) >= 4, log
             for i in side:
-                assert re.match(r"side [1-9]", log[i - 2]) and log[i - 1].startswith("wait ") and \
+                # a bounded part first (beside the product after its mark), or the rest on the full grid
+                assert re.match(r"side (-1|[1-9])", log[i - 2]) and log[i - 1].startswith("wait ") and \
                     log[i - 1].endswith(" side"), log[i - 3:i + 3]
-                assert log[i + 1].startswith("record ") and log[i + 1].endswith(" side") and log[i + 2] == "main"
+                if re.match(r"side [1-9]", log[i - 2]) and log[i + 1] == "main":
+                    assert log[i + 2] == "side -1", log[i:i + 4]  # its remainder follows
+                else:
+                    assert log[i + 1].startswith("record ") and log[i + 1].endswith(" side") and log[i + 2] == "main"
             # and whatever reads what they wrote waits for them: the stand-in's order check
             assert not [line for line in log if line.startswith("RACE")], log
         else:
