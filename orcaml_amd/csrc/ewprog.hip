@@ -639,7 +639,7 @@ int orca_hip_ew_program(orca_hip_ctx* ctx, size_t n, const orca_hip_ew_input* in
     }
     for (size_t k = 0; k < n_instrs; ++k) p.ins[k] = instrs[k];
     if (n == 0) return;
-    ProfScope ps(ctx, "ew_program", 0.0, 4.0 * (double)n * (n_inputs + n_outputs));
+    ProfScope ps(ctx, ctx->main ? "ew_program_overlapped" : "ew_program", 0.0, 4.0 * (double)n * (n_inputs + n_outputs));
     // On the side stream a bounded grid leaves room for a product running beside it (the
     // kernels stride over the grid, so any grid covers n).
     const unsigned cap = ctx->main && ctx->side_bpc > 0 ? (unsigned)(ctx->side_bpc * ctx->num_cus) : ctx->num_cus * 8;

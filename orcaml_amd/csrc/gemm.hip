@@ -1090,14 +1090,18 @@ __device__ __forceinline__ void colsum_narrow_block(float* st, const float* __re
   constexpr int PER_T = CS_ROWS * NW_MAX / NW_THREADS;
   const int t = threadIdx.x;
   float acc = 0.0f;
-  for (int r0 = 0; r0 < rows; r0 += CS_ROWS) {
-    const int cnt = min(CS_ROWS, rows - r0), total = cnt * C;
-    float v[PER_T];
+  float v[PER_T];
+  auto load = [&](int r0) {  // chunk r0's values, thread t taking elements t, t + 256, ...
+    const int total = min(CS_ROWS, rows - r0) * C;
 #pragma unroll
     for (int j = 0; j < PER_T; ++j) {
       const int e = t + j * NW_THREADS;
       v[j] = e < total ? G[(int64_t)(r0 + e / C) * ldg + e % C] : 0.0f;
     }
+  };
+  if (rows > 0) load(0);
+  for (int r0 = 0; r0 < rows; r0 += CS_ROWS) {
+    const int cnt = min(CS_ROWS, rows - r0), total = cnt * C;
     __syncthreads();  // the previous chunk has been added up
 #pragma unroll
     for (int j = 0; j < PER_T; ++j) {
@@ -1105,6 +1109,7 @@ __device__ __forceinline__ void colsum_narrow_block(float* st, const float* __re
       if (e < total) st[(e % C) * CS_LD + e / C] = v[j];
     }
     __syncthreads();
+    if (r0 + CS_ROWS < rows) load(r0 + CS_ROWS);  // the next chunk's loads in flight during the adds
     if (t < C) {
       const float* col = st + t * CS_LD;
       int r = 0;
