@@ -169,6 +169,8 @@ struct Node {
   bool side_made = false;
   // Written in place by an update after it was computed (never read on the second stream).
   bool in_place = false;
+  // Computed by arithmetic (a product, a loss): it holds no signaling NaN, so x * 1 is x.
+  bool quiet = false;
   bool in_pending = false;
   uint64_t pseq = 0;  // creation order among pending nodes
 
@@ -1147,6 +1149,9 @@ Node* fold_const(Backend* be, uint8_t op, Node* a, Node* b) {
   }
   Node* x = cb ? a : b;
   const float c = cb ? cb->cval : ca->cval;
+  // x * 1 is x bit for bit unless x is a signaling NaN (the multiply would quiet it), which
+  // arithmetic never leaves (denormals are kept, as the op's own kernel keeps them)
+  if (op == ORCA_HIP_EW_MUL && c == 1.0f && x->kind == Kind::kValue && x->quiet && x->tshape.empty()) return ref(x);
   std::vector<Ref> o;
   o.emplace_back(ref(x));
   return ew(be, op == ORCA_HIP_EW_ADD ? ORCA_HIP_EW_ADD_SCALAR : ORCA_HIP_EW_MUL_SCALAR, std::move(o), n, c);
@@ -2051,6 +2056,8 @@ int orca_hip_be_softmax_ce(orca_hip_backend* be, orca_hip_storage* logits, orca_
     if (want_grad) d = Ref(value_node(b, B * C, alloc_buf(b, B * C)));
     ck(orca_hip_softmax_ce(b->ctx, lp, B, C, op, nullptr, l->buf->ptr, want_grad ? d->buf->ptr : nullptr, nullptr,
                            nullptr));
+    l->quiet = true;
+    if (want_grad) d->quiet = true;
     *loss = S_(l.release());
     if (want_grad) *dlogits = S_(d.release());
   });

@@ -242,6 +242,23 @@ def test_identity_ops_give_back_the_same_storage(hb):
     assert hb.sum_to_shape(x, (3, 4), (3, 4)) is s
 
 
+def test_times_one_gives_back_a_computed_value(lib, hb):
+    """x * 1 is x bit for bit unless x is a signaling NaN: the gradient of a loss (computed
+    by arithmetic) times the backward seed is that gradient, with no program; an upload (which
+    may hold a signaling NaN) times one is still a multiply."""
+    logits = up(hb, np.random.default_rng(3).standard_normal((4, 5)).astype(np.float32))
+    onehot = up(hb, np.eye(5, dtype=np.float32)[[0, 2, 4, 1]])
+    _, dl = hb.softmax_ce(logits, onehot, 4, 5)
+    one = hb.from_f32_slice((1,), np.ones(1, np.float32))
+    fake_lib.clear(lib)
+    assert hb.mul(hb.expand(one, (1,), (4, 5)), dl, (4, 5)) is dl
+    up_x = up(hb, np.arange(20, dtype=np.float32))
+    y = hb.mul(hb.expand(one, (1,), (20,)), up_x, (20,))
+    assert y is not up_x
+    np.testing.assert_array_equal(down(hb, y), np.arange(20, dtype=np.float32))
+    assert len(programs(lib)) == 1  # the multiply of the upload, run when read
+
+
 def test_errors_carry_the_variant_fields(lib, hb, ctx):
     """Each failure maps to its OrcaError variant with the variant's fields
     (orca-core/src/error.rs:5-31), through orca_hip_last_error_info."""
