@@ -907,14 +907,17 @@ __device__ __forceinline__ void nt_smallk_block(int bx, int by, float* as, const
     if (n >= N) continue;
     float* dst = C + (int64_t)p0 * ldc + n;
     // Rows in groups of 16, the group's mask values loaded before its first row is
-    // computed (a load per row ahead of each store would chain the rows on memory).
-    for (int t0 = 0; t0 < cnt; t0 += NT_ROW_GROUP) {
-      float mk[NT_ROW_GROUP];
-      if (mask) {
+    // computed (a load per row ahead of each store would chain the rows on memory), and
+    // the next group's while this one is computed.
+    float mk[NT_ROW_GROUP], mk_next[NT_ROW_GROUP];
+    auto load_mask = [&](int t0, float (&m)[NT_ROW_GROUP]) {
 #pragma unroll
-        for (int j = 0; j < NT_ROW_GROUP; ++j)
-          mk[j] = t0 + j < cnt ? mask[(int64_t)(p0 + t0 + j) * ldmask + n] : 0.0f;
-      }
+      for (int j = 0; j < NT_ROW_GROUP; ++j)
+        m[j] = t0 + j < cnt ? mask[(int64_t)(p0 + t0 + j) * ldmask + n] : 0.0f;
+    };
+    if (mask) load_mask(0, mk);
+    for (int t0 = 0; t0 < cnt; t0 += NT_ROW_GROUP) {
+      if (mask && t0 + NT_ROW_GROUP < cnt) load_mask(t0 + NT_ROW_GROUP, mk_next);
 #pragma unroll
       for (int j = 0; j < NT_ROW_GROUP; ++j) {
         const int t = t0 + j;
@@ -932,6 +935,10 @@ __device__ __forceinline__ void nt_smallk_block(int bx, int by, float* as, const
         if (mask) c = mk[j] > 0.0f ? c : 0.0f;          // the ReLU-mask epilogue
         dst[(int64_t)t * ldc] = c;
       }
+      if (mask) {
+#pragma unroll
+        for (int j = 0; j < NT_ROW_GROUP; ++j) mk[j] = mk_next[j];
+      }
     }
   }
 }
@@ -948,31 +955,33 @@ __global__ void __launch_bounds__(NW_THREADS) gemm_nt_smallk_kernel(const float*
 }
 
 // C[M x N] = A^T B with A stored [K][M], B [K][N], N <= NP.  Block (x, y):
-// columns 256 x .. + 255 (4 per lane, a float4 of an A row when aligned) and
-// K slice y.  Per 64-row chunk the block stages B's rows in LDS (`bs`,
-// TN_CHUNK x NP floats) and wave w takes chunk rows 16 w .. 16 w + 15; the next
-// chunk's loads are in flight while a chunk is computed.  The lane's sums run in
-// k order, then the 4 waves are added in wave order: waves 1, 2 and 3 hand theirs
-// to wave 0 in turn through `red` (64 x (4 NP + 1) floats), and wave 0 stores.
-// With one slice the result is C, else part[slice][M][N] (ldo = N).
-template <int NP>
+// columns 64 COLS x .. + 64 COLS - 1 (COLS per lane: a float4 or float2 of an A
+// row when aligned) and K slice y.  Per 64-row chunk the block stages B's rows in
+// LDS (`bs`, TN_CHUNK x NP floats) and wave w takes chunk rows 16 w .. 16 w + 15;
+// with PIPE the next chunk's loads are in flight while a chunk is computed.  The
+// lane's sums run in k order, then the 4 waves are added in wave order: waves 1, 2
+// and 3 hand theirs to wave 0 in turn through `red` (64 x (COLS NP + 1) floats), and
+// wave 0 stores.  Each output's sums are the same for every COLS and PIPE.  With one
+// slice the result is C, else part[slice][M][N] (ldo = N).
+template <int NP, int COLS, bool PIPE>
 __device__ __forceinline__ void tn_narrow_block(int bx, int by, float* bs, float* red, const float* __restrict__ A,
                                                 int64_t lda, const float* __restrict__ B, int64_t ldb,
                                                 float* __restrict__ out, int64_t ldo, int M, int N, int K, int kslice,
                                                 int vec_a) {
-  constexpr int RED = 4 * NP + 1;
+  static_assert(COLS == 2 || COLS == 4, "two or four columns per lane");
+  constexpr int RED = COLS * NP + 1;
   constexpr int PER_WAVE = TN_CHUNK / 4;
   constexpr int PER_T = TN_CHUNK * NP / NW_THREADS;  // staged B values per thread
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int m0 = bx * 256 + 4 * lane;
+  const int m0 = bx * 64 * COLS + COLS * lane;
   const int k_beg = by * kslice, k_end = min(K, k_beg + kslice);
-  const bool vec = vec_a && m0 + 3 < M;
-  float acc[4][NP];
+  const bool vec = vec_a && m0 + COLS - 1 < M;
+  float acc[COLS][NP];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < COLS; ++i)
 #pragma unroll
     for (int n = 0; n < NP; ++n) acc[i][n] = 0.0f;
-  float bv[PER_T], a[PER_WAVE][4];
+  float bv[PER_T], a[PER_WAVE][COLS];
   auto load = [&](int k0) {
 #pragma unroll
     for (int i = 0; i < PER_T; ++i) {
@@ -984,26 +993,20 @@ __device__ __forceinline__ void tn_narrow_block(int bx, int by, float* bs, float
       const int k = k0 + PER_WAVE * w + r;
       const float* row = A + (int64_t)k * lda + m0;
       if (k < k_end && vec) {
-        const floatx4 v = *reinterpret_cast<const floatx4*>(row);
-        a[r][0] = v.x, a[r][1] = v.y, a[r][2] = v.z, a[r][3] = v.w;
+        if (COLS == 4) {
+          const floatx4 v = *reinterpret_cast<const floatx4*>(row);
+          a[r][0] = v.x, a[r][1] = v.y, a[r][COLS > 2 ? 2 : 0] = v.z, a[r][COLS > 3 ? 3 : 0] = v.w;
+        } else {
+          const float2 v = *reinterpret_cast<const float2*>(row);
+          a[r][0] = v.x, a[r][1] = v.y;
+        }
       } else {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) a[r][i] = k < k_end && m0 + i < M ? row[i] : 0.0f;
+        for (int i = 0; i < COLS; ++i) a[r][i] = k < k_end && m0 + i < M ? row[i] : 0.0f;
       }
     }
   };
-  if (k_beg < k_end) load(k_beg);
-  for (int k0 = k_beg; k0 < k_end; k0 += TN_CHUNK) {
-    __syncthreads();  // the previous chunk's B reads are done
-#pragma unroll
-    for (int i = 0; i < PER_T; ++i) bs[tid + i * NW_THREADS] = bv[i];
-    float ac[PER_WAVE][4];
-#pragma unroll
-    for (int r = 0; r < PER_WAVE; ++r)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) ac[r][i] = a[r][i];
-    __syncthreads();
-    if (k0 + TN_CHUNK < k_end) load(k0 + TN_CHUNK);
+  auto compute = [&](const float (&ac)[PER_WAVE][COLS]) {
 #pragma unroll
     for (int r = 0; r < PER_WAVE; ++r) {
       const float* brow = bs + (PER_WAVE * w + r) * NP;
@@ -1014,9 +1017,29 @@ __device__ __forceinline__ void tn_narrow_block(int bx, int by, float* bs, float
         b[4 * q] = v.x, b[4 * q + 1] = v.y, b[4 * q + 2] = v.z, b[4 * q + 3] = v.w;
       }
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+      for (int i = 0; i < COLS; ++i)
 #pragma unroll
         for (int n = 0; n < NP; ++n) acc[i][n] = fmaf(ac[r][i], b[n], acc[i][n]);
+    }
+  };
+  if (PIPE && k_beg < k_end) load(k_beg);
+  for (int k0 = k_beg; k0 < k_end; k0 += TN_CHUNK) {
+    if (!PIPE) load(k0);
+    __syncthreads();  // the previous chunk's B reads are done
+#pragma unroll
+    for (int i = 0; i < PER_T; ++i) bs[tid + i * NW_THREADS] = bv[i];
+    if (PIPE) {
+      float ac[PER_WAVE][COLS];
+#pragma unroll
+      for (int r = 0; r < PER_WAVE; ++r)
+#pragma unroll
+        for (int i = 0; i < COLS; ++i) ac[r][i] = a[r][i];
+      __syncthreads();
+      if (k0 + TN_CHUNK < k_end) load(k0 + TN_CHUNK);
+      compute(ac);
+    } else {
+      __syncthreads();
+      compute(a);
     }
   }
   float* mine = red + lane * RED;
@@ -1024,14 +1047,14 @@ __device__ __forceinline__ void tn_narrow_block(int bx, int by, float* bs, float
     __syncthreads();  // wave 0 has read the previous hand-over
     if (w == src) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+      for (int i = 0; i < COLS; ++i)
 #pragma unroll
         for (int n = 0; n < NP; ++n) mine[i * NP + n] = acc[i][n];
     }
     __syncthreads();
     if (w == 0) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+      for (int i = 0; i < COLS; ++i)
 #pragma unroll
         for (int n = 0; n < NP; ++n) acc[i][n] = acc[i][n] + mine[i * NP + n];
     }
@@ -1039,7 +1062,7 @@ __device__ __forceinline__ void tn_narrow_block(int bx, int by, float* bs, float
   if (w == 0) {
     float* o = out + (int64_t)by * M * N;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < COLS; ++i) {
       const int m = m0 + i;
       if (m < M) {
 #pragma unroll
@@ -1057,7 +1080,7 @@ __global__ void __launch_bounds__(NW_THREADS) gemm_tn_narrow_kernel(const float*
                                                                      int K, int kslice, int vec_a) {
   __shared__ __align__(16) float bs[TN_CHUNK * NP];
   __shared__ float red[64 * (4 * NP + 1)];
-  tn_narrow_block<NP>(blockIdx.x, blockIdx.y, bs, red, A, lda, B, ldb, out, ldo, M, N, K, kslice, vec_a);
+  tn_narrow_block<NP, 4, true>(blockIdx.x, blockIdx.y, bs, red, A, lda, B, ldb, out, ldo, M, N, K, kslice, vec_a);
 }
 
 // C[m][n] = sum over slices s (in order) of part[s][m][n] (+ bias[n] when given).
@@ -1149,8 +1172,8 @@ struct NarrowLinearBwArgs {
 };
 
 template <int NP>
-__global__ void __launch_bounds__(NW_THREADS) narrow_linear_bw_kernel(NarrowLinearBwArgs a) {
-  constexpr int TN_SMEM = TN_CHUNK * NP + 64 * (4 * NP + 1);
+__global__ void __launch_bounds__(NW_THREADS, 4) narrow_linear_bw_kernel(NarrowLinearBwArgs a) {
+  constexpr int TN_SMEM = TN_CHUNK * NP + 64 * (2 * NP + 1);
   constexpr int CS_SMEM = NW_MAX * CS_LD;
   constexpr int SMEM = TN_SMEM > CS_SMEM ? TN_SMEM : CS_SMEM;
   __shared__ __align__(16) float smem[SMEM];
@@ -1163,8 +1186,10 @@ __global__ void __launch_bounds__(NW_THREADS) narrow_linear_bw_kernel(NarrowLine
     --b;
   }
   if (b < a.tn_blocks) {
-    tn_narrow_block<NP>(b % a.tn_gx, b / a.tn_gx, smem, smem + TN_CHUNK * NP, a.H, a.K, a.G, a.C, a.dw_out, a.C,
-                        a.K, a.C, a.B, a.tn_kslice, a.tn_vec);
+    // two columns per lane and no prefetch: fewer registers, so the input-gradient blocks
+    // beside it keep their occupancy (the sums are those of the weight gradient's own kernel)
+    tn_narrow_block<NP, 2, false>(b % a.tn_gx, b / a.tn_gx, smem, smem + TN_CHUNK * NP, a.H, a.K, a.G, a.C,
+                                  a.dw_out, a.C, a.K, a.C, a.B, a.tn_kslice, a.tn_vec);
     return;
   }
   b -= a.tn_blocks;
@@ -1394,10 +1419,10 @@ bool narrow_linear_backward(orca_hip_ctx* ctx, const float* H, size_t B, size_t 
   a.B = (int)B;
   a.K = (int)K;
   a.C = (int)C;
-  a.tn_gx = (int)((K + 255) / 256);
+  a.tn_gx = (int)((K + 127) / 128);  // 128 columns per block (two per lane)
   a.tn_blocks = a.tn_gx * tn.splits;
   a.tn_kslice = tn.k_chunk;
-  a.tn_vec = aligned16(H) && K % 4 == 0;
+  a.tn_vec = (reinterpret_cast<uintptr_t>(H) & 7) == 0 && K % 2 == 0;
   size_t gx, gy, rows;
   nt_grid(ctx, B, K, gx, gy, rows);
   a.nt_gx = (int)gx;
