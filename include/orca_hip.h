@@ -260,8 +260,9 @@ int orca_hip_has_nan_or_inf(orca_hip_ctx* ctx, const void* s, size_t n, int dtyp
  *   - products left pending; when their first use is a GEMM epilogue (Linear's bias + ReLU,
  *     ReluBackward's mask) they run with it (orca_hip_gemm);
  *   - the bias gradient sum_to_shape([R, N] -> [1, N]) left pending until the weight
- *     gradient matmul of the same storage computes it (orca_hip_matmul_colsum), and each
- *     storage's identity sum_to_shape computed once;
+ *     gradient matmul of the same storage computes it (orca_hip_matmul_colsum), each
+ *     storage's identity sum_to_shape computed once, and a row sum or maximum onto [R, 1]
+ *     of a pending chain run in the chain's launch (orca_hip_ew_program_rows);
  *   - one-element uploads (the backward seed, scalars) kept on the host and applied as
  *     instruction scalars;
  *   - with the fused optimizer passes, the events that let part of an update run on the
@@ -277,7 +278,7 @@ typedef struct orca_hip_storage orca_hip_storage;
 
 typedef struct {
   int lazy;         /* elementwise ops and products pending (fused at first use); 0: every op runs at once */
-  int deferred;     /* the identity memo and the pending bias column sums */
+  int deferred;     /* the identity memo, the pending bias column sums and the row reductions with their chain */
   int fold;         /* pending products run with their epilogue chain (needs lazy) */
   int overlap;      /* fused optimizer passes may run part of the update on the second stream */
   double side_frac; /* share of that part run beside the product after its gradients (0..1) */
@@ -514,6 +515,17 @@ typedef struct {
 int orca_hip_ew_program(orca_hip_ctx* ctx, size_t n, const orca_hip_ew_input* inputs, size_t n_inputs,
                         float* const* outputs, const uint8_t* out_regs, size_t n_outputs,
                         const orca_hip_ew_instr* instrs, size_t n_instrs, size_t n_regs);
+/* orca_hip_ew_program over a [rows, cols] block (n = rows * cols), and in the same launch
+ * reduced[r] = the sum (reduce_max = 0) or the maximum (reduce_max = 1) over row r of
+ * register red_reg: Backend::sum_to_shape / max_to_shape of the program's value to
+ * [rows, 1] (backend.rs:112-133, 299-314) with their bits -- a sum from +0 in ascending
+ * column order, a maximum from -FLT_MAX that a value replaces only when greater.
+ * 1 <= cols <= 64.  No reference counterpart: it runs a chain and the row reduction after
+ * it (a loss's softmax) as one launch. */
+int orca_hip_ew_program_rows(orca_hip_ctx* ctx, size_t rows, size_t cols, const orca_hip_ew_input* inputs,
+                             size_t n_inputs, float* const* outputs, const uint8_t* out_regs, size_t n_outputs,
+                             const orca_hip_ew_instr* instrs, size_t n_instrs, size_t n_regs, int red_reg,
+                             int reduce_max, float* reduced);
 
 /* Run-time compilation of fused programs.  No counterpart in the reference:
  * controls for callers that want to choose or observe how programs run.  A

@@ -236,6 +236,7 @@ SIGNATURES = {
     "orca_hip_head_forward_ce": [_P, _P, _SZ, _SZ, _P, _P, _SZ, _P, _P, _P, _P, _P, _P, _P],
     "orca_hip_head_backward": [_P, _P, _SZ, _SZ, _P, _SZ, _P, _I, _P, _P, _P],
     "orca_hip_ew_program": [_P, _SZ, _P, _SZ, _P, _P, _SZ, _P, _SZ, _SZ],
+    "orca_hip_ew_program_rows": [_P, _SZ, _SZ, _P, _SZ, _P, _P, _SZ, _P, _SZ, _SZ, _I, _I, _P],
     "orca_hip_ew_set_jit": [_P, ctypes.c_int],
     "orca_hip_adamw_multi": [_P, _P, _SZ, ctypes.c_double, ctypes.c_double, ctypes.c_double, ctypes.c_double,
                              ctypes.c_double, ctypes.c_int64],

@@ -11,6 +11,7 @@
 #include <hip/hiprtc.h>
 
 #include <algorithm>
+#include <cfloat>
 #include <cstdint>
 #include <cstdio>
 #include <cstring>
@@ -203,6 +204,46 @@ __global__ void __launch_bounds__(kEwBlock) ew_program_vec_kernel(EwProgram p, s
 __global__ void __launch_bounds__(kEwBlock) ew_program_scalar_kernel(EwProgram p, size_t n) {
   const size_t stride = (size_t)gridDim.x * kEwBlock;
   for (size_t i = (size_t)blockIdx.x * kEwBlock + threadIdx.x; i < n; i += stride) ew_run<RegFile1>(p, i);
+}
+
+// The program over a [rows, cols] block and the row reduction of one register: each block
+// takes rows_per_block whole rows, one thread per element (coalesced as the plain kernel);
+// the reduced register's values go through LDS and thread r of the block combines its
+// row's values in column order as sum_to_shape's and max_to_shape's loops do (a sum from
+// +0, a maximum from -FLT_MAX that a value replaces only when greater), so reduced[r] has
+// the bits of that reduction of the program's value.
+template <bool IS_MAX>
+__global__ void __launch_bounds__(kEwBlock) ew_program_rows_kernel(EwProgram p, size_t rows, uint32_t cols,
+                                                                    uint32_t rows_per_block, uint32_t red_reg,
+                                                                    float* __restrict__ reduced) {
+  __shared__ float vals[kEwBlock];
+  const size_t r0 = (size_t)blockIdx.x * rows_per_block;
+  const uint32_t nr = rows - r0 < rows_per_block ? (uint32_t)(rows - r0) : rows_per_block;
+  const uint32_t t = threadIdx.x;
+  if (t < nr * cols) {
+    const size_t e = r0 * cols + t;
+    RegFile1 rf;
+    for (uint32_t i = 0; i < p.n_in; ++i) rf.set(i, ew_input(p, i, e));
+    for (uint32_t k = 0; k < p.n_ops; ++k) {
+      const orca_hip_ew_instr I = p.ins[k];
+      rf.set(I.dst, ew_apply<float>(I, rf.get(I.a), rf.get(I.b), rf.get(I.c)));
+    }
+    for (uint32_t o = 0; o < p.n_out; ++o) p.out[o][e] = rf.get(p.out_reg[o]);
+    vals[t] = rf.get(red_reg);
+  }
+  __syncthreads();
+  if (t < nr) {
+    float acc = IS_MAX ? -FLT_MAX : 0.0f;
+    for (uint32_t c = 0; c < cols; ++c) {
+      const float v = vals[t * cols + c];
+      if (IS_MAX) {
+        if (v > acc) acc = v;
+      } else {
+        acc = acc + v;
+      }
+    }
+    reduced[r0 + t] = acc;
+  }
 }
 
 inline bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; }
@@ -600,6 +641,66 @@ hipFunction_t jit_kernel(orca_hip_ctx* ctx, const EwProgram& p, bool vec) {
 using namespace orca_hip;
 
 extern "C" {
+
+int orca_hip_ew_program_rows(orca_hip_ctx* ctx, size_t rows, size_t cols, const orca_hip_ew_input* inputs,
+                             size_t n_inputs, float* const* outputs, const uint8_t* out_regs, size_t n_outputs,
+                             const orca_hip_ew_instr* instrs, size_t n_instrs, size_t n_regs, int red_reg,
+                             int reduce_max, float* reduced) {
+  return guard([&] {
+    bind(ctx);
+    check_program(n_inputs, out_regs, n_outputs, instrs, n_instrs, n_regs);
+    if ((n_inputs && !inputs) || !outputs) fail(ORCA_HIP_ERR_INTERNAL, "ew_program_rows: null program array");
+    if (cols == 0 || cols > 64) fail(ORCA_HIP_ERR_INTERNAL, "ew_program_rows: needs 1 <= cols <= 64");
+    if (rows > ((size_t)1 << 31) / cols) fail(ORCA_HIP_ERR_INTERNAL, "ew_program_rows: too many elements");
+    if (red_reg < 0 || (size_t)red_reg >= n_regs) fail(ORCA_HIP_ERR_INTERNAL, "ew_program_rows: bad register");
+    bool readable = red_reg < (int)n_inputs;
+    for (size_t k = 0; k < n_instrs; ++k) readable = readable || instrs[k].dst == red_reg;
+    if (!readable) fail(ORCA_HIP_ERR_INTERNAL, "ew_program_rows: the reduced register is never written");
+    const size_t n = rows * cols;
+    check_extent(ctx, reduced, rows * sizeof(float), "ew_program_rows (reduced)");
+    if (rows && !reduced) fail(ORCA_HIP_ERR_INTERNAL, "ew_program_rows: null reduced output");
+    EwProgram p{};
+    p.n_in = (uint32_t)n_inputs;
+    p.n_out = (uint32_t)n_outputs;
+    p.n_ops = (uint32_t)n_instrs;
+    for (size_t i = 0; i < n_inputs; ++i) {
+      const orca_hip_ew_input& in = inputs[i];
+      if (n && (!in.ptr || in.div == 0 || in.mod == 0)) fail(ORCA_HIP_ERR_INTERNAL, "ew_program_rows: invalid input");
+      const bool plain = in.div == 1 && in.mod == n;
+      if (n && !plain && in.mod > n) fail(ORCA_HIP_ERR_INTERNAL, "ew_program_rows: broadcast input larger than the output");
+      check_extent(ctx, in.ptr, (plain ? n : in.mod) * sizeof(float), "ew_program_rows (input)");
+      p.in[i] = in.ptr;
+      p.div[i] = in.div;
+      p.mod[i] = in.mod;
+      p.mode[i] = n ? input_mode(n, in.div, in.mod) : (uint8_t)kPlain;
+      if (p.mode[i] == kRow4 || p.mode[i] == kGroup4) p.mode[i] = kIndexed;  // one element at a time here
+      if (p.mode[i] == kIndexed) {
+        p.div_magic[i] = magic_for(in.div);
+        p.mod_magic[i] = magic_for(in.mod);
+      }
+    }
+    for (size_t o = 0; o < n_outputs; ++o) {
+      if (!outputs[o] && n) fail(ORCA_HIP_ERR_INTERNAL, "ew_program_rows: null output");
+      check_extent(ctx, outputs[o], n * sizeof(float), "ew_program_rows (output)");
+      p.out[o] = outputs[o];
+      p.out_reg[o] = out_regs[o];
+    }
+    for (size_t k = 0; k < n_instrs; ++k) p.ins[k] = instrs[k];
+    if (rows == 0) return;
+    ProfScope ps(ctx, ctx->main ? "ew_program_rows_overlapped" : "ew_program_rows", 0.0,
+                 4.0 * (double)n * (n_inputs + n_outputs) + 4.0 * rows);
+    // whole rows per block: rows_per_block * cols <= kEwBlock elements
+    const uint32_t rpb = (uint32_t)(kEwBlock / cols);
+    const unsigned g = (unsigned)((rows + rpb - 1) / rpb);
+    if (reduce_max)
+      hipLaunchKernelGGL(ew_program_rows_kernel<true>, dim3(g), dim3(kEwBlock), 0, ctx->stream, p, rows,
+                         (uint32_t)cols, rpb, (uint32_t)red_reg, reduced);
+    else
+      hipLaunchKernelGGL(ew_program_rows_kernel<false>, dim3(g), dim3(kEwBlock), 0, ctx->stream, p, rows,
+                         (uint32_t)cols, rpb, (uint32_t)red_reg, reduced);
+    ORCA_HIP_CHECK(hipGetLastError());
+  });
+}
 
 int orca_hip_ew_program(orca_hip_ctx* ctx, size_t n, const orca_hip_ew_input* inputs, size_t n_inputs,
                         float* const* outputs, const uint8_t* out_regs, size_t n_outputs,

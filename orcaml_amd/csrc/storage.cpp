@@ -1008,6 +1008,67 @@ void flush(Backend* be, Node* root) {
   for (size_t i = 0; i < out_idx.size(); ++i) set_value(w.order[out_idx[i]], bufs[i]);
 }
 
+// Runs root's pending chain as flush does, together with the row reduction
+// sum_to_shape / max_to_shape([rows, cols] -> [rows, 1]) of its value, in one launch
+// (orca_hip_ew_program_rows, whose rows have the bits of the one-by-one reduction).  Null,
+// with nothing run, when the chain does not qualify: a chain headed by a pending product
+// (left to the product's epilogue), rows wider than the launch takes, a program past the
+// interpreter's limits, or launches going to the second stream.
+Node* chain_rows(Backend* be, Node* root, size_t rows, size_t cols, bool is_max) {
+  if (root->kind != Kind::kEw || be->on_side || cols == 0 || cols > 64 || rows * cols != root->n ||
+      rows > ((size_t)1 << 31) / cols)
+    return nullptr;
+  Walk w;
+  w.visit(root);
+  if (be->opt.fold && w.leaves[0]->kind == Kind::kProd) return nullptr;
+  std::vector<int> out_idx;
+  const int n_ops = (int)w.order.size();
+  for (int k = 0; k + 1 < n_ops; ++k) {
+    Node* x = w.order[k];
+    if (x->rc.load(std::memory_order_relaxed) > w.inner[x]) out_idx.push_back(k);
+  }
+  out_idx.push_back(n_ops - 1);  // the root
+  std::string key(reinterpret_cast<const char*>(w.sig.data()), w.sig.size() * sizeof(int));
+  key.append("|");
+  key.append(reinterpret_cast<const char*>(out_idx.data()), out_idx.size() * sizeof(int));
+  key.append(std::to_string(w.leaves.size()));
+  auto it = be->programs.find(key);
+  if (it == be->programs.end()) it = be->programs.emplace(key, compile(w, out_idx)).first;
+  Program& prog = it->second;
+  if (!prog.ok) return nullptr;
+  std::vector<Ref> hold;
+  hold.reserve(w.order.size() + w.leaves.size());
+  for (Node* x : w.order) hold.emplace_back(ref(x));
+  for (Node* x : w.leaves) hold.emplace_back(ref(x));
+  for (int k : prog.scalar_at) prog.instrs[k].scalar = w.scalars[k];
+  const size_t n = root->n;
+  std::vector<orca_hip_ew_input> ins(std::max<size_t>(1, w.leaves.size()));
+  for (size_t i = 0; i < w.leaves.size(); ++i) {
+    Node* lf = w.leaves[i];
+    if (lf->kind == Kind::kBcast) {
+      ins[i].ptr = dptr(be, lf->lhs);
+      ins[i].div = lf->div;
+      ins[i].mod = lf->mod;
+    } else {
+      ins[i].ptr = dptr(be, lf);
+      ins[i].div = 1;
+      ins[i].mod = n;
+    }
+  }
+  std::vector<BufP> bufs;
+  std::vector<float*> outs;
+  for (size_t i = 0; i < out_idx.size(); ++i) {
+    bufs.push_back(alloc_buf(be, n));
+    outs.push_back(bufs.back()->ptr);
+  }
+  BufP red = alloc_buf(be, rows);
+  ck(orca_hip_ew_program_rows(be->ctx, rows, cols, ins.data(), w.leaves.size(), outs.data(), prog.oregs.data(),
+                              outs.size(), prog.instrs.data(), prog.instrs.size(), prog.n_regs, prog.oregs.back(),
+                              is_max ? 1 : 0, red->ptr));
+  for (size_t i = 0; i < out_idx.size(); ++i) set_value(w.order[out_idx[i]], bufs[i]);
+  return value_node(be, rows, std::move(red));
+}
+
 // ---- creating pending nodes
 bool is_lazy_f32(Backend* be, int dtype) { return be->opt.lazy && dtype == ORCA_HIP_F32; }
 
@@ -1861,6 +1922,9 @@ int orca_hip_trait_sum_to_shape(orca_hip_backend* be, orca_hip_storage* s, const
       const bool row = in_rank == 2 && ((out_rank == 2 && out_shape[0] == 1 && out_shape[1] == in_shape[1]) ||
                                         (out_rank == 1 && out_shape[0] == in_shape[1]));
       if (row) return put(out, deferred_colsum(b, x, in_shape[0], in_shape[1]));
+      const bool per_row = in_rank == 2 && out_rank == 2 && out_shape[0] == in_shape[0] && out_shape[1] == 1;
+      if (per_row && b->opt.lazy)
+        if (Node* r = chain_rows(b, x, in_shape[0], in_shape[1], false)) return put(out, r);
     }
     put(out, reshape_like(b, orca_hip_sum_to_shape, x, in_shape, in_rank, out_shape, out_rank, dtype));
   });
@@ -2019,6 +2083,9 @@ int orca_hip_trait_max_to_shape(orca_hip_backend* be, orca_hip_storage* s, const
       o.emplace_back(ref(x));
       return put(out, ew(b, ORCA_HIP_EW_MAX_VISIT, std::move(o), x->n));
     }
+    const bool per_row = in_rank == 2 && out_rank == 2 && out_shape[0] == in_shape[0] && out_shape[1] == 1;
+    if (per_row && is_lazy_f32(b, dtype) && b->opt.deferred && x->tshape.empty())
+      if (Node* r = chain_rows(b, x, in_shape[0], in_shape[1], true)) return put(out, r);
     put(out, reshape_like(b, orca_hip_max_to_shape, x, in_shape, in_rank, out_shape, out_rank, dtype));
   });
 }

@@ -633,74 +633,110 @@ int orca_hip_max_to_shape_backward(orca_hip_ctx* ctx, const void* g, const void*
 }
 
 // ---- fused programs: each instruction is the op's own array pass
+// The interpreter: the registers after the program ran over n elements.
+std::vector<std::vector<float>> fake_program(orca_hip_ctx* ctx, size_t n, const orca_hip_ew_input* inputs,
+                                             size_t n_inputs, size_t n_outputs, const orca_hip_ew_instr* instrs,
+                                             size_t n_instrs, size_t n_regs) {
+  if (n_inputs > ORCA_HIP_EW_MAX_INPUTS || n_outputs > ORCA_HIP_EW_MAX_OUTPUTS || n_instrs > ORCA_HIP_EW_MAX_OPS ||
+      n_regs > ORCA_HIP_EW_MAX_REGS || n_inputs > n_regs)
+    fail(ORCA_HIP_ERR_INTERNAL, "program exceeds the interpreter's limits");
+  std::vector<std::vector<float>> reg(n_regs, std::vector<float>(n));
+  for (size_t i = 0; i < n_inputs; ++i) R(ctx, inputs[i].ptr, 4 * std::min<uint64_t>(inputs[i].mod, n ? n : 1));
+  for (size_t i = 0; i < n_inputs; ++i) {
+    const orca_hip_ew_input& in = inputs[i];
+    if (!in.mod || !in.div) fail(ORCA_HIP_ERR_INTERNAL, "bad input map");
+    check_extent(ctx, in.ptr, 4 * std::min<uint64_t>(in.mod, n ? n : 1), "ew_program input");
+    for (size_t e = 0; e < n; ++e) reg[i][e] = in.ptr[(e / in.div) % in.mod];
+  }
+  std::vector<float> tmp(n);
+  for (size_t k = 0; k < n_instrs; ++k) {
+    const orca_hip_ew_instr& I = instrs[k];
+    if (I.dst >= n_regs || I.a >= n_regs || I.b >= n_regs || I.c >= n_regs)
+      fail(ORCA_HIP_ERR_INTERNAL, "register out of range");
+    const float *a = reg[I.a].data(), *b = reg[I.b].data(), *c = reg[I.c].data();
+    float* d = tmp.data();
+    switch (I.op) {
+      case ORCA_HIP_EW_ADD: orc_add(a, b, d, n); break;
+      case ORCA_HIP_EW_SUB: orc_sub(a, b, d, n); break;
+      case ORCA_HIP_EW_MUL: orc_mul(a, b, d, n); break;
+      case ORCA_HIP_EW_DIV: orc_div(a, b, d, n); break;
+      case ORCA_HIP_EW_MUL_SCALAR: orc_mul_scalar(a, I.scalar, d, n); break;
+      case ORCA_HIP_EW_RELU: orc_relu(a, d, n); break;
+      case ORCA_HIP_EW_RELU_BW: orc_relu_backward(a, b, d, n); break;
+      case ORCA_HIP_EW_EXP: orc_exp(a, d, n); break;
+      case ORCA_HIP_EW_LOG: orc_log(a, d, n); break;
+      case ORCA_HIP_EW_SQRT: orc_sqrt(a, d, n); break;
+      case ORCA_HIP_EW_SIGMOID: orc_sigmoid(a, d, n); break;
+      case ORCA_HIP_EW_EXP_BW: orc_exp_backward(a, b, d, n); break;
+      case ORCA_HIP_EW_LOG_BW: orc_log_backward(a, b, d, n); break;
+      case ORCA_HIP_EW_SQRT_BW: orc_sqrt_backward(a, b, d, n); break;
+      case ORCA_HIP_EW_SIGMOID_BW: orc_sigmoid_backward(a, b, d, n); break;
+      case ORCA_HIP_EW_DIV_BW_RHS: orc_div_backward_rhs(a, b, c, d, n); break;
+      case ORCA_HIP_EW_SUM_VISIT: {
+        const size_t dims[1] = {n};
+        check_oracle(orc_sum_to_shape(a, d, dims, 1, dims, 1), "sum visit");
+        break;
+      }
+      case ORCA_HIP_EW_MAX_VISIT: {
+        const size_t dims[1] = {n};
+        check_oracle(orc_max_to_shape(a, d, dims, 1, dims, 1), "max visit");
+        break;
+      }
+      case ORCA_HIP_EW_COPY: std::copy(a, a + n, d); break;
+      case ORCA_HIP_EW_ADD_SCALAR: {
+        std::vector<float> sc(n, I.scalar);
+        orc_add(a, sc.data(), d, n);
+        break;
+      }
+      default: fail(ORCA_HIP_ERR_INTERNAL, "unknown opcode");
+    }
+    reg[I.dst].swap(tmp);
+  }
+  return reg;
+}
+
+void fake_outputs(orca_hip_ctx* ctx, size_t n, const std::vector<std::vector<float>>& reg, float* const* outputs,
+                  const uint8_t* out_regs, size_t n_outputs) {
+  for (size_t o = 0; o < n_outputs; ++o) {
+    if (out_regs[o] >= reg.size()) fail(ORCA_HIP_ERR_INTERNAL, "output register out of range");
+    check_extent(ctx, outputs[o], 4 * n, "ew_program output");
+    W(ctx, outputs[o], 4 * n);
+    std::copy(reg[out_regs[o]].begin(), reg[out_regs[o]].end(), outputs[o]);
+  }
+}
+
 int orca_hip_ew_program(orca_hip_ctx* ctx, size_t n, const orca_hip_ew_input* inputs, size_t n_inputs,
                         float* const* outputs, const uint8_t* out_regs, size_t n_outputs,
                         const orca_hip_ew_instr* instrs, size_t n_instrs, size_t n_regs) {
   return guard([&] {
-    if (n_inputs > ORCA_HIP_EW_MAX_INPUTS || n_outputs > ORCA_HIP_EW_MAX_OUTPUTS || n_instrs > ORCA_HIP_EW_MAX_OPS ||
-        n_regs > ORCA_HIP_EW_MAX_REGS || n_inputs > n_regs)
-      fail(ORCA_HIP_ERR_INTERNAL, "program exceeds the interpreter's limits");
-    std::vector<std::vector<float>> reg(n_regs, std::vector<float>(n));
     launch(ctx, "program");
-    for (size_t i = 0; i < n_inputs; ++i) R(ctx, inputs[i].ptr, 4 * std::min<uint64_t>(inputs[i].mod, n ? n : 1));
-    for (size_t o = 0; o < n_outputs; ++o) W(ctx, outputs[o], 4 * n);
-    for (size_t i = 0; i < n_inputs; ++i) {
-      const orca_hip_ew_input& in = inputs[i];
-      if (!in.mod || !in.div) fail(ORCA_HIP_ERR_INTERNAL, "bad input map");
-      check_extent(ctx, in.ptr, 4 * std::min<uint64_t>(in.mod, n ? n : 1), "ew_program input");
-      for (size_t e = 0; e < n; ++e) reg[i][e] = in.ptr[(e / in.div) % in.mod];
-    }
-    std::vector<float> tmp(n);
-    for (size_t k = 0; k < n_instrs; ++k) {
-      const orca_hip_ew_instr& I = instrs[k];
-      if (I.dst >= n_regs || I.a >= n_regs || I.b >= n_regs || I.c >= n_regs)
-        fail(ORCA_HIP_ERR_INTERNAL, "register out of range");
-      const float *a = reg[I.a].data(), *b = reg[I.b].data(), *c = reg[I.c].data();
-      float* d = tmp.data();
-      switch (I.op) {
-        case ORCA_HIP_EW_ADD: orc_add(a, b, d, n); break;
-        case ORCA_HIP_EW_SUB: orc_sub(a, b, d, n); break;
-        case ORCA_HIP_EW_MUL: orc_mul(a, b, d, n); break;
-        case ORCA_HIP_EW_DIV: orc_div(a, b, d, n); break;
-        case ORCA_HIP_EW_MUL_SCALAR: orc_mul_scalar(a, I.scalar, d, n); break;
-        case ORCA_HIP_EW_RELU: orc_relu(a, d, n); break;
-        case ORCA_HIP_EW_RELU_BW: orc_relu_backward(a, b, d, n); break;
-        case ORCA_HIP_EW_EXP: orc_exp(a, d, n); break;
-        case ORCA_HIP_EW_LOG: orc_log(a, d, n); break;
-        case ORCA_HIP_EW_SQRT: orc_sqrt(a, d, n); break;
-        case ORCA_HIP_EW_SIGMOID: orc_sigmoid(a, d, n); break;
-        case ORCA_HIP_EW_EXP_BW: orc_exp_backward(a, b, d, n); break;
-        case ORCA_HIP_EW_LOG_BW: orc_log_backward(a, b, d, n); break;
-        case ORCA_HIP_EW_SQRT_BW: orc_sqrt_backward(a, b, d, n); break;
-        case ORCA_HIP_EW_SIGMOID_BW: orc_sigmoid_backward(a, b, d, n); break;
-        case ORCA_HIP_EW_DIV_BW_RHS: orc_div_backward_rhs(a, b, c, d, n); break;
-        case ORCA_HIP_EW_SUM_VISIT: {
-          const size_t dims[1] = {n};
-          check_oracle(orc_sum_to_shape(a, d, dims, 1, dims, 1), "sum visit");
-          break;
-        }
-        case ORCA_HIP_EW_MAX_VISIT: {
-          const size_t dims[1] = {n};
-          check_oracle(orc_max_to_shape(a, d, dims, 1, dims, 1), "max visit");
-          break;
-        }
-        case ORCA_HIP_EW_COPY: std::copy(a, a + n, d); break;
-        case ORCA_HIP_EW_ADD_SCALAR: {
-          std::vector<float> sc(n, I.scalar);
-          orc_add(a, sc.data(), d, n);
-          break;
-        }
-        default: fail(ORCA_HIP_ERR_INTERNAL, "unknown opcode");
-      }
-      reg[I.dst].swap(tmp);
-    }
-    for (size_t o = 0; o < n_outputs; ++o) {
-      if (out_regs[o] >= n_regs) fail(ORCA_HIP_ERR_INTERNAL, "output register out of range");
-      check_extent(ctx, outputs[o], 4 * n, "ew_program output");
-      std::copy(reg[out_regs[o]].begin(), reg[out_regs[o]].end(), outputs[o]);
-    }
+    auto reg = fake_program(ctx, n, inputs, n_inputs, n_outputs, instrs, n_instrs, n_regs);
+    fake_outputs(ctx, n, reg, outputs, out_regs, n_outputs);
     logf("program " + std::to_string(n_inputs) + " " + std::to_string(n_outputs) + " " + std::to_string(n_instrs) +
          " " + std::to_string(n_regs) + (ctx->main ? " side" : ""));
+  });
+}
+
+// The program, then the rows of one register reduced as the oracle's sum_to_shape / max_to_shape.
+int orca_hip_ew_program_rows(orca_hip_ctx* ctx, size_t rows, size_t cols, const orca_hip_ew_input* inputs,
+                             size_t n_inputs, float* const* outputs, const uint8_t* out_regs, size_t n_outputs,
+                             const orca_hip_ew_instr* instrs, size_t n_instrs, size_t n_regs, int red_reg,
+                             int reduce_max, float* reduced) {
+  return guard([&] {
+    if (cols == 0 || cols > 64 || red_reg < 0 || (size_t)red_reg >= n_regs)
+      fail(ORCA_HIP_ERR_INTERNAL, "ew_program_rows: bad arguments");
+    launch(ctx, "program_rows");
+    const size_t n = rows * cols;
+    auto reg = fake_program(ctx, n, inputs, n_inputs, n_outputs, instrs, n_instrs, n_regs);
+    fake_outputs(ctx, n, reg, outputs, out_regs, n_outputs);
+    W(ctx, reduced, 4 * rows);
+    const size_t in[2] = {rows, cols}, os[2] = {rows, 1};
+    check_oracle(reduce_max ? orc_max_to_shape(reg[red_reg].data(), reduced, in, 2, os, 2)
+                            : orc_sum_to_shape(reg[red_reg].data(), reduced, in, 2, os, 2),
+                 "ew_program_rows");
+    logf("program_rows " + std::to_string(n_inputs) + " " + std::to_string(n_outputs) + " " +
+         std::to_string(n_instrs) + " " + std::to_string(n_regs) + (reduce_max ? " max" : " sum") +
+         (ctx->main ? " side" : ""));
   });
 }
 

@@ -298,3 +298,44 @@ def test_unaligned_inputs_take_the_element_kernel(ctx, pair, jit, n):
     got = lazy.sqrt(lazy.add(lazy.mul(va, vb, sh), lazy.relu(va, sh), sh), sh)
     want = eager.sqrt(eager.add(eager.mul(va, vb, sh), eager.relu(va, sh), sh), sh)
     np.testing.assert_array_equal(lazy.to_f32_vec(got), eager.to_f32_vec(want))
+
+
+@pytest.mark.parametrize("rows,cols", [(1024, 10), (1, 64), (1000, 64), (4097, 3), (255, 2), (100003, 7),
+                                       (33, 4)])
+@pytest.mark.parametrize("is_max", [False, True], ids=["sum", "max"])
+def test_row_reductions_with_their_chain_bit_identical(pair, ctx, rows, cols, is_max):
+    """sum_to_shape / max_to_shape([R, C] -> [R, 1]) of a pending chain runs in the chain's
+    launch (orca_hip_ew_program_rows) and equals the eager backend's chain and reduction
+    kernels bit for bit, over special values (NaN, +-inf, -0, subnormals, whole rows of -inf,
+    f32::MIN), with a per-row and a per-column broadcast input.  Against the oracle: the
+    reduction and every op but exp bit for bit on the device's values; exp within the device
+    library's ulp of glibc's."""
+    lazy, eager = pair
+    rng = np.random.default_rng(rows + 7 * cols)
+    n = rows * cols
+    a = special(rng, n).reshape(rows, cols)
+    a[min(1, rows - 1), :] = -np.inf
+    a[min(2, rows - 1), 0] = np.finfo(np.float32).min
+    m = rng.standard_normal((rows, 1)).astype(np.float32)
+    t = special(rng, n).reshape(rows, cols)
+    bias = rng.standard_normal((1, cols)).astype(np.float32)
+    sh, rs, cs = (rows, cols), (rows, 1), (1, cols)
+    got = {}
+    ctx.prof_enable(True)
+    ctx.prof_reset()
+    for be in pair:
+        A_, M_, T_, B_ = up(be, a), up(be, m), up(be, t), up(be, bias)
+        e = be.exp(be.sub(A_, be.expand(M_, rs, sh), sh), sh)
+        y = be.mul_scalar(be.mul(be.add(T_, be.expand(B_, cs, sh), sh), e, sh), -1.0, sh)
+        r = (be.max_to_shape if is_max else be.sum_to_shape)(y, sh, rs)
+        got[be is lazy] = (be.to_f32_vec(r), be.to_f32_vec(e), be.to_f32_vec(y))
+    names = {k["name"] for k in ctx.prof_report()["kernels"]}
+    ctx.prof_enable(False)
+    assert "ew_program_rows" in names, names
+    for g, w in zip(got[True], got[False]):
+        np.testing.assert_array_equal(g, w)
+    e, y = got[True][1].reshape(sh), got[True][2].reshape(sh)
+    np.testing.assert_allclose(e, O.exp(O.sub(a, O.expand(m, sh))), rtol=4e-7, atol=0)
+    np.testing.assert_array_equal(y, O.mul_scalar(O.mul(O.add(t, O.expand(bias, sh)), e), np.float32(-1.0)))
+    want = (O.max_to_shape if is_max else O.sum_to_shape)(y, rs)
+    np.testing.assert_array_equal(got[True][0], np.asarray(want).reshape(-1))

@@ -144,6 +144,49 @@ def test_random_chains_match_ops_run_one_by_one(lib, hb, seed, n_leaves, n_ops, 
         assert n_regs <= N_REGS_MAX
 
 
+@pytest.mark.parametrize("rows,cols,is_max", [(16, 10, False), (16, 10, True), (37, 1, False), (5, 64, True),
+                                               (300, 3, False), (9, 65, False), (9, 65, True)])
+def test_row_reductions_run_with_their_chain(lib, ctx, rows, cols, is_max):
+    """sum_to_shape / max_to_shape([R, C] -> [R, 1]) of a pending chain runs in the chain's own
+    launch (C <= 64) and gives the bits of the chain's values reduced one op at a time: the
+    eager backend's kernels and the oracle.  The chain's values held elsewhere are written by
+    the same launch.  Rows with NaN, -inf and f32::MIN keep max_to_shape's strict `>` from
+    f32::MIN (orca-backend-cpu/src/backend.rs:1336-1381)."""
+    from orcaml_amd.backend import HipBackend
+
+    rng = np.random.default_rng(rows * 100 + cols)
+    a = rng.standard_normal((rows, cols)).astype(np.float32) * 4
+    if cols > 1:
+        a[0, 1] = np.nan
+        a[min(1, rows - 1), :] = -np.inf
+        a[min(2, rows - 1), 0] = np.finfo(np.float32).min
+    m = rng.standard_normal((rows, 1)).astype(np.float32)
+    t = rng.standard_normal((rows, cols)).astype(np.float32)
+    sh, rs = (rows, cols), (rows, 1)
+    got = {}
+    for lazy in (True, False):
+        hb = HipBackend(ctx, lazy=lazy)
+        A_, M_, T_ = (up(hb, v.reshape(-1)) for v in (a, m, t))
+        fake_lib.clear(lib)
+        e = hb.exp(hb.sub(A_, hb.expand(M_, rs, sh), sh), sh)  # held: written by the reducing launch
+        y = hb.mul_scalar(hb.mul(T_, e, sh), -1.0, sh)
+        r = (hb.max_to_shape if is_max else hb.sum_to_shape)(y, sh, rs)
+        got[lazy] = (down(hb, r), down(hb, e), down(hb, y))
+        rows_launches = [line for line in fake_lib.log(lib) if line.startswith("program_rows ")]
+        if lazy:  # (one column: the identity reduction, an instruction of the chain)
+            fused = 1 < cols <= 64
+            assert len(rows_launches) == int(fused) and len(programs(lib)) == 1 - int(fused), fake_lib.log(lib)
+        del A_, M_, T_, e, y, r, hb
+        gc.collect()
+    for g, w in zip(got[True], got[False]):
+        np.testing.assert_array_equal(g, w)
+    e = O.exp(O.sub(a, O.expand(m, sh)))
+    y = O.mul_scalar(O.mul(t, e), np.float32(-1.0))
+    want = (O.max_to_shape if is_max else O.sum_to_shape)(y, rs)
+    np.testing.assert_array_equal(got[True][0], np.asarray(want).reshape(-1))
+    np.testing.assert_array_equal(got[True][1], np.asarray(e).reshape(-1))
+
+
 def test_programs_are_reused_across_steps(lib, hb):
     """Each step's chain has the same structure and its own scalar (AdamW's bias corrections
     change every step); every step computes with its own."""
@@ -355,8 +398,9 @@ def test_composed_step_folds_and_fuses(lib, ctx):
     """What one steady-state composed step launches: the Linear forwards as products with the
     bias (+ ReLU) epilogue, each ReluBackward as the next product's mask epilogue, the weight
     gradients with their bias column sums in one launch, the head's weight, bias and masked
-    input gradients from one grid, and no single elementwise op (only the loss's row reductions
-    run as kernels of their own)."""
+    input gradients from one grid, the loss's row sums in the launches of the chains they
+    reduce, and no single elementwise op (only the logits' row maximum, its backward and the
+    batch sum run as kernels of their own)."""
     from orcaml_amd.backend import HipBackend
 
     dims, B = (784, 48, 40, 10), 16
@@ -381,6 +425,8 @@ def test_composed_step_folds_and_fuses(lib, ctx):
     # the hidden layers' dW with its db; the head's dW, db and masked dX from one grid
     assert sum(line.startswith("matmul_colsum ") for line in log) == 2, log
     assert sum(line.startswith("narrow_linear_backward 16x40x10 mask") for line in log) == 1, log
+    # the softmax's and its backward's row sums run with the chains before them
+    assert sum(line.startswith("program_rows ") for line in log) == 4, log
     reductions = ("op max_to_shape", "op sum_to_shape", "op max_to_shape_backward")
     assert not [line for line in log if line.startswith("op ") and line not in reductions], log
 
