@@ -171,6 +171,9 @@ struct Node {
   bool in_place = false;
   // Computed by arithmetic (a product, a loss): it holds no signaling NaN, so x * 1 is x.
   bool quiet = false;
+  // Holds no -0 either (a loss gradient whose every element is a sum of terms that are never
+  // -0), so 0 + x is x too: its identity sum_to_shape is the value itself.
+  bool canon = false;
   bool in_pending = false;
   uint64_t pseq = 0;  // creation order among pending nodes
 
@@ -1906,6 +1909,7 @@ int orca_hip_trait_sum_to_shape(orca_hip_backend* be, orca_hip_storage* s, const
     if (b->opt.deferred && dtype == ORCA_HIP_F32 && x->tshape.empty() && no_fill) {
       const bool same = in_rank == out_rank && std::equal(in_shape, in_shape + in_rank, out_shape);
       if (same) {  // computed once per storage (storages are immutable)
+        if (x->kind == Kind::kValue && x->canon) return put(out, ref(x));
         if (x->ident) return put(out, ref(x->ident));
         Node* r;
         if (b->opt.lazy) {
@@ -2124,7 +2128,9 @@ int orca_hip_be_softmax_ce(orca_hip_backend* be, orca_hip_storage* logits, orca_
     ck(orca_hip_softmax_ce(b->ctx, lp, B, C, op, nullptr, l->buf->ptr, want_grad ? d->buf->ptr : nullptr, nullptr,
                            nullptr));
     l->quiet = true;
-    if (want_grad) d->quiet = true;
+    // every element of the gradient is (0 + a) + (0 + b), plus (0 + c) at a row's maximum:
+    // never -0, never a signaling NaN
+    if (want_grad) d->quiet = d->canon = true;
     *loss = S_(l.release());
     if (want_grad) *dlogits = S_(d.release());
   });

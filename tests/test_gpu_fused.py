@@ -366,6 +366,36 @@ def test_softmax_ce_ties_nan_and_equal_logits(ctx):
     assert_close(grad[rows], grad_ref[rows], what="dlogits")
 
 
+@pytest.mark.parametrize("B,C", [(1024, 10), (64, 64), (37, 300), (6, 4096)])
+def test_softmax_ce_onehot_gradient_holds_no_negative_zero(ctx, B, C):
+    """With one-hot targets every element of dL/dlogits is (0 + a) + (0 + b), plus (0 + c) at a
+    row's maximum: never -0 and never a signaling NaN, so 0 + d is d bit for bit.  The storage
+    layer relies on it to hand the loss gradient on as its own identity sum_to_shape.  Rows of
+    zeros, ties, +-inf, NaN, huge and tiny logits, labels on and off the maximum."""
+    rng = np.random.default_rng(B + C)
+    logits = (3.0 * rng.standard_normal((B, C))).astype(np.float32)
+    logits[0, :] = 0.0
+    logits[1, :] = -np.inf
+    logits[1, C // 2] = 0.0
+    logits[2, 0] = np.nan
+    logits[3, C - 1] = np.inf
+    logits[4, :] = np.float32(-3.0e38)
+    logits[5, :] = 1e-30
+    if B > 6:
+        logits[6, C // 3] = 300.0
+        logits[7, :] = np.float32(3.0e38)
+    labels = rng.integers(0, C, B)
+    labels[0] = 0
+    labels[1] = C // 2
+    onehot = synth.one_hot(labels, C)
+    _, grad, _, _ = run_ce(ctx, logits, onehot=onehot)
+    bits = grad.view(np.uint32)
+    assert not (bits == 0x80000000).any(), np.argwhere(bits == 0x80000000)[:5]
+    nan = np.isnan(grad)
+    assert ((bits[nan] & 0x00400000) != 0).all()  # quiet NaNs only
+    np.testing.assert_array_equal((np.float32(0.0) + grad).view(np.uint32), bits)
+
+
 def test_adamw_and_sgd_bit_exact(ctx):
     rng = np.random.default_rng(11)
     n = 100003  # odd length exercises the scalar tail

@@ -49,7 +49,8 @@ def pair(ctx):
 @pytest.fixture(params=[0, 2], ids=["interpreted", "compiled"])
 def jit(request, ctx):
     """Runs the test with every program interpreted, then with every program compiled at
-    its first use (orca_hip_ew_set_jit); the compiled run must not fall back."""
+    its first use (orca_hip_ew_set_jit); the compiled run must not fall back.  (A test whose
+    ops leave no chain to run -- the fused loss and update -- launches no program at all.)"""
     before = ctx.ew_jit_stats()
     ctx.set_ew_jit(request.param)
     yield request.param
@@ -57,7 +58,8 @@ def jit(request, ctx):
     after = ctx.ew_jit_stats()
     assert after["failures"] == before["failures"]
     if request.param == 2:
-        assert after["compiled_launches"] > before["compiled_launches"]
+        none_expected = request.node.callspec.params.get("fused", False)
+        assert (after["compiled_launches"] > before["compiled_launches"]) != none_expected
         assert after["interpreted"] == before["interpreted"]
     else:
         assert after["compiled_launches"] == before["compiled_launches"]

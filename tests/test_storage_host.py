@@ -431,6 +431,30 @@ def test_composed_step_folds_and_fuses(lib, ctx):
     assert not [line for line in log if line.startswith("op ") and line not in reductions], log
 
 
+def test_fused_step_hands_the_loss_gradient_on_unchanged(lib, ctx):
+    """With the fused loss, the loss gradient times the seed of one and the identity
+    sum_to_shape of the head's bias add are the gradient itself (it holds no -0 and no
+    signaling NaN): the head's backward grid reads softmax_ce's output, and a steady-state
+    step runs no elementwise program at all."""
+    from orcaml_amd.backend import HipBackend
+
+    dims, B = (784, 48, 40, 10), 16
+    params, x, labels, onehot = synth.mlp_problem(16, dims, B)
+    ad = A.Autodiff(HipBackend(ctx))
+    composed(ad, params, x, onehot, "adamw", 1, fused=True, lr=1e-3)
+    model = A.build_mlp(ad, params)
+    optim = A.AdamW(model.parameters(), lr=1e-3, weight_decay=0.01, fused=True)
+    xt, tt = A.Tensor.from_numpy(ad, x), A.Tensor.from_numpy(ad, onehot)
+    fake_lib.clear(lib)
+    optim.zero_grad()
+    A.CrossEntropyLoss(fused=True)(model(xt), tt).backward()
+    optim.step()
+    log = fake_lib.log(lib)
+    assert not [line for line in log if line.startswith("program")], log
+    i = next(k for k, line in enumerate(log) if line.startswith("softmax_ce"))
+    assert log[i + 1].startswith("narrow_linear_backward 16x40x10 mask"), log
+
+
 @pytest.mark.parametrize("kind", ["adamw", "sgd"])
 def test_composed_update_runs_beside_the_backward_products(lib, ctx, kind):
     """The reference's own composed optimizer (unchanged user code): an update program whose
