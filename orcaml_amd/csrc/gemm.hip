@@ -534,6 +534,318 @@ __global__ void __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2
   write_tile(acc, C, ldc, epi, m0 + wm * (BM / 2), n0 + wn * (BN / 2), m0 + BM <= p.M && n0 + BN <= p.N, p);
 }
 
+// ---------------------------------------------------------------------------
+// Banded weight gradients: C = A^T B with A stored [K][lda] (X of a layer whose
+// input count M is not a multiple of 128, e.g. 784 = 28 x 28) and B stored
+// [K][ldb] (dY, N a multiple of 128), one K chunk, pipelined as the kernel
+// above.  With 128 x 128 tiles M = 784 takes 7 tile rows, the last one 16/128
+// full, and each busy CU runs four MFMA 32 x 32 blocks per SIMD and k step.
+// Both forms below use 32 x 32 blocks for 96 rows of a block's 128 columns
+// (wave w: columns 32 w .. 32 w + 31, three blocks) and 16 x 16 x 4 blocks for
+// 16 more rows:
+//   ROWS112 (M = 112 R, R <= 7): block (c, r) owns rows 112 r .. 112 r + 111;
+//     wave w's last 16 rows are two 16 x 16 blocks with the full k range.  7 x
+//     N/128 blocks (224 for N = 4096, CUs left free for work beside it, as the
+//     128 x 128 grid leaves them), 3 x 1024 + 2 x 256 MFMA cycles per SIMD and
+//     slab instead of 4 x 1024.
+//   EIGHT (M = 768 + E, 4 <= E <= 16): block (c, r), r < 8, owns rows 96 r ..
+//     96 r + 95 and the E leftover rows 768 .. M - 1 of its 16 columns 128 c +
+//     16 r .. + 15: one 16 x 16 block whose k range the four waves share (wave
+//     w: k = 8 w .. 8 w + 7 of every slab), the partial sums added in wave order
+//     at the end.  8 x N/128 blocks (256 for N = 4096: every CU), 3 x 1024 + 64
+//     MFMA cycles per SIMD and slab.
+// A's LDS rows hold the 96 band values, then the 16 others (pitch 112).
+// COLSUM: the bias gradient, colsum[n] = sum of B's column n in ascending k from
+// +0 (the additions of sum_to_shape, so the same bits).  EIGHT: on a fifth wave
+// per block that does nothing else, the 16 columns 128 c + 16 r .. + 15; it
+// reads each slab's B tile between the same barriers as the MFMA waves, and its
+// dependent adds issue on SIMD 0 beside wave 0's matrix instructions.  ROWS112
+// (whose waves need more than half a SIMD's registers, so a fifth one does not
+// fit): one more row of N/128 blocks, each summing its 128 columns straight from
+// global memory, one per thread, on CUs the product's blocks leave free.
+constexpr int BAND_M = 96, BAND_EX = 16, BAND_AP = BAND_M + BAND_EX, BAND_ROWS = 8 * BAND_M;
+constexpr int BAND_EIGHT = 0, BAND_ROWS112 = 1;
+
+typedef float floatx2 __attribute__((ext_vector_type(2)));
+
+// A of a banded product: per slab and thread three float4s of the block's 96
+// band rows (32 k rows x 24 float4) and one float2 of its 16 other rows (32 x 8)
+// starting at m_ex; rows past M - 1 repeat the last valid pair (never stored).
+struct BandOperandA {
+  const char* base;
+  uint32_t voff[4];
+  uint32_t slab_bytes;
+  __device__ __forceinline__ void init(const float* a, int64_t lda, int m0, int m_ex, int M) {
+    base = reinterpret_cast<const char*>(a);
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+      const int idx = tid + NTHREADS * j;
+      voff[j] = (uint32_t)(((int64_t)(idx / 24) * lda + m0 + (idx % 24) * 4) * 4);
+    }
+    voff[3] = (uint32_t)(((int64_t)(tid >> 3) * lda + min(m_ex + (tid & 7) * 2, M - 2)) * 4);
+    slab_bytes = (uint32_t)(BK * lda * 4);
+  }
+  __device__ __forceinline__ void load(int t, floatx4 (&r)[3], floatx2& e) const {
+    const char* slab = base + (size_t)slab_bytes * (uint32_t)t;
+#pragma unroll
+    for (int j = 0; j < 3; ++j) r[j] = *reinterpret_cast<const floatx4*>(slab + voff[j]);
+    e = *reinterpret_cast<const floatx2*>(slab + voff[3]);
+  }
+  // The last, partial slab: k offsets >= klen are zero-filled without touching memory.
+  __device__ __forceinline__ void load_tail(int t, int klen, floatx4 (&r)[3], floatx2& e) const {
+    const char* slab = base + (size_t)slab_bytes * (uint32_t)t;
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+      const int kk = t * BK + (tid + NTHREADS * j) / 24;
+      r[j] = kk < klen ? *reinterpret_cast<const floatx4*>(slab + voff[j]) : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+    const int kk = t * BK + (tid >> 3);
+    e = kk < klen ? *reinterpret_cast<const floatx2*>(slab + voff[3]) : floatx2{0.0f, 0.0f};
+  }
+};
+
+template <int MODE, bool COLSUM>
+__global__ void __launch_bounds__(COLSUM && MODE == BAND_EIGHT ? NTHREADS + 64 : NTHREADS)
+__attribute__((amdgpu_waves_per_eu(MODE == BAND_EIGHT ? 2 : 1))) gemm_tn_band_kernel(GemmParams p) {
+  constexpr bool EIGHT = MODE == BAND_EIGHT;
+  constexpr int MT = BAND_M / 32;
+  constexpr int NX = EIGHT ? 1 : 2;  // 16 x 16 blocks per wave
+  constexpr int A_TILE = BK * BAND_AP + MN_GAP, B_TILE = BK * 128 + MN_GAP;
+  __shared__ __attribute__((aligned(16))) float smem[2][A_TILE + B_TILE];
+
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int band = blockIdx.y, n0 = blockIdx.x * 128;
+  const int m0 = EIGHT ? band * BAND_M : band * BAND_AP;
+  const int m_ex = EIGHT ? BAND_ROWS : m0 + BAND_M;  // first of the 16 other rows
+  const int klen = p.K;
+  const int nfull = klen / BK;
+  const int n = (klen + BK - 1) / BK;
+
+  if (EIGHT && COLSUM && wave == 4) {
+    // Slab t sits in smem[t % 2] from barrier t (the prologue's is barrier 0)
+    // until barrier t + 1, after which region A of slab t + 1 overwrites it.
+    // The MFMA waves pass n + 3 barriers: the prologue's, one per slab and two
+    // around the leftover-row reduction.  Lanes 16 .. 63 repeat lanes 0 .. 15.
+    const int c0 = 16 * band + (lane & 15);
+    float cs = 0.0f;
+    __syncthreads();
+    for (int t = 0; t < n; ++t) {
+      const float* sb = smem[t & 1] + A_TILE + c0;
+#pragma unroll
+      for (int k = 0; k < BK; ++k) cs = cs + sb[mn_off<128>(k)];
+      __syncthreads();
+    }
+    if (lane < 16) p.colsum[n0 + c0] = cs;
+    __syncthreads();
+    __syncthreads();
+    return;
+  }
+  if (!EIGHT && COLSUM && m0 >= p.M) {
+    // The column-sum row: threads 0 .. 127 each add one column of B in row order,
+    // the next 16 rows' loads in flight while 16 are added.
+    if (tid < 128) {
+      const float* src = p.B + n0 + tid;
+      float cs = 0.0f, v[16], w[16];
+      int k = 0;
+      auto fetch = [&](float (&d)[16], int k0) {
+#pragma unroll
+        for (int u = 0; u < 16; ++u) d[u] = src[(int64_t)(k0 + u) * p.ldb];
+      };
+      if (klen >= 16) fetch(v, 0);
+      for (; k + 32 <= klen; k += 32) {
+        fetch(w, k + 16);
+#pragma unroll
+        for (int u = 0; u < 16; ++u) cs = cs + v[u];
+        if (k + 48 <= klen) fetch(v, k + 32);
+#pragma unroll
+        for (int u = 0; u < 16; ++u) cs = cs + w[u];
+      }
+      if (k + 16 <= klen) {
+#pragma unroll
+        for (int u = 0; u < 16; ++u) cs = cs + v[u];
+        k += 16;
+      }
+      for (; k < klen; ++k) cs = cs + src[(int64_t)k * p.ldb];
+      p.colsum[n0 + tid] = cs;
+    }
+    return;
+  }
+
+  BandOperandA opa;
+  BufOperand<false> opb;
+  opa.init(p.A, p.lda, m0, m_ex, p.M);
+  opb.init(p.B, p.ldb, n0, p.N, 0);
+
+  floatx16 acc[MT][1];
+#pragma unroll
+  for (int a = 0; a < MT; ++a)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[a][0][r] = 0.0f;
+  floatx4 accx[NX];
+#pragma unroll
+  for (int x = 0; x < NX; ++x) accx[x] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  floatx4 ra[3], rb[4];
+  floatx2 re;
+  float f0a[MT][8], f0b[8], f1a[MT][8], f1b[8];
+  // 16 x 16 fragments of a half slab: EIGHT one step (A, B), ROWS112 four
+  // steps of A and of the wave's two column blocks of B.
+  constexpr int XS = EIGHT ? 1 : 4;
+  float x0a[XS], x0b[XS][NX], x1a[XS], x1b[XS][NX];
+
+  // LDS offsets of this thread's A stores (k row, column).
+  int soff[4];
+#pragma unroll
+  for (int j = 0; j < 3; ++j) {
+    const int idx = tid + NTHREADS * j;
+    soff[j] = mn_off<BAND_AP>(idx / 24) + (idx % 24) * 4;
+  }
+  soff[3] = mn_off<BAND_AP>(tid >> 3) + BAND_M + (tid & 7) * 2;
+  // 16 x 16 x 4 lane layout: lane (g, c) = (lane / 16, lane % 16) holds A[row c][k g]
+  // and B[k g][column c]; EIGHT's k is 8 w + 4 half + g, ROWS112's 16 half + 4 s + g.
+  const int xg = lane >> 4, xc = lane & 15;
+  const int xcol = EIGHT ? 16 * band + xc : 32 * wave + xc;  // column within the tile
+
+  auto store = [&](float* s) {
+#pragma unroll
+    for (int j = 0; j < 3; ++j) *reinterpret_cast<floatx4*>(s + soff[j]) = ra[j];
+    *reinterpret_cast<floatx2*>(s + soff[3]) = re;
+    store_slab<false, 128>(s + A_TILE, rb);
+  };
+  auto load = [&](int t) {
+    opa.load(t, ra, re);
+    opb.load(t, rb);
+  };
+  auto load_any = [&](int t) {  // uniform branch: whole or partial slab
+    if (t < nfull) {
+      load(t);
+    } else {
+      opa.load_tail(t, klen, ra, re);
+      opb.load_tail(t, klen, rb);
+    }
+  };
+  auto frags = [&](const float* s, int half, float (&fa)[MT][8], float (&fb)[8], float (&xa)[XS],
+                   float (&xb)[XS][NX]) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) read_frag<false, BAND_AP>(s, mt * 32, half, fa[mt]);
+    read_frag<false, 128>(s + A_TILE, wave * 32, half, fb);
+#pragma unroll
+    for (int st = 0; st < XS; ++st) {
+      const int kk = EIGHT ? 8 * wave + 4 * half + xg : 16 * half + 4 * st + xg;
+      xa[st] = s[mn_off<BAND_AP>(kk) + BAND_M + xc];
+#pragma unroll
+      for (int x = 0; x < NX; ++x) xb[st][x] = s[A_TILE + mn_off<128>(kk) + xcol + 16 * x];
+    }
+  };
+  auto mfma = [&](const float (&fa)[MT][8], const float (&fb)[8], const float (&xa)[XS], const float (&xb)[XS][NX]) {
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+        acc[mt][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[mt][q], fb[q], acc[mt][0], 0, 0, 0);
+      if (!EIGHT && (q & 1)) {  // ROWS112: the 16 x 16 steps spread among the 32 x 32 ones
+#pragma unroll
+        for (int x = 0; x < NX; ++x)
+          accx[x] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa[q >> 1], xb[q >> 1][x], accx[x], 0, 0, 0);
+      }
+    }
+    if (EIGHT) accx[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa[0], xb[0][0], accx[0], 0, 0, 0);
+  };
+  // Region A: 8 LDS stores, 8 VMEM loads and the half-slab fragments among its
+  // matrix instructions (EIGHT: 25 and 34 scalar LDS reads; ROWS112: 32 and 44).
+  constexpr int NMF = EIGHT ? 25 : 32, NRD = EIGHT ? 34 : 44;
+  auto interleave_a = [&]() {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // DS write
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // DS read
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+    }
+#pragma unroll
+    for (int j = 0; j < NMF - 16; ++j) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, (NRD - 32 + NMF - 17) / (NMF - 16), 0);
+    }
+  };
+  auto interleave_b = [&]() {
+#pragma unroll
+    for (int j = 0; j < (NRD + 1) / 2; ++j) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+    }
+  };
+
+  auto body = [&](auto P_, int t, bool full) {
+    constexpr int P = decltype(P_)::value;
+    float* lcur = smem[P];
+    float* lnxt = smem[P ^ 1];
+    if (full) {
+      store(lnxt);
+      load(t + 2);
+      frags(lcur, 1, f1a, f1b, x1a, x1b);
+      mfma(f0a, f0b, x0a, x0b);
+      interleave_a();
+    } else {
+      if (t + 1 < n) store(lnxt);
+      if (t + 2 < n) load_any(t + 2);
+      frags(lcur, 1, f1a, f1b, x1a, x1b);
+      mfma(f0a, f0b, x0a, x0b);
+    }
+    __syncthreads();
+    if (full) {
+      frags(lnxt, 0, f0a, f0b, x0a, x0b);
+      mfma(f1a, f1b, x1a, x1b);
+      interleave_b();
+    } else {
+      if (t + 1 < n) frags(lnxt, 0, f0a, f0b, x0a, x0b);
+      mfma(f1a, f1b, x1a, x1b);
+    }
+  };
+
+  load_any(0);
+  store(smem[0]);
+  if (n > 1) load_any(1);
+  __syncthreads();
+  frags(smem[0], 0, f0a, f0b, x0a, x0b);
+
+  int t = 0;
+  for (; t + 3 < nfull; t += 2) {
+    body(std::integral_constant<int, 0>{}, t, true);
+    body(std::integral_constant<int, 1>{}, t + 1, true);
+  }
+  if (t < n) body(std::integral_constant<int, 0>{}, t, false);
+  if (t + 1 < n) body(std::integral_constant<int, 1>{}, t + 1, false);
+  if (t + 2 < n) body(std::integral_constant<int, 0>{}, t + 2, false);
+  if (t + 3 < n) body(std::integral_constant<int, 1>{}, t + 3, false);
+
+  // The 16 x 16 blocks: lane (g, c) holds rows 4 g .. 4 g + 3 of column c.
+  if (EIGHT) {  // the four waves' partial sums, added in wave order
+    __syncthreads();
+    float* red = smem[0];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) red[wave * 256 + (4 * xg + j) * 16 + xc] = accx[0][j];
+    __syncthreads();
+    const int row = BAND_ROWS + (tid >> 4);
+    const float v = ((red[tid] + red[256 + tid]) + red[512 + tid]) + red[768 + tid];
+    if (row < p.M) p.C[(int64_t)row * p.ldc + n0 + 16 * band + (tid & 15)] = v;
+  } else {
+#pragma unroll
+    for (int x = 0; x < NX; ++x)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        p.C[(int64_t)(m_ex + 4 * xg + j) * p.ldc + n0 + xcol + 16 * x] = accx[x][j];
+  }
+  write_tile(acc, p.C, p.ldc, p.epi, m0, n0 + 32 * wave, true, p);
+}
+
 // Sums split-K partials in split order and applies the epilogue.
 struct SplitReduceParams {
   const float* ws;
@@ -1211,6 +1523,7 @@ namespace {
 struct GemmPlan {
   bool fast;
   bool skinny;  // 32 x 32 tiles on gemm_skinny_kernel, no K split
+  int band;     // 0, or 1 + the gemm_tn_band_kernel mode of a banded X^T dY (no K split)
   int narrow;   // 0, or a narrow product: 1 NN (N <= 16), 2 NT (K <= 16), 3 TN (N <= 16)
   size_t BM, BN, mt, nt;
   int splits, k_chunk;  // for a narrow TN product: K slices and rows per slice
@@ -1218,7 +1531,7 @@ struct GemmPlan {
 
 GemmPlan plan_gemm(orca_hip_ctx* ctx, bool trans_a, bool trans_b, size_t M, size_t N, size_t K, const float* A,
                    size_t lda, size_t sa, const float* B, size_t ldb, size_t sb, size_t batch,
-                   int epi_kind = ORCA_HIP_EPI_NONE) {
+                   int epi_kind = ORCA_HIP_EPI_NONE, int band_pref = 0) {
   GemmPlan g{};
   // Narrow products (one batch entry; a bias on X W, a ReLU mask on dY W^T) take the vector-unit kernels.
   if (ctx->gemm_narrow && batch == 1 && K > 0) {
@@ -1260,6 +1573,32 @@ GemmPlan plan_gemm(orca_hip_ctx* ctx, bool trans_a, bool trans_b, size_t M, size
   int bn = t128 >= target ? 128 : 64;
   if (ctx->gemm_tile_bn) bn = ctx->gemm_tile_bn;
   if (g.fast) bn = 128;
+  // A weight gradient X^T dY (no epilogue) whose banded grid is one round between
+  // half and all of the CUs (so it takes no K split) runs banded: 112-row tiles for
+  // M = 112 R (R <= 7: as many tiles as 128 rows need, each 12.5 % smaller), or
+  // eight 96-row bands plus 16 x 16 blocks for M = 768 + E, whichever the context
+  // prefers when both apply.
+  const size_t band_cols = N / 128;
+  if (g.fast && ctx->gemm_band && trans_a && !trans_b && batch == 1 && epi_kind == ORCA_HIP_EPI_NONE &&
+      N % 128 == 0) {
+    const size_t r112 = M / BAND_AP;
+    const bool rows112 = M % BAND_AP == 0 && r112 >= 1 && r112 <= 7 && r112 * band_cols <= target &&
+                         2 * r112 * band_cols > target;
+    const bool eight = M > (size_t)BAND_ROWS && M <= (size_t)(BAND_ROWS + BAND_EX) && 8 * band_cols <= target &&
+                       16 * band_cols > target;
+    if (rows112 || eight) {
+      const int pref = band_pref ? band_pref : ctx->gemm_band;
+      const bool use_eight = eight && (!rows112 || pref == 1);
+      g.band = 1 + (use_eight ? BAND_EIGHT : BAND_ROWS112);
+      g.BM = use_eight ? BAND_M : BAND_AP;
+      g.BN = 128;
+      g.mt = use_eight ? 8 : r112;
+      g.nt = band_cols;
+      g.splits = 1;
+      g.k_chunk = (int)K;
+      return g;
+    }
+  }
   size_t BM = 128;
   // Short products (K <= 512) whose 128 x 128 grid leaves at least half the
   // CUs idle take 64 x 64 tiles on the generic kernel instead of splitting K,
@@ -1494,7 +1833,7 @@ void gemm_launch(orca_hip_ctx* ctx, bool trans_a, bool trans_b, size_t M, size_t
     if (epi.colsum) launch_fill(ctx, epi.colsum, 0.0f, N);
     return;
   }
-  const GemmPlan plan = plan_gemm(ctx, trans_a, trans_b, M, N, K, A, lda, sa, B, ldb, sb, batch, epi.kind);
+  const GemmPlan plan = plan_gemm(ctx, trans_a, trans_b, M, N, K, A, lda, sa, B, ldb, sb, batch, epi.kind, epi.band);
   if (plan.narrow) {
     gemm_narrow(ctx, plan, M, N, K, A, lda, B, ldb, C, ldc, epi);
     return;
@@ -1588,8 +1927,11 @@ void gemm_launch(orca_hip_ctx* ctx, bool trans_a, bool trans_b, size_t M, size_t
     // Profiler records carry the product's shape: "gemm_tn_pipe 4096x4096x1024".
     std::string pname;
     if (ctx->prof.enabled) {
-      pname = std::string(kernel_name(trans_a, trans_b, fast)) + " " + std::to_string(M) + "x" + std::to_string(N) +
-              "x" + std::to_string(K);
+      pname = std::string(plan.band == 1 + BAND_EIGHT     ? "gemm_tn_band8"
+                          : plan.band == 1 + BAND_ROWS112 ? "gemm_tn_band112"
+                                                          : kernel_name(trans_a, trans_b, fast)) +
+              " " +
+              std::to_string(M) + "x" + std::to_string(N) + "x" + std::to_string(K);
       if (batch > 1) pname += "x" + std::to_string(batch);
     }
     ProfScope ps(ctx, pname.c_str(), 2.0 * (double)M * N * K * batch,
@@ -1614,7 +1956,24 @@ void gemm_launch(orca_hip_ctx* ctx, bool trans_a, bool trans_b, size_t M, size_t
     // The pipelined kernel is the product's last launch unless a split
     // reduce or a separate column sum follows it.
     const bool bind = epi.done && splits == 1 && (!epi.colsum || fold_colsum);
-    if (fast) {
+#define BAND_LAUNCH(MODE_, CS_)                                                                          \
+  do {                                                                                                    \
+    const dim3 threads(CS_ && MODE_ == BAND_EIGHT ? NTHREADS + 64 : NTHREADS);                           \
+    const dim3 bgrid(grid.x, grid.y + (CS_ && MODE_ == BAND_ROWS112 ? 1 : 0));                            \
+    if (bind)                                                                                             \
+      hipExtLaunchKernelGGL((gemm_tn_band_kernel<MODE_, CS_>), bgrid, threads, 0, ctx->stream, nullptr, epi.done, \
+                            0, p);                                                                        \
+    else                                                                                                  \
+      hipLaunchKernelGGL((gemm_tn_band_kernel<MODE_, CS_>), bgrid, threads, 0, ctx->stream, p);           \
+  } while (0)
+    if (plan.band) {
+      bound = bind;
+      const bool eight = plan.band == 1 + BAND_EIGHT;
+      if (eight && p.colsum) BAND_LAUNCH(BAND_EIGHT, true);
+      else if (eight) BAND_LAUNCH(BAND_EIGHT, false);
+      else if (p.colsum) BAND_LAUNCH(BAND_ROWS112, true);
+      else BAND_LAUNCH(BAND_ROWS112, false);
+    } else if (fast) {
       bound = bind;
       // The column sum reads only B's LDS tile (row-major B), so it folds in
       // whatever A's layout is.
@@ -1632,6 +1991,7 @@ void gemm_launch(orca_hip_ctx* ctx, bool trans_a, bool trans_b, size_t M, size_t
     } else {
       GEMM_DISPATCH(128, 64);
     }
+#undef BAND_LAUNCH
 #undef FAST_LAUNCH
 #undef GEMM_DISPATCH
 #undef GEMM_LAUNCH

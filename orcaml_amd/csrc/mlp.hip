@@ -86,6 +86,11 @@ struct orca_hip_mlp {
   // fork / mid events bound to the completion of the GEMM before them
   bool bind_events = true;
   size_t side_a = 0;
+  // The second side part [split + side_a, split + side_a + side_b) beside layer 0's
+  // dW on side_bpc2 blocks per CU (0 = the flat grid); what is left of the arena
+  // after it is updated on the context stream after that product, with layer 0.
+  size_t side_b = 0;
+  int side_bpc2 = 0;
   // Persistent workspaces: a step makes no allocator call, so it can be
   // captured once into a HIP graph and replayed.
   orca_hip::AdamWScalars* kdev = nullptr;  // this step's AdamW scalars (device)
@@ -200,6 +205,9 @@ void step_body(orca_hip_mlp* m, const AdamWScalars* kdev) {
     // Layers >= 1 have all their gradients after dW of layer 1; with a second
     // arena nothing of this step writes the P that layer 1's dZ reads.
     const bool early = l == 1 && m->P_next && m->side && split > 0;
+    // Layer 0's weight gradient has the update of the layers above beside it when there
+    // is a side stream: its banded grid then leaves CUs free for that update.
+    if (l == 0) ew.band = m->side ? 2 : 1;
     // The fork and mid events complete with the product's kernel rather than
     // as markers of their own between two launches.
     if (early && m->bind_events) ew.done = m->fork;
@@ -226,13 +234,14 @@ void step_body(orca_hip_mlp* m, const AdamWScalars* kdev) {
     if (early) {
       if (!m->bind_events) ORCA_HIP_CHECK(hipEventRecord(m->mid, ctx->stream));
       ORCA_HIP_CHECK(hipStreamWaitEvent(m->side, m->mid, 0));
-      update(split + m->side_a, m->arena, m->side);
+      update(split + m->side_a, split + m->side_a + m->side_b, m->side, m->side_bpc2);
       ORCA_HIP_CHECK(hipEventRecord(m->join, m->side));
     }
   }
   // ---- update (parameter order W_0, b_0, W_1, ...; flat passes over the arena) ----
   if (forked) {
     update(0, split, ctx->stream, m->u0_bpc);
+    if (m->P_next && m->side) update(split + m->side_a + m->side_b, m->arena, ctx->stream, m->u0_bpc);
     ORCA_HIP_CHECK(hipStreamWaitEvent(ctx->stream, m->join, 0));
   } else {
     update(0, m->arena, ctx->stream);
@@ -407,6 +416,10 @@ int orca_hip_mlp_create(orca_hip_ctx* ctx, const size_t* dims, size_t n_layers, 
       const double frac = sf ? std::atof(sf) / 100.0 : 0.7;
       const size_t span = o - m->off[2];
       m->side_a = std::min(span, (size_t)(frac * (double)span) / 64 * 64);
+      const char* sf2 = std::getenv("ORCA_HIP_SIDE_FRAC2");
+      m->side_b = span - m->side_a;
+      if (sf2) m->side_b = std::min(m->side_b, (size_t)(std::atof(sf2) / 100.0 * (double)span) / 64 * 64);
+      if (const char* b2 = std::getenv("ORCA_HIP_SIDE_BPC2")) m->side_bpc2 = std::atoi(b2);
     }
     host_sync(ctx);
     *out = m.release();

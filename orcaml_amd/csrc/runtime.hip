@@ -108,6 +108,7 @@ int orca_hip_ctx_create(int device, orca_hip_ctx** out) {
     if (const char* v = std::getenv("ORCA_HIP_GEMM_SMALL_TILES")) ctx->gemm_small_tiles = v[0] != '0';
     if (const char* v = std::getenv("ORCA_HIP_GEMM_SKINNY")) ctx->gemm_skinny = v[0] != '0';
     if (const char* v = std::getenv("ORCA_HIP_GEMM_NARROW")) ctx->gemm_narrow = v[0] != '0';
+    if (const char* v = std::getenv("ORCA_HIP_GEMM_BAND")) ctx->gemm_band = v[0] == '0' ? 0 : v[0] == '1' ? 1 : 2;
     if (const char* v = std::getenv("ORCA_HIP_EW_JIT")) ctx->ew_jit_mode = v[0] == '0' ? 0 : v[0] == '2' ? 2 : 1;
     if (const char* v = std::getenv("ORCA_HIP_GEMM_TILE")) {
       if (std::strcmp(v, "128x128") == 0) ctx->gemm_tile_bn = 128;

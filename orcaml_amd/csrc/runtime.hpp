@@ -214,6 +214,10 @@ struct orca_hip_ctx {
   bool gemm_skinny = true;
   // ORCA_HIP_GEMM_NARROW=0 keeps products with N <= 16 (or K <= 16 against B^T) on the tiled kernels.
   bool gemm_narrow = true;
+  // ORCA_HIP_GEMM_BAND: 0 keeps weight gradients X^T dY of 784-like row counts on the
+  // 128 x 128 tiles; 1 prefers the eight-band grid (every CU), 2 the 112-row tiles
+  // (the CUs the 128 x 128 grid leaves free stay free) where both apply.
+  int gemm_band = 2;
   // Host waits on this context's work so far (stream or event synchronisations).
   std::atomic<uint64_t> host_syncs{0};
   orca_hip::StagingRing staging;
@@ -363,6 +367,10 @@ struct GemmEpi {
   // kernel is the last one (no separate marker between it and the next
   // launch), else recorded after it.
   hipEvent_t done = nullptr;
+  // Banded weight gradient grid where both forms apply (gemm_band's values): 0 the
+  // context's preference, 1 every CU (nothing runs beside the product), 2 the grid
+  // that leaves CUs free for work on another stream.
+  int band = 0;
 };
 // Workspace floats gemm() needs for this product (0 when K is not split).
 size_t gemm_workspace_floats(orca_hip_ctx* ctx, bool trans_a, bool trans_b, size_t M, size_t N, size_t K,

@@ -3,6 +3,7 @@ device-resident MLP training step against the CPU oracle, through the C ABI."""
 from __future__ import annotations
 
 import ctypes
+import os
 
 import numpy as np
 import pytest
@@ -233,6 +234,93 @@ def test_gemm_colsum_is_bias_gradient(ctx, M, N, K):
     dW, cs = run_gemm(ctx, True, False, X, dY, colsum=True)
     np.testing.assert_array_equal(cs, O.sum_to_shape(dY, (1, N)).reshape(N))
     assert_gemm_error_bound(dW, X.T, dY)
+
+
+# Banded weight gradients X^T dY (N = 128 j, one round of blocks between half and all of a
+# 256-CU GPU's CUs): the 112-row tiles (M = 112 R, R <= 7) and the eight-band grid
+# (M = 768 + E, E = 4 .. 16); 784 takes either, as the context prefers.  Whole and partial
+# K slabs, K from one slab to 32, every leftover-row count.
+BAND_SHAPES = [(2, 784, 4096, 1024), (2, 784, 4096, 1020), (2, 784, 4096, 36), (2, 784, 4096, 4),
+               (2, 672, 4096, 64), (2, 784, 2432, 96), (1, 784, 4096, 1024), (1, 784, 4096, 1020),
+               (1, 784, 4096, 512), (1, 784, 4096, 36), (1, 784, 4096, 4), (1, 772, 4096, 64), (1, 776, 2304, 128),
+               (1, 780, 3968, 100), (1, 784, 2176, 32)]
+
+
+@pytest.fixture(scope="module")
+def band_ctx(request):
+    """A context preferring the eight-band grid (1) or the 112-row tiles (2) for 784 rows."""
+    from orcaml_amd.device import Context
+
+    old = os.environ.get("ORCA_HIP_GEMM_BAND")
+    os.environ["ORCA_HIP_GEMM_BAND"] = str(request.param)
+    try:
+        c = Context(0)
+    finally:
+        if old is None:
+            del os.environ["ORCA_HIP_GEMM_BAND"]
+        else:
+            os.environ["ORCA_HIP_GEMM_BAND"] = old
+    c.band_mode = request.param
+    yield c
+    c.close()
+
+
+def _band_kernel(M, N, mode, cus):
+    """The banded kernel a product takes (None when neither form's grid fits one round)."""
+    cols = N // 128
+    r112 = M // 112
+    rows112 = M % 112 == 0 and 1 <= r112 <= 7 and r112 * cols <= cus < 2 * r112 * cols
+    eight = 768 < M <= 784 and 8 * cols <= cus < 16 * cols
+    if eight and (not rows112 or mode == 1):
+        return "gemm_tn_band8"
+    return "gemm_tn_band112" if rows112 else None
+
+
+@pytest.mark.parametrize("band_ctx,M,N,K", BAND_SHAPES, indirect=["band_ctx"])
+def test_gemm_band_exact_on_integers_with_exact_colsum(band_ctx, M, N, K):
+    """The banded weight gradient (32 x 32 blocks for 96 rows, 16 x 16 blocks for 16 more):
+    exact on integers, and its bias column sum equals sum_to_shape bit for bit, with and
+    without the column sum; every element of C is written."""
+    ctx = band_ctx
+    cus = ctx.prof_report()["num_cus"]
+    kernel = _band_kernel(M, N, ctx.band_mode, cus)
+    if kernel is None:
+        pytest.skip(f"no banded grid is one round of {cus} CUs for {M} x {N}")
+    rng = np.random.default_rng(M + 3 * N + 5 * K)
+    X, dY = int_matrix(rng, (K, M)), int_matrix(rng, (K, N))
+    want = (X.T.astype(np.int64) @ dY.astype(np.int64)).astype(np.float32)
+    for colsum in (False, True):
+        ctx.prof_reset()
+        ctx.prof_enable(True)
+        out = run_gemm(ctx, True, False, X, dY, colsum=colsum)
+        ctx.prof_enable(False)
+        names = {k["name"] for k in ctx.prof_report()["kernels"]}
+        assert f"{kernel} {M}x{N}x{K}" in names, names
+        C, cs = out if colsum else (out, None)
+        np.testing.assert_array_equal(C, want)
+        if colsum:
+            np.testing.assert_array_equal(cs, O.sum_to_shape(dY, (1, N)).reshape(N))
+
+
+@pytest.mark.parametrize("band_ctx", [1, 2], indirect=True, ids=["band8", "band112"])
+@pytest.mark.parametrize("K", [1024, 256, 60])
+def test_gemm_band_error_bound_and_bias_gradient_bits(band_ctx, K):
+    """Real-valued X^T dY on either banded kernel: within the f32 dot-product bound of the
+    fp64 product, and the folded bias gradient bit-identical to sum_to_shape (NaN,
+    infinities, signed zeros and subnormals in dY pass through its adds as in the loop)."""
+    ctx = band_ctx
+    rng = np.random.default_rng(K)
+    X = rng.standard_normal((K, 784)).astype(np.float32)
+    dY = rng.standard_normal((K, 4096)).astype(np.float32)
+    dW, cs = run_gemm(ctx, True, False, X, dY, colsum=True)
+    assert_gemm_error_bound(dW, X.T, dY)
+    np.testing.assert_array_equal(cs, O.sum_to_shape(dY, (1, 4096)).reshape(4096))
+    dY[:, 7] = -0.0
+    dY[3, 100] = np.inf
+    dY[5, 200] = np.nan
+    dY[:, 300] = np.float32(1e-40)
+    _, cs = run_gemm(ctx, True, False, X, dY, colsum=True)
+    np.testing.assert_array_equal(cs, O.sum_to_shape(dY, (1, 4096)).reshape(4096))
 
 
 def _relu_bw_colsum_order(g, pre):
