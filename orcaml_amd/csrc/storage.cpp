@@ -2110,59 +2110,23 @@ int orca_hip_trait_max_to_shape_backward(orca_hip_backend* be, orca_hip_storage*
 }
 
 // ---------------------------------------------------------------- beside the trait
-// The fused loss over logits still pending as a classifier head's Linear, x @ W + b with at
-// most 16 outputs (Linear.forward, python/orca/nn/linear.py:77-86: the product and the bias
-// add, held by nothing but that add): one launch of the head forward kernel computes the
-// logits, the loss and its gradient, reading x once (orca_hip_head_forward_ce).  The logits
-// come from that kernel's sums (within the f32 dot-product bound of the product's).  False
-// (nothing run) when the logits are not in that form.
-bool head_forward_fold(Backend* be, Node* lg, Node* oh, size_t B, size_t C, float* loss, float* dlogits) {
-  if (!be->opt.fold || be->on_side || lg->kind != Kind::kEw || !lg->tshape.empty() || C < 1 || C > 16) return false;
-  Walk w;
-  w.visit(lg);
-  if (!sig_is(w, {{ORCA_HIP_EW_COPY, -2}, {ORCA_HIP_EW_ADD, -1, 0}})) return false;
-  if (w.order[0]->rc.load(std::memory_order_relaxed) > w.inner[w.order[0]]) return false;  // the bias copy is read elsewhere
-  Node* prod = w.leaves[0];
-  Node* bc = w.leaves[1];
-  if (prod->kind != Kind::kProd || prod->lt || prod->rt || prod->rc.load(std::memory_order_relaxed) > 1) return false;
-  if (prod->M != B || prod->N != C || prod->K < 4 || prod->K % 4 != 0) return false;
-  if (bc->kind != Kind::kBcast || bc->div != 1 || bc->mod != C || bc->lhs->n != C || !bc->lhs->tshape.empty())
-    return false;
-  if (!prod->lhs->tshape.empty() || !prod->rhs->tshape.empty()) return false;
-  Ref hold(ref(lg)), pr(ref(prod)), x(ref(prod->lhs)), wt(ref(prod->rhs)), bias(ref(bc->lhs));
-  float* xp = dptr(be, x.get());
-  float* wp = dptr(be, wt.get());
-  float* bp = dptr(be, bias.get());
-  float* op = dptr(be, oh);
-  if ((reinterpret_cast<uintptr_t>(xp) & 15) || (reinterpret_cast<uintptr_t>(wp) & 15)) return false;
-  BufP out = alloc_buf(be, B * C);
-  ck(orca_hip_head_forward_ce(be->ctx, xp, B, prod->K, wp, bp, C, op, nullptr, out->ptr, loss, dlogits, nullptr,
-                              nullptr));
-  set_value(prod, nullptr);  // nobody else reads it
-  set_value(lg, out);
-  return true;
-}
-
 int orca_hip_be_softmax_ce(orca_hip_backend* be, orca_hip_storage* logits, orca_hip_storage* onehot, size_t B, size_t C,
                            int want_grad, orca_hip_storage** loss, orca_hip_storage** dlogits) {
   return entry(be, [&](Backend* b) {
     check_out(loss);
     if (want_grad) check_out(dlogits);
-    Node* lgn = arg(b, logits, "softmax_ce logits");
+    Ref lg = plain(b, arg(b, logits, "softmax_ce logits"));
     Ref oh = plain(b, arg(b, onehot, "softmax_ce targets"));
-    if (lgn->n != B * C || oh->n != B * C)
+    if (lg->n != B * C || oh->n != B * C)
       fail_shape("softmax_ce", std::to_string(B * C) + " elements",
-                 std::to_string(lgn->n) + " and " + std::to_string(oh->n) + " elements");
+                 std::to_string(lg->n) + " and " + std::to_string(oh->n) + " elements");
+    float* lp = dptr(b, lg.get());
+    float* op = dptr(b, oh.get());
     Ref l(value_node(b, 1, alloc_buf(b, 1)));
     Ref d;
     if (want_grad) d = Ref(value_node(b, B * C, alloc_buf(b, B * C)));
-    if (!head_forward_fold(b, lgn, oh.get(), B, C, l->buf->ptr, want_grad ? d->buf->ptr : nullptr)) {
-      Ref lg = plain(b, lgn);
-      float* lp = dptr(b, lg.get());
-      float* op = dptr(b, oh.get());
-      ck(orca_hip_softmax_ce(b->ctx, lp, B, C, op, nullptr, l->buf->ptr, want_grad ? d->buf->ptr : nullptr, nullptr,
-                             nullptr));
-    }
+    ck(orca_hip_softmax_ce(b->ctx, lp, B, C, op, nullptr, l->buf->ptr, want_grad ? d->buf->ptr : nullptr, nullptr,
+                           nullptr));
     l->quiet = true;
     // every element of the gradient is (0 + a) + (0 + b), plus (0 + c) at a row's maximum:
     // never -0, never a signaling NaN

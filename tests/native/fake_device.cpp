@@ -759,34 +759,6 @@ int orca_hip_softmax_ce(orca_hip_ctx* ctx, const float* logits, size_t B, size_t
   });
 }
 
-// The fused head forward: logits = H Wt + bias (the oracle's matmul, expand and add), then the
-// oracle's cross-entropy on them, so the same values as the product, bias add and softmax_ce.
-int orca_hip_head_forward_ce(orca_hip_ctx* ctx, const float* H, size_t B, size_t K, const float* Wt, const float* bias,
-                             size_t C, const float* onehot, const int32_t* labels, float* logits, float* loss,
-                             float* dlogits, int32_t* preds, int64_t* correct) {
-  return guard([&] {
-    if (!onehot || labels || preds || correct) fail(ORCA_HIP_ERR_INTERNAL, "the stand-in takes one-hot targets only");
-    launch(ctx, "head_forward_ce");
-    R(ctx, H, 4 * B * K);
-    R(ctx, Wt, 4 * K * C);
-    R(ctx, bias, 4 * C);
-    R(ctx, onehot, 4 * B * C);
-    W(ctx, logits, 4 * B * C);
-    W(ctx, loss, 4);
-    W(ctx, dlogits, 4 * B * C);
-    std::vector<float> p = product(H, false, K, Wt, false, C, B, C, K), row(B * C);
-    const size_t bd[2] = {1, C}, od[2] = {B, C};
-    check_oracle(orc_expand(bias, row.data(), bd, 2, od, 2), "head_forward_ce bias");
-    orc_add(p.data(), row.data(), logits, B * C);
-    std::vector<float> d(B * C);
-    float l = 0.0f;
-    if (orc_cross_entropy(logits, onehot, B, C, &l, d.data()) != 0) fail(ORCA_HIP_ERR_INTERNAL, "oracle CE failed");
-    if (loss) *loss = l;
-    if (dlogits) std::copy(d.begin(), d.end(), dlogits);
-    logf("head_forward_ce " + std::to_string(B) + "x" + std::to_string(K) + "x" + std::to_string(C));
-  });
-}
-
 static orc_opt make_opt(int kind, double lr, double b1, double b2, double eps, double wd) {
   orc_opt o{};
   o.kind = kind;

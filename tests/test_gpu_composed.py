@@ -198,44 +198,3 @@ def test_fused_update_on_second_stream_changes_no_bit(ctx, wl, bias):
             out[overlap] += [snap[k].numpy() for k in sorted(k for k in snap if k != "t")]
     for i, (a, b) in enumerate(zip(out[True], out[False])):
         np.testing.assert_array_equal(a, b, err_msg=f"array {i}")
-
-
-@pytest.mark.parametrize("B,K,C", [(1024, 4096, 10), (256, 1024, 10), (64, 128, 10), (37, 20, 3), (1000, 36, 16)])
-def test_fused_loss_over_a_pending_head_runs_the_head_forward(ctx, hb, B, K, C):
-    """CrossEntropyLoss(fused=True) on a classifier head's Linear still pending as its
-    product and bias add: the logits, the loss and its gradient come from one head-forward
-    launch (profiler record head_fwd_ce, no narrow product for the logits).  The logits are
-    within the f32 dot-product bound of the fp64 x @ W (+ b added in f32), the argmax is the
-    oracle's on them, and the loss and gradient are the oracle's cross-entropy of those very
-    logits within tolerance; the backward then runs on that gradient as usual."""
-    from tests.util import assert_close
-
-    rng = np.random.default_rng(B + K + C)
-    H = np.maximum(rng.standard_normal((B, K)), 0.0).astype(np.float32)
-    W = (rng.standard_normal((K, C)) * 0.05).astype(np.float32)
-    b = (rng.standard_normal(C) * 0.1).astype(np.float32)
-    onehot = synth.one_hot(rng.integers(0, C, B), C)
-    ad = A.Autodiff(hb)
-    head = A.build_mlp(ad, [W, b])
-    xt, tt = A.Tensor.from_numpy(ad, H), A.Tensor.from_numpy(ad, onehot)
-    ctx.prof_reset()
-    ctx.prof_enable(True)
-    try:
-        logits_t = head(xt)
-        loss = A.CrossEntropyLoss(fused=True)(logits_t, tt)
-        loss.backward()
-        lv = loss.to_list()[0]
-    finally:
-        ctx.prof_enable(False)
-    names = {k["name"] for k in ctx.prof_report()["kernels"]}
-    assert "head_fwd_ce" in names, names
-    assert not [n for n in names if n.startswith("gemm_nn")], names
-    logits = logits_t.numpy().reshape(B, C)
-    prod = H.astype(np.float64) @ W.astype(np.float64)
-    bound = K * 2.0 ** -24 * (np.abs(H).astype(np.float64) @ np.abs(W).astype(np.float64)) + 1e-30
-    z = (logits - b).astype(np.float64)  # the bias add is one f32 rounding on top of the sum
-    assert (np.abs(z - prod) <= bound + np.abs(logits).astype(np.float64) * 2.0 ** -23).all()
-    ref_loss, ref_dl = O.cross_entropy(logits, onehot)
-    assert_close(lv, ref_loss, what="loss")
-    gW = list(head.parameters())[0].tensor.grad().numpy().reshape(K, C)
-    assert_close(gW, O.matmul(O.transpose(H, 0, 1), ref_dl), what="dW")
