@@ -623,3 +623,31 @@ def test_multi_segment_optimizer_equals_one_tensor_kernels(ctx, kind):
         if not in_place[k]:
             written[o:o + n] = True
     assert not q[~written].any()
+
+
+@pytest.mark.parametrize("band_ctx", [1, 2], indirect=True, ids=["band8", "band112"])
+def test_gemm_band_padded_leading_dimensions(band_ctx):
+    """The banded kernels read A, B and write C through their leading dimensions: X stored
+    [K][lda] with lda = 800 > 784, dY [K][ldb] with ldb = 4100, C [784][ldc] with ldc = 4104;
+    exact on integers, the padding of C untouched, the column sum bit-identical."""
+    ctx = band_ctx
+    M, N, K, lda, ldb, ldc = 784, 4096, 96, 800, 4100, 4104
+    rng = np.random.default_rng(8)
+    X = int_matrix(rng, (K, lda))
+    dY = int_matrix(rng, (K, ldb))
+    dA, dB = ctx.upload(X), ctx.upload(dY)
+    C0 = np.full((M, ldc), 7.0, np.float32)
+    dC, dcs = ctx.upload(C0), ctx.alloc(4 * N)
+    e = _lib.Epilogue(_lib.EPI_NONE, None, None, 0, None)
+    e.colsum = dcs.ptr
+    ctx.prof_reset()
+    ctx.prof_enable(True)
+    _lib.call("orca_hip_gemm", ctx.handle, 1, 0, M, N, K, dA.ptr, lda, dB.ptr, ldb, dC.ptr, ldc, ctypes.byref(e))
+    ctx.prof_enable(False)
+    names = {k["name"] for k in ctx.prof_report()["kernels"]}
+    assert f"{'gemm_tn_band8' if ctx.band_mode == 1 else 'gemm_tn_band112'} {M}x{N}x{K}" in names, names
+    C = dC.download(count=M * ldc).reshape(M, ldc)
+    want = (X[:, :M].T.astype(np.int64) @ dY[:, :N].astype(np.int64)).astype(np.float32)
+    np.testing.assert_array_equal(C[:, :N], want)
+    np.testing.assert_array_equal(C[:, N:], C0[:, N:])
+    np.testing.assert_array_equal(dcs.download(count=N), O.sum_to_shape(np.ascontiguousarray(dY[:, :N]), (1, N)).reshape(N))
