@@ -150,11 +150,13 @@ def test_mlp784_1024_b256_free_running_within_natural_spread(ctx):
     assert gpu[-1] < 0.05 * gpu[0]  # the fixed batch is memorised
 
 
-@pytest.mark.parametrize("batch", [1024, 512])
+@pytest.mark.parametrize("batch", [1024, 512, 256, 128])
 def test_mlp784_4096_b1024_one_adamw_step(ctx, batch):
     """784-4096-4096-10, batch 1024, one AdamW step against the oracle, end to end
-    (and batch 512, where F1, F2 and dX2 each split K in two and sum the chunks
-    in their reduce pass, which also applies the epilogue):
+    (and the 512 / 256 / 128-row shares of 2-, 4- and 8-way data parallelism: F2 and dX2
+    split K in two, four and eight chunks and sum them in their reduce pass, which also
+    applies the epilogue; at 128 rows F1 runs whole on the skinny kernel; dW1 stays on the
+    banded kernel with K = 512, 256, 128):
     loss and logits to the path's tolerance (1e-5 abs + 1e-4 rel); gradients and
     updated parameters to that tolerance except for a reported fraction <= 1e-5
     of elements.  Those outliers come from ReLU masks that differ between the
