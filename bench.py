@@ -7,10 +7,14 @@ already resident in HBM.  Prints ONE JSON line (see the keys below).
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--no-secondary]
                   [--batch B] [--workload NAME] [--path trainer|composed|composed-fused]
-                  [--sustained-s S]
+                  [--sustained-s S] [--update-shards G]
 
 --batch measures one GPU's share of the 1024-row batch under data parallelism
-(512, 256, 128 rows); the default is the benchmark workload itself.  --workload
+(512, 256, 128 rows); the default is the benchmark workload itself.
+--update-shards G (with --batch 1024 / G) measures that share with the optimizer
+state sharded over the G ranks: the step's update passes cover one rank's 1/G
+slice of each (the gradients' reduce-scatter and the parameters' all-gather,
+which move the bytes of the all-reduce they replace, are not on one GPU).  --workload
 and --path step another configuration or the drop-in path instead (for
 profiling them); the defaults are the benchmark.
 
@@ -293,6 +297,9 @@ def main() -> int:
     ap.add_argument("--batch", type=int, default=None,
                     help="rows per step (default: the workload's; for the benchmark workload 512 / 256 / 128 are "
                          "one GPU's share of its 1024-row batch under 2 / 4 / 8-way data parallelism)")
+    ap.add_argument("--update-shards", type=int, default=1,
+                    help="trainer path: update one rank's 1/G slice of each update pass (the optimizer state "
+                         "sharded over G data-parallel ranks); 1, the default, updates every parameter")
     ap.add_argument("--sustained-s", type=float, default=3.0,
                     help="after the timed steps, keep stepping for about this many seconds and report that rate "
                          "too (a window long enough for an outside observer of the GPU); 0 skips it")
@@ -303,6 +310,9 @@ def main() -> int:
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); the library has no multi-GPU path",
               file=sys.stderr)
+        return 2
+    if args.update_shards < 1:
+        print(f"--update-shards must be at least 1 (got {args.update_shards})", file=sys.stderr)
         return 2
 
     from orcaml_amd.device import Context
@@ -328,8 +338,13 @@ def main() -> int:
                         betas=o.get("betas", (0.9, 0.999)), eps=o.get("eps", 1e-8))
         tr.set_params(params)
         tr.set_batch(x, onehot=onehot)
+        if args.update_shards > 1:
+            tr.set_update_shard(0, args.update_shards)
         step = tr.step
     else:
+        if args.update_shards != 1:
+            print("--update-shards applies to the trainer path only", file=sys.stderr)
+            return 2
         step = _composed_step(ctx, dims, batch, o, params, x, onehot, fused=args.path == "composed-fused")
     mallocs_before = None
 
@@ -420,7 +435,8 @@ def main() -> int:
         "dtype": "f32",
         "data": "synthetic",
         "config": {"workload": "mlp_train_step", "dims": list(dims), "batch": batch, "optimizer": o["kind"],
-                   "lr": o["lr"], "weight_decay": o.get("weight_decay", 0.0), "seed": seed, "path": args.path},
+                   "lr": o["lr"], "weight_decay": o.get("weight_decay", 0.0), "seed": seed, "path": args.path,
+                   "update_shard": f"1/{args.update_shards}" if args.update_shards > 1 else "all"},
         "samples_per_s": steps_per_s * batch,
         "step_tflops": flops * steps_per_s / 1e12,
         "step_frac_fp32_mfma_peak": flops * steps_per_s / 1e12 / PEAK_FP32_MFMA_TFLOPS,

@@ -721,6 +721,15 @@ int orca_hip_mlp_get_activation(orca_hip_mlp* mlp, size_t layer, float* host, si
 /* AdamW step counter t (python/orca/optim/adamw.py:33, 64); set restores it from a checkpoint. */
 int orca_hip_mlp_get_step_count(const orca_hip_mlp* mlp, int64_t* t);
 int orca_hip_mlp_set_step_count(orca_hip_mlp* mlp, int64_t t);
+/* One rank's share of a data-parallel step whose optimizer state is sharded over `count`
+ * ranks: each optimizer pass of orca_hip_mlp_step updates only slice `index` of `count` of
+ * its parameter range (cut at multiples of 64 floats; the slices of all indices cover every
+ * parameter once), with the whole update's bits there.  The other slices keep the values
+ * they hold when this is called (set_param writes them too); in a data-parallel run the
+ * ranks' all-gather would write them.  count = 1 restores the whole update.  No reference
+ * counterpart: the reference's optimizers update every parameter (python/orca/optim/
+ * adamw.py:66-99), as each rank of a replicated data-parallel step does. */
+int orca_hip_mlp_set_update_shard(orca_hip_mlp* mlp, size_t index, size_t count);
 
 /* ===================== kernel timing ===================== */
 /* When enabled, each GEMM / fused-kernel launch is bracketed by HIP events on

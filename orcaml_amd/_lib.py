@@ -266,6 +266,7 @@ SIGNATURES = {
     "orca_hip_mlp_get_activation": [_P, _SZ, _P, _SZ],
     "orca_hip_mlp_get_step_count": [_P, ctypes.POINTER(ctypes.c_int64)],
     "orca_hip_mlp_set_step_count": [_P, ctypes.c_int64],
+    "orca_hip_mlp_set_update_shard": [_P, _SZ, _SZ],
     "orca_hip_prof_enable": [_P, _I],
     "orca_hip_prof_reset": [_P],
     "orca_hip_prof_report": [_P, ctypes.c_char_p, _SZ],

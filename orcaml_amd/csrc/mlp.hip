@@ -91,6 +91,11 @@ struct orca_hip_mlp {
   // after it is updated on the context stream after that product, with layer 0.
   size_t side_b = 0;
   int side_bpc2 = 0;
+  // One rank's share of a data-parallel step whose optimizer state is sharded over
+  // shard_count ranks: every update pass covers slice shard_index of its range (cuts at
+  // multiples of 64 floats), so each rank's passes keep the whole schedule's placement at
+  // 1/shard_count of its bytes.  The other slices keep their values in both arenas.
+  size_t shard_index = 0, shard_count = 1;
   // Persistent workspaces: a step makes no allocator call, so it can be
   // captured once into a HIP graph and replayed.
   orca_hip::AdamWScalars* kdev = nullptr;  // this step's AdamW scalars (device)
@@ -179,6 +184,12 @@ void step_body(orca_hip_mlp* m, const AdamWScalars* kdev) {
   // With a second arena the update writes P_next and reads P.
   float* P_out = m->P_next ? m->P_next : m->P;
   auto update = [&](size_t begin, size_t end, hipStream_t stream, int bpc = 0) {
+    if (m->shard_count > 1 && end > begin) {  // this rank's slice of the pass
+      const size_t len = end - begin, s = m->shard_index, c = m->shard_count;
+      auto cut = [&](size_t i) { return i == c ? len : len * i / c / 64 * 64; };
+      end = begin + cut(s + 1);
+      begin += cut(s);
+    }
     if (end <= begin) return;
     if (m->opt.kind == 1)
       adamw(ctx, P_out + begin, m->G + begin, m->Mo + begin, m->Vo + begin, end - begin, m->opt.lr, m->opt.beta1,
@@ -451,6 +462,25 @@ int orca_hip_mlp_set_param(orca_hip_mlp* mlp, size_t index, const float* host, s
     checked(mlp);
     check_index(mlp, index, n);
     upload_async(mlp->ctx, mlp->P + mlp->off[index], host, n * sizeof(float));
+    // a sharded update writes only its slices of the second arena: the rest comes from here
+    if (mlp->shard_count > 1 && mlp->P_next)
+      upload_async(mlp->ctx, mlp->P_next + mlp->off[index], host, n * sizeof(float));
+  });
+}
+
+int orca_hip_mlp_set_update_shard(orca_hip_mlp* mlp, size_t index, size_t count) {
+  return guard([&] {
+    checked(mlp);
+    if (count == 0 || index >= count)
+      fail(ORCA_HIP_ERR_INTERNAL, "update shard " + std::to_string(index) + " of " + std::to_string(count) +
+                                      " out of range");
+    // Both arenas hold the current values of the slices this share leaves alone.
+    if (count > 1 && mlp->P_next)
+      ORCA_HIP_CHECK(hipMemcpyAsync(mlp->P_next, mlp->P, mlp->arena * sizeof(float), hipMemcpyDeviceToDevice,
+                                    mlp->ctx->stream));
+    mlp->shard_index = index;
+    mlp->shard_count = count;
+    invalidate_graph(mlp);  // a captured step holds the passes' ranges
   });
 }
 

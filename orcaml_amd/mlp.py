@@ -123,6 +123,12 @@ class MLPTrainer:
     def set_step_count(self, t: int) -> None:
         _lib.call("orca_hip_mlp_set_step_count", self.handle, int(t))
 
+    def set_update_shard(self, index: int, count: int) -> None:
+        """One rank's share of a data-parallel step with the optimizer state sharded over
+        `count` ranks: each step's update passes cover slice `index` of their ranges only
+        (the other slices keep their current values); count = 1 restores the whole update."""
+        _lib.call("orca_hip_mlp_set_update_shard", self.handle, int(index), int(count))
+
     def save(self, path: str) -> None:
         """Parameters (named as the equivalent nn.Sequential's) and AdamW state, as safetensors."""
         from .serialize import save_trainer

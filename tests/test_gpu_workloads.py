@@ -179,6 +179,45 @@ def test_mlp784_4096_b1024_one_adamw_step(ctx, batch):
                          what=f"784-4096-4096-10 b{batch} end-to-end")
 
 
+@pytest.mark.parametrize("batch,count", [(128, 8), (512, 3)])
+def test_update_shards_partition_the_whole_update(ctx, batch, count):
+    """784-4096-4096-10 at a data-parallel share, one AdamW step with the optimizer state
+    sharded over `count` ranks (set_update_shard), each rank's share run in turn from the
+    same state.  Every parameter, m and v element either takes the whole step's bits or keeps
+    its value (the parameters read back come from the second arena, which the update wrote);
+    each element the whole step changes is taken by exactly one share; the shares are
+    balanced (every update pass is cut at multiples of 64 floats); loss and logits are the
+    whole step's."""
+    w = dict(synth.WORKLOADS[synth.MLP_LARGE], batch=batch)
+    params, x, labels, onehot = synth.mlp_problem(w["seed"], w["dims"], batch)
+    full = make_trainer(ctx, w, params)
+    full.set_batch(x, onehot=onehot)
+    full.step()
+    loss_full, logits_full = full.metrics()[0], full.logits()
+    want = [np.concatenate([a.ravel() for a in arrs]) for arrs in (full.params(), full.moments(0), full.moments(1))]
+    full.close()
+    p0 = np.concatenate([p.ravel() for p in params])
+    changed = (want[0] != p0) | (want[1] != 0) | (want[2] != 0)
+    takers = np.zeros(p0.size, np.int32)
+    for s in range(count):
+        tr = make_trainer(ctx, w, params)
+        tr.set_update_shard(s, count)
+        tr.set_batch(x, onehot=onehot)
+        tr.step()
+        assert tr.metrics()[0] == loss_full
+        np.testing.assert_array_equal(tr.logits(), logits_full)
+        got = [np.concatenate([a.ravel() for a in arrs]) for arrs in (tr.params(), tr.moments(0), tr.moments(1))]
+        tr.close()
+        took = (got[0] == want[0]) & (got[1] == want[1]) & (got[2] == want[2])
+        kept = (got[0] == p0) & (got[1] == 0) & (got[2] == 0)
+        assert np.all(took | kept), f"share {s}: {np.count_nonzero(~(took | kept))} elements neither updated nor kept"
+        mine = took & ~kept
+        takers += mine
+        share = np.count_nonzero(mine) / np.count_nonzero(changed)
+        assert abs(share - 1.0 / count) < 0.01, (s, share)
+    assert np.all(takers[changed] == 1), np.bincount(takers[changed])
+
+
 @pytest.mark.parametrize("switch", ["ORCA_HIP_DOUBLE_ARENA", "ORCA_HIP_BIND_EVENTS"])
 def test_mlp784_4096_b1024_schedule_changes_no_bit(ctx, monkeypatch, switch):
     """784-4096-4096-10, batch 1024, three AdamW steps, each schedule switch on and off: every
