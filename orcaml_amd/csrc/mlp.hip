@@ -93,8 +93,9 @@ struct orca_hip_mlp {
   int side_bpc2 = 0;
   // One rank's share of a data-parallel step whose optimizer state is sharded over
   // shard_count ranks: every update pass covers slice shard_index of its range (cuts at
-  // multiples of 64 floats), so each rank's passes keep the whole schedule's placement at
-  // 1/shard_count of its bytes.  The other slices keep their values in both arenas.
+  // multiples of 64 floats), so every rank does the same work; a slice of layers >= 1 too small
+  // for the second stream (kMinShardOverlapParams) updates with layer 0's after the backward.
+  // The other slices keep their values in both arenas.
   size_t shard_index = 0, shard_count = 1;
   // Persistent workspaces: a step makes no allocator call, so it can be
   // captured once into a HIP graph and replayed.
@@ -129,6 +130,11 @@ constexpr unsigned kStreamEventFlags = hipEventDisableTiming | hipEventDisableSy
 
 // Smallest update (parameters of layers >= 1) worth a second stream.
 constexpr size_t kMinOverlapParams = size_t(1) << 22;
+// The same for one rank's slice of a sharded update: on 784-4096-4096-10 the second stream paid
+// at 8.4 M parameters per rank (512 rows, 2 ranks: 0.518 against 0.520 ms per step) and not at
+// 4.2 M (256 rows, 4 ranks: 0.306 against 0.302) or 2.1 M (128 rows, 8 ranks: 0.204 against
+// 0.194), where the whole slice runs after the backward on the context stream instead.
+constexpr size_t kMinShardOverlapParams = size_t(6) << 20;
 
 // Everything a step enqueues.  With kdev set, AdamW reads its scalars from
 // that device buffer, so the enqueued work is identical from step to step and
@@ -180,6 +186,9 @@ void step_body(orca_hip_mlp* m, const AdamWScalars* kdev) {
   // weight-gradient GEMM (memory-bound beside compute-bound); the step ends
   // when both streams have finished.
   const size_t split = L > 1 ? m->off[2] : 0;  // arena offset of W_1
+  // whether this step's update of layers >= 1 runs on the second stream
+  const bool overlap = m->side && split > 0 &&
+                       (m->shard_count == 1 || (m->arena - split) / m->shard_count >= kMinShardOverlapParams);
   bool forked = false;
   // With a second arena the update writes P_next and reads P.
   float* P_out = m->P_next ? m->P_next : m->P;
@@ -207,7 +216,7 @@ void step_body(orca_hip_mlp* m, const AdamWScalars* kdev) {
   for (size_t l = n_gemm; l-- > 0;) {
     const size_t K = m->dims[l], N = m->dims[l + 1];
     const float* a = l == 0 ? m->x : m->H[l - 1];
-    if (l == 0 && m->side && split > 0 && !forked) fork_update();
+    if (l == 0 && overlap && !forked) fork_update();
     GemmEpi ew;
     ew.ws = m->gemm_ws;
     ew.ws_floats = m->gemm_ws_floats;
@@ -215,9 +224,11 @@ void step_body(orca_hip_mlp* m, const AdamWScalars* kdev) {
     ew.colsum = m->head_db && l + 2 == L ? nullptr : m->G + m->off[2 * l + 1];
     // Layers >= 1 have all their gradients after dW of layer 1; with a second
     // arena nothing of this step writes the P that layer 1's dZ reads.
-    const bool early = l == 1 && m->P_next && m->side && split > 0;
+    const bool early = l == 1 && m->P_next && overlap;
     // Layer 0's weight gradient has the update of the layers above beside it when there
     // is a side stream: its banded grid then leaves CUs free for that update.
+    // The form follows the model (a second stream or not), not the step's schedule, so that a
+    // sharded step runs the whole step's dW bits (the two forms round differently).
     if (l == 0) ew.band = m->side ? 2 : 1;
     // The fork and mid events complete with the product's kernel rather than
     // as markers of their own between two launches.
@@ -252,7 +263,7 @@ void step_body(orca_hip_mlp* m, const AdamWScalars* kdev) {
   // ---- update (parameter order W_0, b_0, W_1, ...; flat passes over the arena) ----
   if (forked) {
     update(0, split, ctx->stream, m->u0_bpc);
-    if (m->P_next && m->side) update(split + m->side_a + m->side_b, m->arena, ctx->stream, m->u0_bpc);
+    if (m->P_next) update(split + m->side_a + m->side_b, m->arena, ctx->stream, m->u0_bpc);
     ORCA_HIP_CHECK(hipStreamWaitEvent(ctx->stream, m->join, 0));
   } else {
     update(0, m->arena, ctx->stream);

@@ -179,11 +179,12 @@ def test_mlp784_4096_b1024_one_adamw_step(ctx, batch):
                          what=f"784-4096-4096-10 b{batch} end-to-end")
 
 
-@pytest.mark.parametrize("batch,count", [(128, 8), (512, 3)])
+@pytest.mark.parametrize("batch,count", [(128, 8), (512, 2), (256, 3)])
 def test_update_shards_partition_the_whole_update(ctx, batch, count):
     """784-4096-4096-10 at a data-parallel share, one AdamW step with the optimizer state
     sharded over `count` ranks (set_update_shard), each rank's share run in turn from the
-    same state.  Every parameter, m and v element either takes the whole step's bits or keeps
+    same state: at 2 ranks the slices of layers 1-2 update on the second stream beside dX2 and
+    dW1; at 3 and 8 ranks every slice updates after the backward on the context stream.  Every parameter, m and v element either takes the whole step's bits or keeps
     its value (the parameters read back come from the second arena, which the update wrote);
     each element the whole step changes is taken by exactly one share; the shares are
     balanced (every update pass is cut at multiples of 64 floats); loss and logits are the
