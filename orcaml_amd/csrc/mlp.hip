@@ -92,11 +92,16 @@ struct orca_hip_mlp {
   size_t side_b = 0;
   int side_bpc2 = 0;
   // One rank's share of a data-parallel step whose optimizer state is sharded over
-  // shard_count ranks: every update pass covers slice shard_index of its range (cuts at
-  // multiples of 64 floats), so every rank does the same work; a slice of layers >= 1 too small
-  // for the second stream (kMinShardOverlapParams) updates with layer 0's after the backward.
-  // The other slices keep their values in both arenas.
+  // shard_count ranks.  The rank owns slice shard_index (cuts at multiples of 64 floats) of
+  // each range between consecutive shard_cuts: layer 0, then the parts of layers >= 1 that
+  // the double-arena schedule updates beside layer 1's dZ product, beside layer 0's dW and
+  // after it.  That map is fixed for the model, whatever schedule a step takes (captured or
+  // not, second stream or not), and every rank does the same work.  Each update pass covers
+  // its range's intersection with the owned slices; a slice of layers >= 1 too small for the
+  // second stream (kMinShardOverlapParams) updates with layer 0's after the backward.  The
+  // other slices keep their values in both arenas.
   size_t shard_index = 0, shard_count = 1;
+  std::vector<size_t> shard_cuts;
   // Persistent workspaces: a step makes no allocator call, so it can be
   // captured once into a HIP graph and replayed.
   orca_hip::AdamWScalars* kdev = nullptr;  // this step's AdamW scalars (device)
@@ -192,19 +197,27 @@ void step_body(orca_hip_mlp* m, const AdamWScalars* kdev) {
   bool forked = false;
   // With a second arena the update writes P_next and reads P.
   float* P_out = m->P_next ? m->P_next : m->P;
-  auto update = [&](size_t begin, size_t end, hipStream_t stream, int bpc = 0) {
-    if (m->shard_count > 1 && end > begin) {  // this rank's slice of the pass
-      const size_t len = end - begin, s = m->shard_index, c = m->shard_count;
-      auto cut = [&](size_t i) { return i == c ? len : len * i / c / 64 * 64; };
-      end = begin + cut(s + 1);
-      begin += cut(s);
-    }
-    if (end <= begin) return;
+  auto update_range = [&](size_t begin, size_t end, hipStream_t stream, int bpc) {
     if (m->opt.kind == 1)
       adamw(ctx, P_out + begin, m->G + begin, m->Mo + begin, m->Vo + begin, end - begin, m->opt.lr, m->opt.beta1,
             m->opt.beta2, m->opt.eps, m->opt.weight_decay, m->t, stream, kdev, m->P + begin, bpc);
     else
       sgd(ctx, m->P + begin, m->G + begin, end - begin, m->opt.lr, stream);
+  };
+  auto update = [&](size_t begin, size_t end, hipStream_t stream, int bpc = 0) {
+    if (end <= begin) return;
+    if (m->shard_count > 1) {  // the pass's intersection with this rank's slices
+      const std::vector<size_t>& cu = m->shard_cuts;
+      const size_t s = m->shard_index, c = m->shard_count;
+      for (size_t r = 0; r + 1 < cu.size(); ++r) {
+        const size_t len = cu[r + 1] - cu[r];
+        auto cut = [&](size_t i) { return i == c ? len : len * i / c / 64 * 64; };
+        const size_t lo = std::max(begin, cu[r] + cut(s)), hi = std::min(end, cu[r] + cut(s + 1));
+        if (lo < hi) update_range(lo, hi, stream, bpc);
+      }
+      return;
+    }
+    update_range(begin, end, stream, bpc);
   };
   auto fork_update = [&]() {
     ORCA_HIP_CHECK(hipEventRecord(m->fork, ctx->stream));
@@ -426,6 +439,16 @@ int orca_hip_mlp_create(orca_hip_ctx* ctx, const size_t* dims, size_t n_layers, 
     // A captured step holds fixed arena pointers, so the second arena is for
     // eager steps with AdamW and a side stream only.
     const char* da = std::getenv("ORCA_HIP_DOUBLE_ARENA");
+    // The side-stream parts of the update of layers >= 1 ([span] floats): a beside layer 1's
+    // dZ product, b beside layer 0's dW.
+    auto side_split = [](size_t span, size_t& a, size_t& b) {
+      const char* sf = std::getenv("ORCA_HIP_SIDE_FRAC");
+      const double frac = sf ? std::atof(sf) / 100.0 : 0.7;
+      a = std::min(span, (size_t)(frac * (double)span) / 64 * 64);
+      b = span - a;
+      if (const char* sf2 = std::getenv("ORCA_HIP_SIDE_FRAC2"))
+        b = std::min(b, (size_t)(std::atof(sf2) / 100.0 * (double)span) / 64 * 64);
+    };
     const char* sb = std::getenv("ORCA_HIP_SIDE_BPC");
     if (sb) m->side_bpc = std::atoi(sb);
     if (const char* u0 = std::getenv("ORCA_HIP_U0_BPC")) m->u0_bpc = std::atoi(u0);
@@ -434,15 +457,21 @@ int orca_hip_mlp_create(orca_hip_ctx* ctx, const size_t* dims, size_t n_layers, 
       m->P_next = m->dev(o);
       launch_fill(ctx, m->P_next, 0.0f, o);
       ORCA_HIP_CHECK(hipEventCreateWithFlags(&m->mid, kStreamEventFlags));
-      const char* sf = std::getenv("ORCA_HIP_SIDE_FRAC");
-      const double frac = sf ? std::atof(sf) / 100.0 : 0.7;
-      const size_t span = o - m->off[2];
-      m->side_a = std::min(span, (size_t)(frac * (double)span) / 64 * 64);
-      const char* sf2 = std::getenv("ORCA_HIP_SIDE_FRAC2");
-      m->side_b = span - m->side_a;
-      if (sf2) m->side_b = std::min(m->side_b, (size_t)(std::atof(sf2) / 100.0 * (double)span) / 64 * 64);
+      side_split(o - m->off[2], m->side_a, m->side_b);
       if (const char* b2 = std::getenv("ORCA_HIP_SIDE_BPC2")) m->side_bpc2 = std::atoi(b2);
     }
+    // The ranges a sharded update's slices are cut from: the double-arena schedule's update
+    // passes, whichever schedule this trainer runs, so that a rank's slices depend on the
+    // model (and the split's settings) only.
+    m->shard_cuts = {0};
+    if (n_layers > 1) {
+      const size_t split = m->off[2];
+      size_t a = m->side_a, b = m->side_b;
+      if (!m->P_next) side_split(o - split, a, b);
+      for (size_t cut : {split, split + a, split + a + b})
+        if (cut > m->shard_cuts.back() && cut < o) m->shard_cuts.push_back(cut);
+    }
+    m->shard_cuts.push_back(o);
     host_sync(ctx);
     *out = m.release();
   });

@@ -72,3 +72,30 @@ def test_graph_replays_back_to_back_sgd(ctx, monkeypatch):
     assert_same(state(trs[0]), state(trs[1]), "after 10 steps")
     for tr in trs:
         tr.close()
+
+
+@pytest.mark.parametrize("batch,count", [(512, 2), (128, 8)])
+def test_graph_replays_with_an_update_shard(ctx, monkeypatch, batch, count):
+    """784-4096-4096-10 at a data-parallel share: after one step, the optimizer update is
+    sharded (rank count - 1 of count), which must rebuild the captured step; every later
+    replay matches the eager trainer with the same shard bit for bit (the eager one keeps two
+    parameter arenas, the captured one updates in place)."""
+    w = dict(synth.WORKLOADS[synth.MLP_LARGE], batch=batch)
+    params, x, labels, onehot = synth.mlp_problem(w["seed"], w["dims"], batch)
+    trs = [make(ctx, monkeypatch, w, graph) for graph in (True, False)]
+    for tr in trs:
+        tr.set_params(params)
+        tr.set_batch(x, onehot=onehot)
+    for step in range(3):
+        if step == 1:
+            for tr in trs:
+                tr.set_update_shard(count - 1, count)
+        results = []
+        for tr in trs:
+            tr.step()
+            results.append((tr.metrics(), state(tr)))
+        (m_g, s_g), (m_e, s_e) = results
+        assert m_g == m_e, f"step {step}: loss / correct differ between replay and eager"
+        assert_same(s_g, s_e, f"step {step}")
+    for tr in trs:
+        tr.close()
